@@ -1,0 +1,208 @@
+"""Benchmark of the tile-binned splat renderer on one MI355X.
+
+Workload (BASELINE.json configs[1]/[2]): one 768x768 RGB fp32 frame from 92,160 seeded synthetic splats
+(10 per 8x8 cell of a 96x96 grid), upstream gradient ~ N(0, 1). A step is one forward + backward render
+through render_alpha_full_triton(cull=True): softplus, binning (decode, count, scan, pair scatter, radix
+sort, tile starts), per-tile compositing, and the backward to every splat parameter. Inputs are resident
+in HBM before the timed region. `value` is frames/s x 0.589824 Mpix of the fwd+bwd step.
+
+Also reported: forward-only and the render_alpha_octave entry point, per-stage event times,
+the roofline of the dominant kernel from HIP events around its launches (on the stream it runs on), and
+the reference's CPU renderer (render.py math) on a bounded band of the same frame, on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gaussian-2d-splat-encoder_amd"))
+
+import torch  # noqa: E402
+
+from gaussian_splat_encoder import render_hip as RH  # noqa: E402
+from gaussian_splat_encoder import synth  # noqa: E402
+
+# AMD's published MI355X peaks: fp32 vector 157.3 TFLOP/s, HBM3E 8.0 TB/s.
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+# Algorithmic flops per pixel-pair evaluation, counting each operation of the reference's expressions once
+# (render_triton.py:476-499 forward, :668-710 backward incl. the 9 pixel-reduction adds), per-splat terms
+# hoisted.
+FLOPS_FWD = {False: 27, True: 28}
+FLOPS_BWD = {False: 71, True: 74}
+
+
+def algorithmic_bytes_fwd(N, tot, P):
+    """Composite forward: splat params 36 B/splat, pair list 8 B/pair (id + gathered record index), out+T+
+    asum+fg 32 B/pixel."""
+    return 36 * N + 8 * tot + 32 * P
+
+
+def algorithmic_bytes_bwd(N, tot, P):
+    """Backward: params in + grads out 72 B/splat, pair ids 4 B/pair, T+asum+fg+gout 32 B/pixel."""
+    return 72 * N + 4 * tot + 32 * P
+
+
+def ppe_of(bins, H, W, TILE=8):
+    """Pixel-pair evaluations: sum over tiles of pairs x in-canvas pixels of the tile."""
+    st = bins.starts_b[0].long()
+    cnt = (st[1:] - st[:-1]).double()
+    ntx = bins.ntx
+    t = torch.arange(cnt.numel(), device=cnt.device)
+    ty, tx = t // ntx, t % ntx
+    ph = torch.clamp(H - ty * TILE, max=TILE).double()
+    pw = torch.clamp(W - tx * TILE, max=TILE).double()
+    return float((cnt * ph * pw).sum().item())
+
+
+def time_loop(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(end) / steps, wall
+
+
+def cpu_baseline(s, rows=(368, 376), threads=None):
+    """The reference's CPU renderer (render.py:90-110 math, fp32 torch, materialised falloff), restated in
+    oracle/render_ref.py, over a band of rows of the same frame; scaled to a full frame."""
+    sys.path.insert(0, ROOT)
+    from oracle import render_ref
+    n = threads or min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(n)
+    args = (s.mu, s.log_scale, s.color, s.opacity, s.bg, s.H, s.W)
+    render_ref.render_alpha_full_f32(*args, theta=s.theta, chunk_pixels=256, rows=(rows[0], rows[0] + 1))  # warm
+    t0 = time.perf_counter()
+    render_ref.render_alpha_full_f32(*args, theta=s.theta, chunk_pixels=256, rows=rows)
+    dt = time.perf_counter() - t0
+    frame_s = dt * s.H / (rows[1] - rows[0])
+    return {"value": round(s.H * s.W / 1e6 / frame_s, 6), "unit": "Mpix/s", "cores": n, "kind": "port",
+            "ms_per_frame": round(frame_s * 1e3, 1),
+            "sample": f"render.py exact fp32 forward (oracle/render_ref.render_alpha_full_f32, torch CPU, "
+                      f"{n} threads) over rows {rows[0]}-{rows[1] - 1} of the 768x768 / 92,160-splat frame "
+                      f"({(rows[1] - rows[0]) * s.W * s.n / 1e9:.2f} G pixel-pairs, {dt:.1f} s), "
+                      f"scaled to a full frame; forward only"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--odds", action="store_true", help="odds compositing instead of alpha")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              f"multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    s_cpu = synth.config("c2")
+    s = s_cpu.to(dev)
+    H, W, N = s.H, s.W, s.n
+    P = H * W
+    odds = args.odds
+    # dL/dimage stored in the image's own memory layout ([B,H,W,C] behind the [B,C,H,W] view)
+    gout = s.grad_out.permute(0, 2, 3, 1).contiguous().permute(0, 3, 1, 2)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (s.mu, s.log_scale, s.color, s.opacity, s.bg,
+                                                                  s.theta)]
+
+    def fwd():
+        with torch.no_grad():
+            return RH.render_alpha_full_triton(*leaves[:5], H, W, theta=leaves[5], cull=True, odds=odds)
+
+    def fwd_bwd():
+        for t in leaves:
+            t.grad = None
+        out = RH.render_alpha_full_triton(*leaves[:5], H, W, theta=leaves[5], cull=True, odds=odds)
+        out.backward(gout)
+
+    def oct_fwd():
+        with torch.no_grad():
+            return RH.render_alpha_octave(*leaves[:5], H, W, theta=leaves[5], odds=odds)
+
+    def oct_fwd_bwd():
+        for t in leaves:
+            t.grad = None
+        RH.render_alpha_octave(*leaves[:5], H, W, theta=leaves[5], odds=odds).backward(gout)
+
+    # the headline: fwd + bwd, then the other measurements
+    ms, wall_ms = time_loop(fwd_bwd, args.steps, args.warmup)
+    ms_fwd, _ = time_loop(fwd, args.steps, args.warmup)
+    ms_oct_fwd, _ = time_loop(oct_fwd, args.steps, args.warmup)
+    ms_oct, _ = time_loop(oct_fwd_bwd, args.steps, args.warmup)
+
+    # live kernel timing: HIP events bracketing the per-tile forward / backward launches over K steps
+    RH.kernel_timer.enable(True)
+    for _ in range(args.steps):
+        fwd_bwd()
+    ev = RH.kernel_timer.elapsed_ms()
+    RH.kernel_timer.enable(False)
+    avg = {k: sum(v) / len(v) for k, v in ev.items()}
+    _, _, bins = RH._forward_cull(leaves[0].detach(), torch.nn.functional.softplus(leaves[1].detach()) + 1e-4,
+                                  leaves[2].detach(), leaves[3].detach(), leaves[4].detach(), leaves[5].detach(),
+                                  H, W, 8, 3.0, odds=odds)
+    tot = bins.tot_b[0]
+    ppe = ppe_of(bins, H, W)
+    fl_f, fl_b = FLOPS_FWD[odds] * ppe, FLOPS_BWD[odds] * ppe
+    kern = {
+        "fwd": {"ms": avg["fwd"], "tflops": fl_f / (avg["fwd"] * 1e-3) / 1e12,
+                "gbs": algorithmic_bytes_fwd(N, tot, P) / (avg["fwd"] * 1e-3) / 1e9},
+        "bwd": {"ms": avg["bwd"], "tflops": fl_b / (avg["bwd"] * 1e-3) / 1e12,
+                "gbs": algorithmic_bytes_bwd(N, tot, P) / (avg["bwd"] * 1e-3) / 1e9},
+    }
+    dom = "bwd" if avg["bwd"] >= avg["fwd"] else "fwd"
+    dk = kern[dom]
+    mpix = P / 1e6
+    line = {
+        "metric": "render ms/frame + Mpix/s at 768x768, 92,160 splats (fwd, fwd+bwd); % roofline",
+        "value": round(mpix / (ms * 1e-3), 2),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splat set of BASELINE configs[2]; CPU torch.Generator, seed 0)",
+        "config": {"workload": "768x768 RGB, 92,160 splats, fwd+bwd, render_alpha_full_triton(cull=True, TILE=8, "
+                               f"cutoff=3, odds={odds}); configs[2]",
+                   "H": H, "W": W, "splats": N, "pairs": tot, "pixel_pairs": int(ppe)},
+        "roofline": {"bound": "valu", "kernel": f"k_{dom}_cull" + (" (+acc fill, finalize)" if dom == "bwd" else ""),
+                     "achieved": round(dk["tflops"], 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dk["tflops"] / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": fl_b if dom == "bwd" else fl_f, "avg_launch_ms": round(dk["ms"], 4),
+                     "hbm_achieved_gbs": round(dk["gbs"], 1),
+                     "hbm_frac": round(dk["gbs"] / PEAK_HBM_GBS, 4)},
+        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kern.items()},
+        "stages_ms": {k: round(v, 4) for k, v in avg.items()},
+        "fwd_ms": round(ms_fwd, 4),
+        "fwd_mpix_s": round(mpix / (ms_fwd * 1e-3), 2),
+        "octave_fwd_ms": round(ms_oct_fwd, 4),
+        "octave_fwd_bwd_ms": round(ms_oct, 4),
+        "wall_ms_per_step": round(wall_ms, 4),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(s_cpu)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,488 @@
+// Splat -> tile binning on gfx950, bit-exact with render_triton.py:351-409 (`_build_tiles`):
+//   k_decode_count   one coalesced pass over the splat parameters: the decoded render record, the tile
+//                    rect and the pair count of every splat, and per-block count sums
+//   k_scan_sums /    exclusive scan of the counts into per-splat pair offsets (offsets[N] = tot)
+//   k_offsets
+//   k_scatter_pairs  load-balanced expansion of every splat's rect into (tile, splat) pairs, splat-major
+//                    as the reference generates them (:396-404), fused with the first radix histogram
+//   k_radix_*        stable LSD radix sort on the tile id, splat id as the value: within a tile the
+//                    splats keep ascending order, the order of the reference's stable argsort (:405-407)
+//   k_tile_starts    CSR starts: starts[t] = number of pairs with tile < t (:408)
+//
+// This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
+// operation separately (a fused mu*W - r*W changes floor() near tile edges).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "splat_common.h"
+
+namespace splat {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+constexpr int kItems = 16;                      // keys per thread in the pair/sort kernels
+constexpr int kSortKeys = kBlock * kItems;      // 4096 keys per block
+constexpr int kWaveKeys = kSortKeys / kWaves;   // 1024 consecutive keys per wave
+constexpr long long kBadBit = 1LL << 62;        // marks a block holding an empty or inverted rect
+
+// ----------------------------------------------------------------------------------------------------
+// decode + rect + count
+template <int C>
+__global__ __launch_bounds__(kBlock) void k_decode_count(
+    const float* __restrict__ mu, const float* __restrict__ scale, const float* __restrict__ theta,
+    const float* __restrict__ opacity, const float* __restrict__ color, int N, float fH, float fW, float fT,
+    float cutoff, float xmax, float ymax, int do_bin, float4* __restrict__ rec, int4* __restrict__ rect,
+    int* __restrict__ counts, long long* __restrict__ block_sums) {
+  __shared__ long long s_part[kWaves];
+  const int g = blockIdx.x * kBlock + threadIdx.x;
+  int cnt = 0;
+  bool bad = false;
+  if (g < N) {
+    const float2 m = reinterpret_cast<const float2*>(mu)[g];      // (y, x)
+    const float2 s = reinterpret_cast<const float2*>(scale)[g];   // (sy, sx)
+    float sn = 0.f, cs = 1.f;
+    if (theta) sincosf(theta[g], &sn, &cs);
+    const float ky = kWhiten / s.x, kx = kWhiten / s.y;
+    float4 col = make_float4(0.f, 0.f, 0.f, 0.f);
+    col.x = color[(size_t)g * C];
+    if (C > 1) col.y = color[(size_t)g * C + 1];
+    if (C > 2) col.z = color[(size_t)g * C + 2];
+    if (C > 3) col.w = color[(size_t)g * C + 3];
+    float4* r = rec + (size_t)g * 4;
+    r[0] = make_float4(m.x, m.y, cs * ky, sn * ky);
+    const float op = opacity[g];
+    r[1] = make_float4(-sn * kx, cs * kx, op, 1.f - op);
+    r[2] = col;
+    r[3] = make_float4(s.x, s.y, cs, sn);
+    if (do_bin) {
+      // render_triton.py:367-377, one rounding per operation.
+      const float cx = m.y * fW;
+      const float cy = m.x * fH;
+      const float rr = cutoff * fmaxf(s.x, s.y);
+      const float rx = rr * fW;
+      const float ry = rr * fH;
+      const int tx0 = (int)fminf(fmaxf(floorf((cx - rx) / fT), 0.f), xmax);
+      const int tx1 = (int)fminf(fmaxf(floorf((cx + rx) / fT), 0.f), xmax);
+      const int ty0 = (int)fminf(fmaxf(floorf((cy - ry) / fT), 0.f), ymax);
+      const int ty1 = (int)fminf(fmaxf(floorf((cy + ry) / fT), 0.f), ymax);
+      const int w = tx1 - tx0 + 1, h = ty1 - ty0 + 1;
+      bad = (w < 1) || (h < 1);
+      cnt = bad ? 0 : w * h;
+      rect[g] = make_int4(tx0, ty0, w, h);
+      counts[g] = cnt;
+    }
+  }
+  if (!do_bin) return;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  long long v = cnt;
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) v += __shfl_xor(v, msk, 64);
+  const bool any_bad = __any(bad);
+  if (lane == 0) s_part[wv] = v | (any_bad ? kBadBit : 0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long t = 0, b = 0;
+    for (int i = 0; i < kWaves; ++i) { t += s_part[i] & ~kBadBit; b |= s_part[i] & kBadBit; }
+    block_sums[blockIdx.x] = t | b;
+  }
+}
+
+// Exclusive scan of the per-block count sums in one workgroup; info[0] = total pairs, info[1] = error
+// bits (1: empty/inverted rect, 2: total exceeds int32).
+__global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums, int n, long long* __restrict__ info) {
+  __shared__ long long s_w[16];
+  __shared__ long long s_carry;
+  __shared__ long long s_bad;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (threadIdx.x == 0) { s_carry = 0; s_bad = 0; }
+  __syncthreads();
+  for (int base = 0; base < n; base += 1024) {
+    const int i = base + threadIdx.x;
+    long long v = i < n ? sums[i] : 0;
+    if (v & kBadBit) atomicOr((unsigned long long*)&s_bad, 1ull);
+    v &= ~kBadBit;
+    long long inc = wave_incl_scan(v, lane);
+    if (lane == 63) s_w[wv] = inc;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      long long x = s_w[threadIdx.x];
+      for (int d = 1; d < 16; d <<= 1) {
+        long long o = __shfl_up(x, d, 64);
+        if ((int)threadIdx.x >= d) x += o;
+      }
+      s_w[threadIdx.x] = x;
+    }
+    __syncthreads();
+    const long long carry = s_carry;
+    const long long excl = carry + (wv ? s_w[wv - 1] : 0) + inc - v;
+    if (i < n) sums[i] = excl;
+    __syncthreads();
+    if (threadIdx.x == 0) s_carry = carry + s_w[15];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const long long tot = s_carry;
+    info[0] = tot;
+    info[1] = (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0);
+  }
+}
+
+// counts -> exclusive offsets in place; offsets[N] = total.
+__global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, const long long* __restrict__ block_pre,
+                                                    int N, const long long* __restrict__ info) {
+  __shared__ int s_w[kWaves];
+  const int g = blockIdx.x * kBlock + threadIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = g < N ? offsets[g] : 0;
+  const int inc = wave_incl_scan(c, lane);
+  if (lane == 63) s_w[wv] = inc;
+  __syncthreads();
+  int pre = 0;
+  for (int i = 0; i < wv; ++i) pre += s_w[i];
+  if (info[1] & 2) return;   // total overflows int32: the host raises, offsets are not used
+  if (g < N) offsets[g] = (int)block_pre[blockIdx.x] + pre + inc - c;
+  if (g == N - 1) offsets[N] = (int)info[0];
+}
+
+// ----------------------------------------------------------------------------------------------------
+// pair expansion: pair p belongs to the last splat g with offsets[g] <= p; its k = p - offsets[g] walks
+// the splat's rect row-major (render_triton.py:400-404).
+__device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi, int p) {
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a[mid] <= p) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
+                                                          int N, int ntx, int tot, int dmask, int* __restrict__ keys,
+                                                          int* __restrict__ vals, int* __restrict__ hist, int nblocks) {
+  __shared__ int s_off[kSortKeys + 1];
+  __shared__ int s_hist[256];
+  __shared__ int s_rng[2];
+  const int p_base = blockIdx.x * kSortKeys;
+  const int p_last = min(p_base + kSortKeys, tot) - 1;
+  for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
+  if (threadIdx.x == 0) {
+    s_rng[0] = last_le(offsets, 0, N - 1, p_base);
+    s_rng[1] = last_le(offsets, 0, N - 1, p_last);
+  }
+  __syncthreads();
+  const int glo = s_rng[0], ghi = s_rng[1];
+  const int nwin = ghi - glo + 1;
+  const bool in_lds = nwin <= kSortKeys;
+  if (in_lds)
+    for (int i = threadIdx.x; i <= nwin; i += kBlock) s_off[i] = offsets[glo + i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll 4
+  for (int j = 0; j < kItems; ++j) {
+    const int p = p_base + wv * kWaveKeys + j * 64 + lane;
+    if (p > p_last) continue;
+    int w0, o;
+    if (in_lds) { w0 = last_le(s_off, 0, nwin - 1, p); o = s_off[w0]; }
+    else { w0 = last_le(offsets + glo, 0, nwin - 1, p); o = offsets[glo + w0]; }
+    const int g = glo + w0;
+    const int k = p - o;
+    const int4 rc = rect[g];
+    const int ky = k / rc.z;
+    const int kx = k - ky * rc.z;
+    const int tile = (rc.y + ky) * ntx + rc.x + kx;
+    keys[p] = tile;
+    vals[p] = g;
+    if (hist) atomicAdd(&s_hist[tile & dmask], 1);
+  }
+  if (!hist) return;
+  __syncthreads();
+  for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
+}
+
+__global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ keys, int tot, int shift, int dmask,
+                                                       int* __restrict__ hist, int nblocks) {
+  __shared__ int s_hist[256];
+  for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
+  __syncthreads();
+  const int p_base = blockIdx.x * kSortKeys;
+  for (int j = 0; j < kItems; ++j) {
+    const int p = p_base + j * kBlock + threadIdx.x;
+    if (p < tot) atomicAdd(&s_hist[(keys[p] >> shift) & dmask], 1);
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
+}
+
+// Stable scatter of one radix pass. Wave w of the block owns keys [base + w*1024, base + (w+1)*1024) and
+// walks them 64 at a time in index order; lanes holding the same digit are ranked among themselves with
+// ballots (lane order = index order), on top of the wave's running count for that digit. Wave counts are
+// then prefixed across the waves, and the block's base for each digit comes from the scanned histogram.
+__global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
+                                                          int tot, int shift, int dbits, const int* __restrict__ hist_scan,
+                                                          int nblocks, int* __restrict__ keys_out,
+                                                          int* __restrict__ vals_out) {
+  __shared__ int s_cnt[kWaves][256];
+  __shared__ int s_base[256];
+  const int dmask = (1 << dbits) - 1;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < kWaves * 256; i += kBlock) (&s_cnt[0][0])[i] = 0;
+  for (int d = threadIdx.x; d <= dmask; d += kBlock) s_base[d] = hist_scan[d * nblocks + blockIdx.x];
+  __syncthreads();
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int p0 = blockIdx.x * kSortKeys + wv * kWaveKeys + lane;
+  int key[kItems], val[kItems], rank[kItems];
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const int p = p0 + j * 64;
+    const bool act = p < tot;
+    key[j] = act ? keys_in[p] : 0;
+    val[j] = act ? vals_in[p] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const bool act = p0 + j * 64 < tot;
+    const int d = (key[j] >> shift) & dmask;
+    unsigned long long peers = __ballot(act);
+    for (int b = 0; b < dbits; ++b) {
+      const bool bit = (d >> b) & 1;
+      const unsigned long long m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int below = __popcll(peers & lt);
+    const int before = s_cnt[wv][d];
+    if (act && below == 0) s_cnt[wv][d] = before + __popcll(peers);
+    rank[j] = before + below;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d <= dmask; d += kBlock) {
+    int run = s_base[d];
+    for (int w = 0; w < kWaves; ++w) { const int c = s_cnt[w][d]; s_cnt[w][d] = run; run += c; }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    if (p0 + j * 64 >= tot) continue;
+    const int d = (key[j] >> shift) & dmask;
+    const int pos = s_cnt[wv][d] + rank[j];
+    keys_out[pos] = key[j];
+    vals_out[pos] = val[j];
+  }
+}
+
+// ----------------------------------------------------------------------------------------------------
+// Exclusive scan of int32, used for the radix histograms (digit-major, so the scan yields each
+// (digit, block) its global base).
+constexpr int kScanItems = 4;
+constexpr int kScanBlock = 1024;
+constexpr int kScanChunk = kScanBlock * kScanItems;
+
+__device__ __forceinline__ int block_excl_scan_1024(int v, int* s_w, int& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int inc = wave_incl_scan(v, lane);
+  if (lane == 63) s_w[wv] = inc;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    int x = s_w[threadIdx.x];
+    for (int d = 1; d < 16; d <<= 1) {
+      int o = __shfl_up(x, d, 64);
+      if ((int)threadIdx.x >= d) x += o;
+    }
+    s_w[threadIdx.x] = x;
+  }
+  __syncthreads();
+  const int excl = (wv ? s_w[wv - 1] : 0) + inc - v;
+  total = s_w[15];
+  __syncthreads();
+  return excl;
+}
+
+// One workgroup scans a whole array (chunks of 4096 with a running carry), or with `partial` set, each
+// workgroup scans its 4096-chunk and adds partial[blockIdx].
+__global__ __launch_bounds__(kScanBlock) void k_scan_chunks(int* __restrict__ a, int n, const int* __restrict__ partial,
+                                                            int whole) {
+  __shared__ int s_w[16];
+  int carry = partial ? partial[blockIdx.x] : 0;
+  const int first = whole ? 0 : blockIdx.x * kScanChunk;
+  const int last = whole ? n : min(n, first + kScanChunk);
+  for (int base = first; base < last; base += kScanChunk) {
+    const int i0 = base + threadIdx.x * kScanItems;
+    int v[kScanItems], s = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) { v[k] = (i0 + k < last) ? a[i0 + k] : 0; s += v[k]; }
+    int total;
+    int run = carry + block_excl_scan_1024(s, s_w, total);
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+      if (i0 + k < last) a[i0 + k] = run;
+      run += v[k];
+    }
+    carry += total;
+  }
+}
+
+__global__ __launch_bounds__(kScanBlock) void k_scan_reduce(const int* __restrict__ a, int n, int* __restrict__ partial) {
+  __shared__ int s_w[16];
+  const int i0 = blockIdx.x * kScanChunk + threadIdx.x * kScanItems;
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) s += (i0 + k < n) ? a[i0 + k] : 0;
+  int total;
+  block_excl_scan_1024(s, s_w, total);
+  if (threadIdx.x == 0) partial[blockIdx.x] = total;
+}
+
+static int scan_exclusive(int* a, int n, int* partial, hipStream_t st) {
+  if (n <= 16 * kScanChunk) {
+    k_scan_chunks<<<1, kScanBlock, 0, st>>>(a, n, nullptr, 1);
+    return check_launch("k_scan_chunks");
+  }
+  const int nb = div_up(n, kScanChunk);
+  k_scan_reduce<<<nb, kScanBlock, 0, st>>>(a, n, partial);
+  k_scan_chunks<<<1, kScanBlock, 0, st>>>(partial, nb, nullptr, 1);
+  k_scan_chunks<<<nb, kScanBlock, 0, st>>>(a, n, partial, 0);
+  return check_launch("scan_exclusive");
+}
+
+// starts[t] = number of pairs with tile < t, from the sorted tile ids.
+__global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ keys, int tot, int nt, int* __restrict__ starts) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i >= tot) return;
+  const int k = keys[i];
+  const int prev = i ? keys[i - 1] : -1;
+  for (int t = prev + 1; t <= k; ++t) starts[t] = i;
+  if (i == tot - 1)
+    for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
+}
+
+__global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
+// ----------------------------------------------------------------------------------------------------
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct PairsPlan {
+  int nblk, passes, dbits, radix, nscan_part;
+  size_t off_keys_a, off_keys_b, off_vals_b, off_hist, off_part, total;
+};
+
+static PairsPlan plan_pairs(int nt, long long tot) {
+  PairsPlan p{};
+  p.nblk = tot > 0 ? div_up(tot, kSortKeys) : 0;
+  int nbits = 0;
+  while (nt > 1 && (1LL << nbits) < nt) ++nbits;   // bits of the largest tile id nt - 1
+  p.passes = (nbits + 7) / 8;
+  p.dbits = p.passes ? (nbits + p.passes - 1) / p.passes : 0;
+  p.radix = 1 << p.dbits;
+  const long long nh = (long long)p.radix * p.nblk;
+  p.nscan_part = div_up(nh > 0 ? nh : 1, kScanChunk);
+  size_t o = 0;
+  p.off_keys_a = o; o += align256(sizeof(int) * (size_t)tot);
+  p.off_keys_b = o; o += align256(sizeof(int) * (size_t)tot);
+  p.off_vals_b = o; o += align256(sizeof(int) * (size_t)tot);
+  p.off_hist = o;   o += align256(sizeof(int) * (size_t)(nh > 0 ? nh : 1));
+  p.off_part = o;   o += align256(sizeof(int) * (size_t)p.nscan_part);
+  p.total = o;
+  return p;
+}
+
+}  // namespace splat
+
+using namespace splat;
+
+extern "C" {
+
+size_t splat_bin_count_workspace_bytes(int N) { return align256(sizeof(long long) * (size_t)(N > 0 ? div_up(N, kBlock) : 1)); }
+
+int splat_decode(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
+                 int C, int N, float* rec, void* stream) {
+  if (N < 0 || C < 1 || C > kMaxC) return set_error(kInvalid, "splat_decode: N=%d C=%d (C must be 1..%d)", N, C, kMaxC);
+  if (N == 0) return kOk;
+  if (!mu || !scale || !opacity || !color || !rec) return set_error(kInvalid, "splat_decode: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int nb = div_up(N, kBlock);
+#define SPLAT_DECODE(CC)                                                                                          \
+  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, 1.f, 1.f, 1.f, 0.f, 0.f, 0.f, 0, \
+                                            reinterpret_cast<float4*>(rec), nullptr, nullptr, nullptr)
+  switch (C) { case 1: SPLAT_DECODE(1); break; case 2: SPLAT_DECODE(2); break;
+               case 3: SPLAT_DECODE(3); break; default: SPLAT_DECODE(4); break; }
+#undef SPLAT_DECODE
+  return check_launch("k_decode_count(decode)");
+}
+
+int splat_bin_count(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
+                    int C, int N, int H, int W, int TILE, float cutoff, float* rec, int* rect, int* offsets,
+                    long long* info, void* ws, size_t ws_bytes, void* stream) {
+  if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
+    return set_error(kInvalid, "splat_bin_count: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
+  if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
+    return set_error(kInvalid, "splat_bin_count: null pointer");
+  if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int ntx = (W + TILE - 1) / TILE, nty = (H + TILE - 1) / TILE;
+  const int nb = div_up(N, kBlock);
+  long long* sums = (long long*)ws;
+#define SPLAT_DC(CC)                                                                                         \
+  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, (float)H, (float)W,       \
+                                            (float)TILE, cutoff, (float)(ntx - 1), (float)(nty - 1), 1,   \
+                                            reinterpret_cast<float4*>(rec), reinterpret_cast<int4*>(rect), \
+                                            offsets, sums)
+  switch (C) { case 1: SPLAT_DC(1); break; case 2: SPLAT_DC(2); break;
+               case 3: SPLAT_DC(3); break; default: SPLAT_DC(4); break; }
+#undef SPLAT_DC
+  k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, info);
+  k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
+  return check_launch("splat_bin_count");
+}
+
+size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
+  (void)N;
+  return plan_pairs(nt, tot).total;
+}
+
+int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, long long tot, int* gid_sorted,
+                    int* tile_starts, void* ws, size_t ws_bytes, void* stream) {
+  if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
+    return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
+  if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
+  const int ntx = (W + TILE - 1) / TILE, nt = ntx * ((H + TILE - 1) / TILE);
+  const PairsPlan pl = plan_pairs(nt, tot);
+  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
+  hipStream_t st = (hipStream_t)stream;
+  if (tot == 0) {
+    k_fill_i32<<<div_up(nt + 1, 256), 256, 0, st>>>(tile_starts, nt + 1, 0);
+    k_fill_i32<<<1, 64, 0, st>>>(gid_sorted, 1, 0);
+    return check_launch("splat_bin_pairs(empty)");
+  }
+  char* base = (char*)ws;
+  int* keys_a = (int*)(base + pl.off_keys_a);
+  int* keys_b = (int*)(base + pl.off_keys_b);
+  int* vals_b = (int*)(base + pl.off_vals_b);
+  int* hist = (int*)(base + pl.off_hist);
+  int* part = (int*)(base + pl.off_part);
+  const int fin = pl.passes & 1;
+  int* K[2];
+  int* V[2];
+  K[fin] = keys_a; V[fin] = gid_sorted;
+  K[1 - fin] = keys_b; V[1 - fin] = vals_b;
+  const int t = (int)tot;
+  const int dmask = pl.radix - 1;
+  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, ntx, t, dmask, K[0], V[0],
+                                              pl.passes ? hist : nullptr, pl.nblk);
+  int rc = check_launch("k_scatter_pairs");
+  if (rc) return rc;
+  for (int pass = 0; pass < pl.passes; ++pass) {
+    const int shift = pass * pl.dbits;
+    const int src = pass & 1, dst = 1 - src;
+    if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], t, shift, dmask, hist, pl.nblk);
+    rc = scan_exclusive(hist, pl.radix * pl.nblk, part, st);
+    if (rc) return rc;
+    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, pl.nblk, K[dst], V[dst]);
+    rc = check_launch("k_radix_scatter");
+    if (rc) return rc;
+  }
+  k_tile_starts<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], t, nt, tile_starts);
+  return check_launch("k_tile_starts");
+}
+
+}  // extern "C"

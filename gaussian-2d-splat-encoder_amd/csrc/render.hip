@@ -1,0 +1,530 @@
+// Per-tile compositing on gfx950: forward and backward of the order-independent alpha composite of
+// render_triton.py:423-517 (forward) and 602-720 (backward), plus the exact (unculled) path of :58-266.
+//
+// Forward: one wave64 per TILE x TILE tile (8 x 8 = one pixel per lane). The tile's pair list is walked in
+// pair order; the pair's splat id and its decoded record are wave-uniform, so they are read with scalar
+// loads into SGPRs and every lane evaluates its own pixel. Per pixel-pair: whitened offsets u, v; falloff
+// exp2(-(u^2 + v^2)); a = min(op * falloff, 1 - 1e-4); S_log += log2(1 - a) (scaled by ln 2 once);
+// S_a += w; S_ac += w * colour, with w = a or the odds a / (1 - a).
+//
+// Backward: one wave per tile, lane = pair. The tile's per-pixel upstream terms (dS_log, dS_a, dS_ac)
+// are derived once (lane = pixel) into LDS; each lane then walks the tile's pixels for its own pair and
+// accumulates ten per-pair sums in registers (the per-tile reduction), which go to per-splat accumulators
+// with one fp32 atomic each. A finalize pass turns the sums into parameter gradients:
+//   q    = da * falloff where op * falloff < 1 - 1e-4 (0 on the clamp)      da: render_triton.py:688-697
+//   g_op = sum q,   Qu = sum q u,  Qv = sum q v,  Quu = sum q u^2,  Qvv = sum q v^2,  Quv = sum q u v
+//   g_sy = 2 ln2 op Quu / sy,  g_sx = 2 ln2 op Qvv / sx
+//   gry  = -op Qu / (k sy),    grx  = -op Qv / (k sx)     (k = kWhiten)
+//   g_muy = -(cos gry - sin grx),  g_mux = -(sin gry + cos grx)
+//   g_theta = -2 ln2 op Quv (sx^2 - sy^2) / (sx sy)
+// which is the reference's per-pixel chain rule (:697-710) with the per-splat factors taken out of the sums.
+#include <type_traits>
+
+#include "splat_common.h"
+
+namespace splat {
+
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+constexpr int kAcc = 16;   // per-splat accumulator stride (floats): Q, Qu, Qv, Quu, Qvv, Quv, colour[4]
+
+__host__ __device__ constexpr int tile_threads(int tile) { return tile * tile > 64 ? tile * tile : 64; }
+
+// One pixel-pair of the forward sums.
+template <int C, bool ODDS>
+__device__ __forceinline__ void fwd_accumulate(const float* __restrict__ r, float py, float px, float& sl, float& s_a,
+                                               float* sc) {
+  const float dy = py - r[R_GY], dx = px - r[R_GX];
+  const float u = fmaf(r[R_A], dy, r[R_B] * dx);
+  const float v = fmaf(r[R_CC], dy, r[R_D] * dx);
+  const float m = fmaf(u, u, v * v);
+  const float fo = r[R_OP] * hw_exp2(-m);
+  const float a = fminf(fo, kClamp);
+  float oma = 1.f - a;
+  if (ODDS) oma = one_minus_alpha(oma, fo, m, r[R_OP], r[R_1MOP]);
+  sl += hw_log2(oma);
+  const float w = ODDS ? a * hw_rcp(oma) : a;
+  s_a += w;
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = fmaf(w, r[R_COL + c], sc[c]);
+}
+
+template <int C>
+__device__ __forceinline__ void store_composite(int p, float sl2, float s_a, const float* sc, const float* __restrict__ bg,
+                                                float* __restrict__ out, float* __restrict__ Tout,
+                                                float* __restrict__ asum_out, float* __restrict__ fg_out) {
+  const float T = hw_exp2(sl2);                 // exp(S_log), S_log = sl2 * ln 2
+  const float as = fmaxf(s_a, kAsumMin);
+  Tout[p] = T;
+  asum_out[p] = as;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float f = sc[c] / as;
+    fg_out[(size_t)p * C + c] = f;
+    out[(size_t)p * C + c] = (1.f - T) * f + T * bg[c];
+  }
+}
+
+template <int C, bool FIELDS, bool ODDS, int TILE>
+__global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_cull(
+    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
+    int nt, const float* __restrict__ bg, float* __restrict__ out, float* __restrict__ Tout,
+    float* __restrict__ asum_out, float* __restrict__ fg_out, float* __restrict__ slog, float* __restrict__ sa,
+    float* __restrict__ sac) {
+  const int t = xcd_swizzle(blockIdx.x, nt);
+  const int tx = t % ntx, ty = t / ntx;
+  const int l = threadIdx.x;
+  const int yp = ty * TILE + l / TILE, xp = tx * TILE + l % TILE;
+  const bool valid = l < TILE * TILE && yp < H && xp < W;
+  const float py = ((float)yp + 0.5f) / (float)H;   // render_triton.py:455-456
+  const float px = ((float)xp + 0.5f) / (float)W;
+  const int g0 = starts[t], g1 = starts[t + 1];
+  float sl = 0.f, s_a = 0.f, sc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = 0.f;
+  for (int i = g0; i < g1; ++i) {
+    const float* r = rec + (size_t)gid[i] * kRec;
+    fwd_accumulate<C, ODDS>(r, py, px, sl, s_a, sc);
+  }
+  if (!valid) return;
+  const int p = yp * W + xp;
+  if (FIELDS) {
+    slog[p] = sl * kLn2;
+    sa[p] = s_a;
+#pragma unroll
+    for (int c = 0; c < C; ++c) sac[(size_t)p * C + c] = sc[c];
+  } else {
+    store_composite<C>(p, sl, s_a, sc, bg, out, Tout, asum_out, fg_out);
+  }
+}
+
+// Exact path forward (render_triton.py:58-125): 64 pixels per workgroup in flat pixel order, pixel centres
+// supplied by the caller (render.py:61-65 linspace), every splat in splat order.
+template <int C>
+__global__ __launch_bounds__(64) void k_fwd_exact(const float* __restrict__ rec, int N, const float* __restrict__ pyv,
+                                                  const float* __restrict__ pxv, int P, const float* __restrict__ bg,
+                                                  float* __restrict__ out, float* __restrict__ Tout,
+                                                  float* __restrict__ asum_out, float* __restrict__ fg_out) {
+  const int p = blockIdx.x * 64 + threadIdx.x;
+  const bool valid = p < P;
+  const float py = valid ? pyv[p] : 0.f, px = valid ? pxv[p] : 0.f;
+  float sl = 0.f, s_a = 0.f, sc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = 0.f;
+  for (int g = 0; g < N; ++g) fwd_accumulate<C, false>(rec + (size_t)g * kRec, py, px, sl, s_a, sc);
+  if (valid) store_composite<C>(p, sl, s_a, sc, bg, out, Tout, asum_out, fg_out);
+}
+
+// Per-pixel upstream terms of the backward (render_triton.py:640-654). Masked pixels give zeros.
+template <int C, bool FIELDS>
+__device__ __forceinline__ void pixel_upstream(int p, const float* __restrict__ bg, const float* __restrict__ Tin,
+                                               const float* __restrict__ asum_in, const float* __restrict__ fg_in,
+                                               const float* __restrict__ gout, const float* __restrict__ dslog,
+                                               const float* __restrict__ dsa, const float* __restrict__ dsac,
+                                               float4& pa, float4& pb, float* bgp) {
+  float dl, da, dc[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+  if (FIELDS) {
+    dl = dslog[p];
+    da = dsa[p];
+#pragma unroll
+    for (int c = 0; c < C; ++c) dc[c] = dsac[(size_t)p * C + c];
+  } else {
+    const float T = Tin[p], as = asum_in[p];
+    float dTp = 0.f, sfg = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float go = gout[(size_t)p * C + c], f = fg_in[(size_t)p * C + c];
+      const float dfg = go * (1.f - T);
+      dTp += go * (bg[c] - f);
+      sfg += dfg * f;
+      dc[c] = dfg / as;
+      bgp[c] += go * T;
+    }
+    dl = dTp * T;
+    da = -sfg / as;
+  }
+  pa = make_float4(dl, da, dc[0], dc[1]);
+  pb = make_float4(dc[2], dc[3], 0.f, 0.f);
+}
+
+// Per-pair sums over pixels, in registers.
+template <int C>
+struct PairSums {
+  float q = 0.f, qu = 0.f, qv = 0.f, quu = 0.f, qvv = 0.f, quv = 0.f, gc[C];
+  __device__ PairSums() {
+#pragma unroll
+    for (int c = 0; c < C; ++c) gc[c] = 0.f;
+  }
+};
+
+// One pixel-pair of the backward, given whitened offsets u, v.
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float one_m_op, const float4& col,
+                                               const float4& pa, const float4& pb, PairSums<C>& s) {
+  const float m = fmaf(u, u, v * v);
+  const float f = hw_exp2(-m);
+  const float fo = op * f;
+  const float a = fminf(fo, kClamp);
+  const float rr = hw_rcp(one_minus_alpha(1.f - a, fo, m, op, one_m_op));
+  float ct = pa.z * col.x;
+  if (C > 1) ct = fmaf(pa.w, col.y, ct);
+  if (C > 2) ct = fmaf(pb.x, col.z, ct);
+  if (C > 3) ct = fmaf(pb.y, col.w, ct);
+  float da, cw;
+  if (ODDS) {
+    da = fmaf(-pa.x, rr, (pa.y + ct) * (rr * rr));
+    cw = a * rr;
+  } else {
+    da = fmaf(-pa.x, rr, pa.y + ct);
+    cw = a;
+  }
+  s.gc[0] = fmaf(cw, pa.z, s.gc[0]);
+  if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
+  if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
+  if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
+  const float q = fo < kClamp ? da * f : 0.f;   // no gradient through the alpha clamp (:686, :697)
+  const float qu = q * u, qv = q * v;
+  s.q += q;
+  s.qu += qu;
+  s.qv += qv;
+  s.quu = fmaf(qu, u, s.quu);
+  s.qvv = fmaf(qv, v, s.qvv);
+  s.quv = fmaf(qu, v, s.quv);
+}
+
+template <int C>
+__device__ __forceinline__ void add_sums(float* __restrict__ dst, const PairSums<C>& s) {
+  atomicAdd(dst + 0, s.q);
+  atomicAdd(dst + 1, s.qu);
+  atomicAdd(dst + 2, s.qv);
+  atomicAdd(dst + 3, s.quu);
+  atomicAdd(dst + 4, s.qvv);
+  atomicAdd(dst + 5, s.quv);
+#pragma unroll
+  for (int c = 0; c < C; ++c) atomicAdd(dst + 6 + c, s.gc[c]);
+}
+
+template <int C, bool FIELDS, bool ODDS, int TILE>
+__global__ __launch_bounds__(64) void k_bwd_cull(
+    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
+    int nt, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
+    const float* __restrict__ fg_in, const float* __restrict__ gout, const float* __restrict__ dslog,
+    const float* __restrict__ dsa, const float* __restrict__ dsac, float* __restrict__ acc,
+    float* __restrict__ bg_part) {
+  constexpr int NP = TILE * TILE;
+  __shared__ float4 s_pa[NP];
+  __shared__ float4 s_pb[NP];
+  __shared__ float s_py[TILE], s_px[TILE];
+  const int t = xcd_swizzle(blockIdx.x, nt);
+  const int tx = t % ntx, ty = t / ntx;
+  const int lane = threadIdx.x;
+  float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+  for (int l = lane; l < NP; l += 64) {
+    const int yp = ty * TILE + l / TILE, xp = tx * TILE + l % TILE;
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
+    if (yp < H && xp < W)
+      pixel_upstream<C, FIELDS>(yp * W + xp, bg, Tin, asum_in, fg_in, gout, dslog, dsa, dsac, pa, pb, bgp);
+    s_pa[l] = pa;
+    s_pb[l] = pb;
+  }
+  if (lane < TILE) {
+    s_py[lane] = ((float)(ty * TILE + lane) + 0.5f) / (float)H;
+    s_px[lane] = ((float)(tx * TILE + lane) + 0.5f) / (float)W;
+  }
+  if (!FIELDS && bg_part) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float v = wave_sum(bgp[c]);
+      if (lane == 0) bg_part[(size_t)t * C + c] = v;
+    }
+  }
+  __syncthreads();
+  const int g0 = starts[t], g1 = starts[t + 1];
+  for (int i0 = g0; i0 < g1; i0 += 64) {
+    const int i = i0 + lane;
+    const bool act = i < g1;
+    const int g = act ? gid[i] : 0;
+    const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+    const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
+    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z, omo = r1.w;
+    float bdx[TILE], ddx[TILE];
+#pragma unroll
+    for (int xx = 0; xx < TILE; ++xx) {
+      const float dx = s_px[xx] - gx;
+      bdx[xx] = B * dx;
+      ddx[xx] = D * dx;
+    }
+    PairSums<C> s;
+    for (int yy = 0; yy < TILE; ++yy) {
+      const float dy = s_py[yy] - gy;
+      const float uy = A * dy, vy = Cc * dy;
+#pragma unroll
+      for (int xx = 0; xx < TILE; ++xx) {
+        const int l = yy * TILE + xx;
+        const float4 pa = s_pa[l];
+        const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
+        bwd_accumulate<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, omo, col, pa, pb, s);
+      }
+    }
+    if (act) add_sums<C>(acc + (size_t)g * kAcc, s);
+  }
+}
+
+// Exact path backward (render_triton.py:161-266): lane = splat over every pixel; the per-pixel upstream
+// terms of each 64-pixel chunk are staged in LDS. Each splat is owned by one lane: plain stores.
+template <int C>
+__global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec, int N, const float* __restrict__ pyv,
+                                                  const float* __restrict__ pxv, int P, const float* __restrict__ bg,
+                                                  const float* __restrict__ Tin, const float* __restrict__ asum_in,
+                                                  const float* __restrict__ fg_in, const float* __restrict__ gout,
+                                                  float* __restrict__ acc) {
+  __shared__ float4 s_pa[64], s_pb[64];
+  __shared__ float2 s_pyx[64];
+  const int lane = threadIdx.x;
+  const int g = blockIdx.x * 64 + lane;
+  const int gs = g < N ? g : N - 1;
+  const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)gs * 4;
+  const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
+  const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z, omo = r1.w;
+  PairSums<C> s;
+  float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 0; p0 < P; p0 += 64) {
+    const int p = p0 + lane;
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
+    float2 pyx = make_float2(0.f, 0.f);
+    if (p < P) {
+      pixel_upstream<C, false>(p, bg, Tin, asum_in, fg_in, gout, nullptr, nullptr, nullptr, pa, pb, bgp);
+      pyx = make_float2(pyv[p], pxv[p]);
+    }
+    __syncthreads();
+    s_pa[lane] = pa;
+    s_pb[lane] = pb;
+    s_pyx[lane] = pyx;
+    __syncthreads();
+    const int np = P - p0 < 64 ? P - p0 : 64;
+    for (int j = 0; j < np; ++j) {
+      const float2 q = s_pyx[j];
+      const float dy = q.x - gy, dx = q.y - gx;
+      bwd_accumulate<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, omo, col, s_pa[j],
+                               C > 2 ? s_pb[j] : make_float4(0.f, 0.f, 0.f, 0.f), s);
+    }
+  }
+  if (g >= N) return;
+  float* dst = acc + (size_t)g * kAcc;
+  dst[0] = s.q; dst[1] = s.qu; dst[2] = s.qv; dst[3] = s.quu; dst[4] = s.qvv; dst[5] = s.quv;
+#pragma unroll
+  for (int c = 0; c < C; ++c) dst[6 + c] = s.gc[c];
+}
+
+// sum_p gout[p, c] * T[p] partials over 256-pixel chunks (the exact path's g_bg, render_triton.py:301).
+template <int C>
+__global__ __launch_bounds__(256) void k_bg_partial(const float* __restrict__ gout, const float* __restrict__ Tin, int P,
+                                                    float* __restrict__ part) {
+  __shared__ float s_w[4][kMaxC];
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    float v = p < P ? gout[(size_t)p * C + c] * Tin[p] : 0.f;
+    v = wave_sum(v);
+    if (lane == 0) s_w[wv][c] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < C) part[(size_t)blockIdx.x * C + threadIdx.x] = s_w[0][threadIdx.x] + s_w[1][threadIdx.x] +
+                                                                     s_w[2][threadIdx.x] + s_w[3][threadIdx.x];
+}
+
+// Per-splat sums -> parameter gradients. With g_bg set, the last workgroup also reduces the nparts
+// per-tile (or per-chunk) partials of sum_p gout * T.
+template <int C>
+__global__ __launch_bounds__(256) void k_bwd_finalize(const float* __restrict__ rec, const float* __restrict__ acc, int N,
+                                                      float* __restrict__ g_mu, float* __restrict__ g_scale,
+                                                      float* __restrict__ g_theta, float* __restrict__ g_op,
+                                                      float* __restrict__ g_col, const float* __restrict__ bg_part,
+                                                      int nparts, float* __restrict__ g_bg) {
+  const int nb_splat = (N + 255) / 256;
+  if ((int)blockIdx.x >= nb_splat) {
+    __shared__ float s_w[4][kMaxC];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      float v = 0.f;
+      for (int i = threadIdx.x; i < nparts; i += 256) v += bg_part[(size_t)i * C + c];
+      v = wave_sum(v);
+      if (lane == 0) s_w[wv][c] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < C)
+      g_bg[threadIdx.x] = (s_w[0][threadIdx.x] + s_w[1][threadIdx.x]) + (s_w[2][threadIdx.x] + s_w[3][threadIdx.x]);
+    return;
+  }
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= N) return;
+  const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+  const float op = r4[1].z;
+  const float4 r3 = r4[3];
+  const float sy = r3.x, sx = r3.y, cs = r3.z, sn = r3.w;
+  const float* a = acc + (size_t)g * kAcc;
+  const float q = a[0], qu = a[1], qv = a[2], quu = a[3], qvv = a[4], quv = a[5];
+  const float gry = -op * qu / (kWhiten * sy);
+  const float grx = -op * qv / (kWhiten * sx);
+  g_mu[2 * g + 0] = -(cs * gry - sn * grx);
+  g_mu[2 * g + 1] = -(sn * gry + cs * grx);
+  g_scale[2 * g + 0] = 2.f * kLn2 * op * quu / sy;
+  g_scale[2 * g + 1] = 2.f * kLn2 * op * qvv / sx;
+  if (g_theta) g_theta[g] = -2.f * kLn2 * op * quv * ((sx - sy) * (sx + sy) / (sx * sy));
+  g_op[g] = q;
+#pragma unroll
+  for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = a[6 + c];
+}
+
+__global__ void k_fill_f32(float* __restrict__ a, size_t n, float v) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
+// ---------------------------------------------------------------------------------------------------- dispatch
+template <typename F>
+int with_c(int C, F&& f) {
+  switch (C) {
+    case 1: return f(IC<1>{});
+    case 2: return f(IC<2>{});
+    case 3: return f(IC<3>{});
+    case 4: return f(IC<4>{});
+  }
+  return set_error(kUnsupported, "colour channels C=%d not supported (1..%d)", C, kMaxC);
+}
+
+template <typename F>
+int with_tile(int TILE, F&& f) {
+  switch (TILE) {
+    case 4: return f(IC<4>{});
+    case 8: return f(IC<8>{});
+    case 16: return f(IC<16>{});
+  }
+  return set_error(kUnsupported, "TILE=%d not supported (4, 8 or 16)", TILE);
+}
+
+template <typename F>
+int with_flags(int flags, F&& f) {
+  switch (flags & 3) {
+    case 0: return f(IC<0>{}, IC<0>{});
+    case 1: return f(IC<1>{}, IC<0>{});
+    case 2: return f(IC<0>{}, IC<1>{});
+    default: return f(IC<1>{}, IC<1>{});
+  }
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace splat
+
+using namespace splat;
+
+extern "C" {
+
+int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_starts, int C, int H, int W, int TILE,
+                     int flags, const float* bg, float* out, float* T, float* asum, float* fg, float* slog, float* sa,
+                     float* sac, void* stream) {
+  if (H < 1 || W < 1) return set_error(kInvalid, "splat_render_fwd: H=%d W=%d", H, W);
+  if (!rec || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_render_fwd: null pair list");
+  const bool fields = flags & kFlagFields;
+  if (fields ? (!slog || !sa || !sac) : (!bg || !out || !T || !asum || !fg))
+    return set_error(kInvalid, "splat_render_fwd: null output for flags=%d", flags);
+  hipStream_t st = (hipStream_t)stream;
+  return with_c(C, [&](auto cc) {
+    return with_tile(TILE, [&](auto tt) {
+      return with_flags(flags, [&](auto fl, auto od) {
+        constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
+        const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
+        k_fwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, TT>
+            <<<nt, tile_threads(TT), 0, st>>>(rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, out, T, asum, fg, slog,
+                                               sa, sac);
+        return check_launch("k_fwd_cull");
+      });
+    });
+  });
+}
+
+size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE) {
+  const int t = TILE > 0 ? TILE : 1;
+  const size_t nt = (size_t)((W + t - 1) / t) * ((H + t - 1) / t);
+  return align256(sizeof(float) * kAcc * (size_t)(N > 0 ? N : 1)) + align256(sizeof(float) * nt * (C > 0 ? C : 1));
+}
+
+int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, int N, int C, int H, int W,
+                     int TILE, int flags, const float* bg, const float* T, const float* asum, const float* fg,
+                     const float* gout, const float* dslog, const float* dsa, const float* dsac, float* g_mu,
+                     float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws,
+                     size_t ws_bytes, void* stream) {
+  if (N < 1 || H < 1 || W < 1) return set_error(kInvalid, "splat_render_bwd: N=%d H=%d W=%d", N, H, W);
+  if (!rec || !gid_sorted || !tile_starts || !g_mu || !g_scale || !g_op || !g_color)
+    return set_error(kInvalid, "splat_render_bwd: null pointer");
+  const bool fields = flags & kFlagFields;
+  if (fields ? (!dslog || !dsa || !dsac) : (!bg || !T || !asum || !fg || !gout))
+    return set_error(kInvalid, "splat_render_bwd: null upstream for flags=%d", flags);
+  if (ws_bytes < splat_render_bwd_workspace_bytes(N, C, H, W, TILE))
+    return set_error(kWorkspace, "splat_render_bwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  float* acc = (float*)ws;
+  float* bg_part = (float*)((char*)ws + align256(sizeof(float) * kAcc * (size_t)N));
+  const size_t nacc = (size_t)kAcc * N;
+  k_fill_f32<<<(unsigned)((nacc + 255) / 256), 256, 0, st>>>(acc, nacc, 0.f);
+  return with_c(C, [&](auto cc) {
+    return with_tile(TILE, [&](auto tt) {
+      return with_flags(flags, [&](auto fl, auto od) {
+        constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
+        constexpr bool FL = decltype(fl)::value != 0;
+        const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
+        k_bwd_cull<CC, FL, decltype(od)::value != 0, TT><<<nt, 64, 0, st>>>(
+            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, acc,
+            (!FL && g_bg) ? bg_part : nullptr);
+        const int nbs = (N + 255) / 256;
+        const bool want_bg = !FL && g_bg;
+        k_bwd_finalize<CC><<<nbs + (want_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op, g_color,
+                                                                   bg_part, nt, want_bg ? g_bg : nullptr);
+        return check_launch("splat_render_bwd");
+      });
+    });
+  });
+}
+
+int splat_exact_fwd(const float* rec, int N, int C, const float* py, const float* px, int P, const float* bg, float* out,
+                    float* T, float* asum, float* fg, void* stream) {
+  if (N < 0 || P < 1 || !rec || !py || !px || !bg || !out || !T || !asum || !fg)
+    return set_error(kInvalid, "splat_exact_fwd: bad arguments N=%d P=%d", N, P);
+  hipStream_t st = (hipStream_t)stream;
+  return with_c(C, [&](auto cc) {
+    k_fwd_exact<decltype(cc)::value><<<(P + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, out, T, asum, fg);
+    return check_launch("k_fwd_exact");
+  });
+}
+
+size_t splat_exact_bwd_workspace_bytes(int N, int C, int P) {
+  return align256(sizeof(float) * kAcc * (size_t)(N > 0 ? N : 1)) +
+         align256(sizeof(float) * (size_t)((P + 255) / 256 + 1) * (C > 0 ? C : 1));
+}
+
+int splat_exact_bwd(const float* rec, int N, int C, const float* py, const float* px, int P, const float* bg,
+                    const float* T, const float* asum, const float* fg, const float* gout, float* g_mu, float* g_scale,
+                    float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws, size_t ws_bytes, void* stream) {
+  if (N < 1 || P < 1 || !rec || !py || !px || !bg || !T || !asum || !fg || !gout || !g_mu || !g_scale || !g_op ||
+      !g_color)
+    return set_error(kInvalid, "splat_exact_bwd: bad arguments N=%d P=%d", N, P);
+  if (ws_bytes < splat_exact_bwd_workspace_bytes(N, C, P)) return set_error(kWorkspace, "splat_exact_bwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  float* acc = (float*)ws;
+  float* part = (float*)((char*)ws + align256(sizeof(float) * kAcc * (size_t)N));
+  const int nchunk = (P + 255) / 256;
+  return with_c(C, [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    k_bwd_exact<CC><<<(N + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, T, asum, fg, gout, acc);
+    if (g_bg) k_bg_partial<CC><<<nchunk, 256, 0, st>>>(gout, T, P, part);
+    k_bwd_finalize<CC><<<(N + 255) / 256 + (g_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op,
+                                                                         g_color, part, nchunk, g_bg);
+    return check_launch("splat_exact_bwd");
+  });
+}
+
+}  // extern "C"

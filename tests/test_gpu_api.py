@@ -1,0 +1,172 @@
+"""Entry-point parity (render_alpha_full_triton, render_alpha_multires, render_alpha_octave and the
+render.py entry points) with autograd, against the torch float64 oracle, plus the reference's own
+self-test identities (render_triton.py:983-1533) and error behaviour."""
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, np_, random_scene, rel_err
+from gaussian_splat_encoder import render as R_api
+from oracle import render_ref as R
+
+pytestmark = pytest.mark.gpu
+NAMES = ["mu", "ls", "col", "op", "bg", "th"]
+
+
+def device_run(fn, scene, gout, **kw):
+    L = [None if t is None else t.detach().clone().requires_grad_(True) for t in scene]
+    out = fn(*L[:5], theta=L[5], **kw)
+    (out * gout).sum().backward()
+    return out.detach(), {n: (None if t is None else t.grad) for n, t in zip(NAMES, L)}
+
+
+def oracle_run(kind, scene, gout, H, W, **kw):
+    """float64 oracle of one batch; binning/routing use the device's fp32 activated scale."""
+    mu, ls, col, op, bg, th = [None if t is None else t[0] for t in scene]
+    L = R.leaves(mu, ls, col, op, bg, th)
+    sc32 = activate_scale(ls).detach().cpu()
+    sc64 = R.activate_scale(L[1])
+    if kind == "cull":
+        cutoff, odds, TILE = kw.get("cutoff", 3.0), kw.get("odds", False), kw.get("TILE", 8)
+        gid, st = R._bin(L[0], sc32, H, W, TILE, cutoff)
+        out = R.cull_composite(L[0], sc64, L[2], L[3], L[4], L[5], gid, st, H, W, TILE, odds)[0]
+    elif kind == "exact":
+        out = R.exact(L[0], sc64, L[2], L[3], L[4], L[5], H, W)
+    elif kind == "multires":
+        out = R.multires(L[0], sc64, L[2], L[3], L[4], L[5], H, W, scale32=sc32, **kw)
+    elif kind == "octave":
+        oct_dev = RH._octave_of(activate_scale(ls).detach().amax(-1) * float(min(H, W)),
+                                kw.get("base_texels", 8.0), kw.get("max_octaves", 6)).cpu()
+        out = R.octave(L[0], sc64, L[2], L[3], L[4], L[5], H, W, oct=oct_dev, scale32=sc32, **kw)
+    g = gout[0].permute(1, 2, 0).reshape(H * W, -1).cpu().to(torch.float64)
+    (out * g).sum().backward()
+    img = out.detach().reshape(H, W, -1).permute(2, 0, 1)
+    return img, {n: (None if t is None else t.grad) for n, t in zip(NAMES, L)}
+
+
+def compare(dev_out, dev_g, ref_out, ref_g, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL):
+    d = np.abs(np_(dev_out[0]) - ref_out.numpy()).max()
+    assert d <= img_tol, f"image max-abs {d:.2e}"
+    for n in NAMES:
+        if ref_g[n] is None:
+            assert dev_g[n] is None
+            continue
+        e = rel_err(np_(dev_g[n][0]), ref_g[n].numpy())
+        assert e <= grad_tol, f"grad {n}: rel {e:.2e}"
+
+
+def gout_for(H, W, dev, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(1, 3, H, W, generator=g).to(dev)
+
+
+@pytest.mark.parametrize("odds", [False, True])
+@pytest.mark.parametrize("has_theta", [True, False])
+def test_cull_entry_point(dev, odds, has_theta):
+    H = W = 48
+    scene = random_scene(500, H, W, seed=21, dev=dev, op_max=0.95, theta=has_theta)
+    gout = gout_for(H, W, dev, 1)
+    out, g = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=True, odds=odds)
+    ref, rg = oracle_run("cull", scene, gout, H, W, odds=odds)
+    compare(out, g, ref, rg)
+
+
+def test_exact_entry_point_and_render_py(dev):
+    H = W = 24
+    scene = random_scene(200, H, W, seed=22, dev=dev, ls_mean_px=2.0)
+    gout = gout_for(H, W, dev, 2)
+    out, g = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=False)
+    ref, rg = oracle_run("exact", scene, gout, H, W)
+    compare(out, g, ref, rg)
+    out2, g2 = device_run(R_api.render_alpha_full, scene, gout, H=H, W=W)
+    assert torch.equal(out2, out)
+    # subsampled pixels equal the full render at those pixels
+    idx = torch.randperm(H * W, generator=torch.Generator().manual_seed(3))[:100].to(dev)[None]
+    sub, got_idx = R_api.render_alpha_subsampled(*scene[:5], H, W, theta=scene[5], pixel_indices=idx)
+    full = out.reshape(1, 3, H * W)
+    assert torch.equal(got_idx, idx)
+    assert (sub - full[:, :, idx[0]]).abs().max().item() <= 2e-6
+
+
+def test_multires_none_equals_cull(dev):
+    """render_triton.py:1214-1253: the fields path with deferred composite equals the in-kernel composite."""
+    H = W = 64
+    scene = random_scene(1024, H, W, seed=7, dev=dev)
+    gout = gout_for(H, W, dev, 3)
+    a, ga = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=True)
+    b, gb = device_run(RH.render_alpha_multires, scene, gout, H=H, W=W, n_coarse=None)
+    assert (a - b).abs().max().item() <= 1e-6
+    for n in NAMES:
+        assert rel_err(np_(gb[n]), np_(ga[n])) <= 1e-4, n
+
+
+@pytest.mark.parametrize("odds", [False, True])
+def test_octave_zero_equals_cull(dev, odds):
+    """render_triton.py:1334-1367 and 1500-1533 (odds)."""
+    H = W = 64
+    scene = random_scene(1024, H, W, seed=13, dev=dev, op_max=0.9)
+    gout = gout_for(H, W, dev, 4)
+    a, ga = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=True, odds=odds)
+    b, gb = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, max_octaves=0, odds=odds)
+    assert (a - b).abs().max().item() <= 1e-6
+    for n in NAMES:
+        assert rel_err(np_(gb[n]), np_(ga[n])) <= 1e-4, n
+
+
+@pytest.mark.parametrize("odds", [False, True])
+def test_octave_multi_level(dev, odds):
+    """Splats spanning several octaves (render_triton.py:1370-1402's scene shape) against the oracle's
+    octave glue over the same routing."""
+    H = W = 128
+    g = torch.Generator().manual_seed(17)
+    n = 400
+    sig = torch.exp(torch.rand(1, n, generator=g) * (np.log(0.31) - np.log(0.006)) + np.log(0.006))
+    ls = torch.log(torch.exp(sig).clamp_min(1 + 1e-6) - 1.0).unsqueeze(-1).expand(1, n, 2).contiguous()
+    mu = torch.rand(1, n, 2, generator=g)
+    col = torch.rand(1, n, 3, generator=g)
+    op = torch.rand(1, n, generator=g) * 0.4
+    th = torch.rand(1, n, generator=g) * 3.14159
+    bg = torch.rand(1, 3, generator=g)
+    scene = [t.to(dev) for t in (mu, ls, col, op, bg, th)]
+    gout = gout_for(H, W, dev, 5)
+    out, gd = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, odds=odds)
+    ref, rg = oracle_run("octave", scene, gout, H, W, odds=odds)
+    compare(out, gd, ref, rg)
+
+
+def test_multires_split(dev):
+    H = W = 128
+    scene = list(random_scene(576, H, W, seed=11, dev=dev))
+    ls = scene[1].clone()
+    ls[:, :64] = float(np.log(np.exp(0.12) - 1.0))
+    ls[:, 64:] = float(np.log(np.exp(0.015) - 1.0))
+    scene[1] = ls
+    gout = gout_for(H, W, dev, 6)
+    out, gd = device_run(RH.render_alpha_multires, scene, gout, H=H, W=W, n_coarse=64, coarse_factor=8)
+    ref, rg = oracle_run("multires", scene, gout, H, W, n_coarse=64, coarse_factor=8)
+    compare(out, gd, ref, rg)
+
+
+def test_errors(dev):
+    scene = random_scene(64, 32, 32, seed=1, dev=dev)
+    with pytest.raises(NotImplementedError):
+        RH.render_alpha_full_triton(*scene[:5], 32, 32, theta=scene[5], cull=False, odds=True)
+    with pytest.raises(RH.PairBudgetExceeded):
+        RH.render_alpha_octave(*scene[:5], 32, 32, theta=scene[5], max_pairs=10)
+    with pytest.raises(Exception, match="TILE"):
+        RH.render_alpha_full_triton(*scene[:5], 32, 32, theta=scene[5], cull=True, TILE=5)
+
+
+def test_batch_of_three(dev):
+    H = W = 40
+    scene = random_scene(300, H, W, seed=31, dev=dev, B=3)
+    g = torch.Generator().manual_seed(8)
+    gout = torch.randn(3, 3, H, W, generator=g).to(dev)
+    out, gd = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, odds=True)
+    for b in range(3):
+        one = [None if t is None else t[b:b + 1] for t in scene]
+        o1, g1 = device_run(RH.render_alpha_octave, one, gout[b:b + 1], H=H, W=W, odds=True)
+        assert (o1[0] - out[b]).abs().max().item() <= 1e-6
+        for n in ["mu", "ls", "col", "op", "th"]:
+            assert rel_err(np_(g1[n][0]), np_(gd[n][b])) <= 1e-5, n

@@ -1,0 +1,74 @@
+"""Bit-exact binning on the GPU: the device pair list and tile starts equal the oracle's
+(render_triton.py:351-409) for the benchmark configurations and for edge cases."""
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import RH, activate_scale, device_bins, np_, random_scene
+from gaussian_splat_encoder import synth
+from oracle import c_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def check_equal(mu, sc, H, W, TILE, cutoff):
+    gid_d, st_d = device_bins(mu, sc, H, W, TILE, cutoff)
+    for b in range(mu.shape[0]):
+        gid_o, st_o = c_oracle.build_tiles(np_(mu[b]), np_(sc[b]), H, W, TILE, cutoff)
+        assert np.array_equal(st_d[b], st_o), f"tile_starts differ (batch {b})"
+        assert np.array_equal(gid_d[b], gid_o), f"gid_sorted differs (batch {b}, tot {st_o[-1]})"
+
+
+@pytest.mark.parametrize("name,TILE", [("c0", 8), ("c1", 8), ("c1", 4), ("c1", 16), ("c4", 8)])
+def test_configs_bit_exact(dev, name, TILE):
+    s = synth.config(name)
+    mu = s.mu.to(dev)
+    sc = activate_scale(s.log_scale.to(dev))
+    check_equal(mu, sc, s.H, s.W, TILE, 3.0)
+
+
+@pytest.mark.parametrize("H,W,TILE,cutoff,n,margin", [
+    (37, 51, 8, 3.0, 300, 0.3),        # ragged canvas, splats off canvas (clamped to edge tiles)
+    (37, 51, 4, 5.0, 300, 0.0),
+    (100, 60, 16, 3.0, 2000, 0.1),
+    (8, 8, 8, 3.0, 50, 0.5),           # a single tile: no radix pass
+    (2100, 2100, 8, 3.0, 20000, 0.0),  # 69,169 tiles: 17-bit keys, three radix passes
+])
+def test_edge_cases_bit_exact(dev, H, W, TILE, cutoff, n, margin):
+    mu, ls, *_ = random_scene(n, H, W, seed=H + W + n, dev=dev, margin=margin, B=2)
+    check_equal(mu, activate_scale(ls), H, W, TILE, cutoff)
+
+
+def test_near_tile_edges_not_fma_contracted(dev):
+    """Centres placed within one ulp of `tile edge + radius`, where a fused multiply-subtract floors
+    differently from the reference's separately rounded ops."""
+    rng = np.random.default_rng(3)
+    H = W = 768
+    n = 20000
+    tx = rng.integers(1, 95, n)
+    sx = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    rx = (np.float32(3.0) * sx).astype(np.float32) * np.float32(W)
+    mx = ((tx * 8 + rx) / W).astype(np.float32)
+    mx = np.nextafter(mx, np.where(rng.random(n) < 0.5, -np.inf, np.inf).astype(np.float32))
+    my = rng.random(n).astype(np.float32)
+    mu = torch.from_numpy(np.stack([my, mx], -1))[None].to(dev)
+    sc = torch.from_numpy(np.stack([sx * np.float32(0.7), sx], -1))[None].to(dev)
+    check_equal(mu, sc, H, W, 8, 3.0)
+
+
+def test_empty_and_single(dev):
+    z = torch.zeros(1, 0, 2, device=dev)
+    gid_b, st_b, ntx, nt = RH._build_tiles(z, z, 32, 32, 8, 3.0)
+    assert gid_b[0].tolist() == [0] and st_b[0].tolist() == [0] * 17 and (ntx, nt) == (4, 16)
+    mu = torch.tensor([[[0.5, 0.5]]], device=dev)
+    sc = torch.tensor([[[0.01, 0.02]]], device=dev)
+    check_equal(mu, sc, 32, 32, 8, 3.0)
+
+
+def test_pair_budget_raises_before_allocation(dev):
+    s = synth.config("c0")
+    mu = s.mu.to(dev)
+    sc = activate_scale(s.log_scale.to(dev))
+    with pytest.raises(RH.PairBudgetExceeded):
+        RH._build_tiles(mu, sc, s.H, s.W, 8, 3.0, max_pairs=100)

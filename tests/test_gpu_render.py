@@ -1,0 +1,100 @@
+"""Kernel-level parity of the per-tile forward and backward against the float64 C oracle over the same
+(bit-exact) pair lists: images within 1e-5 max-abs, gradients within 1e-4 relative."""
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, np_, random_scene, rel_err
+from gaussian_splat_encoder import synth
+from oracle import c_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_pairs(mu, sc, H, W, TILE, cutoff=3.0):
+    return c_oracle.build_tiles(np_(mu[0]), np_(sc[0]), H, W, TILE, cutoff)
+
+
+def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True):
+    dev = mu.device
+    sc = activate_scale(ls)
+    P, C = H * W, col.shape[-1]
+    gid, st = oracle_pairs(mu, sc, H, W, TILE)
+    args = [np_(mu[0]), np_(sc[0]), None if th is None else np_(th[0]), np_(op[0]), np_(col[0])]
+    g = torch.Generator().manual_seed(seed)
+    if fields:
+        slog, sa, sac, bins = RH._forward_cull_fields(mu, sc, col, op, th, H, W, TILE, odds=odds)
+        ref = c_oracle.fwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=True)
+        for got, r in zip((slog, sa, sac), ref):
+            got = np_(got[0]).reshape(r.shape)
+            assert np.all(np.abs(got - r) <= 2e-5 * (1.0 + np.abs(r))), np.abs(got - r).max()
+        # the image composited from the fields meets the image bar
+        T = np.exp(ref[0]); asum = np.maximum(ref[1], 1e-8)
+        img_ref = (1 - T)[:, None] * ref[2] / asum[:, None] + T[:, None] * np_(bg[0])
+        img = RH._composite_fields(slog, sa, sac, bg, 1, H, W, C)[0].permute(1, 2, 0).reshape(P, C)
+        assert np.abs(np_(img) - img_ref).max() <= IMG_TOL
+        if not check_bwd:
+            return
+        ups = [torch.randn(s.shape, generator=g) for s in (slog, sa, sac)]
+        grads = RH._backward_cull_fields(*[u.to(dev) for u in ups], mu, sc, col, op, th, bins, H, W, TILE, odds=odds)
+        gref = c_oracle.bwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=True, dslog=ups[0][0].numpy(),
+                                 dsa=ups[1][0].numpy(), dsac=ups[2][0].numpy())
+        names = ["mu", "scale", "col", "op", "theta"]
+    else:
+        out, (T, asum, fg), bins = RH._forward_cull(mu, sc, col, op, bg, th, H, W, TILE, odds=odds)
+        ref = c_oracle.fwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=False, bg=np_(bg[0]))
+        assert np.abs(np_(out[0]) - ref[0]).max() <= IMG_TOL
+        assert np.abs(np_(T[0]) - ref[1]).max() <= IMG_TOL
+        if not check_bwd:
+            return
+        gout = torch.randn(out.shape, generator=g).to(dev)
+        grads = RH._backward_cull(gout, mu, sc, col, op, bg, th, T, asum, fg, bins, H, W, TILE, odds=odds)
+        gref = c_oracle.bwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=False, bg=np_(bg[0]), T=ref[1],
+                                 asum=ref[2], fg=ref[3], gout=np_(gout[0]))
+        names = ["mu", "scale", "col", "op", "bg", "theta"]
+    for name, got in zip(names, grads):
+        if got is None:
+            assert name == "theta" and th is None
+            continue
+        r = gref[name]
+        e = rel_err(np_(got[0]), r)
+        assert e <= GRAD_REL_TOL, f"{name}: rel {e:.2e}"
+
+
+@pytest.mark.parametrize("odds", [False, True])
+@pytest.mark.parametrize("fields", [False, True])
+@pytest.mark.parametrize("has_theta", [True, False])
+def test_modes_small(dev, odds, fields, has_theta):
+    H = W = 64
+    scene = random_scene(1024, H, W, seed=11, dev=dev, op_max=0.99, theta=has_theta)
+    run_case(*scene, H, W, 8, odds, fields, seed=1)
+
+
+@pytest.mark.parametrize("TILE,H,W", [(4, 37, 51), (8, 37, 51), (16, 37, 51), (16, 96, 64)])
+def test_tiles_and_ragged_canvas(dev, TILE, H, W):
+    scene = random_scene(600, H, W, seed=TILE * 7 + H, dev=dev, margin=0.2)
+    run_case(*scene, H, W, TILE, odds=False, fields=False, seed=2)
+    run_case(*scene, H, W, TILE, odds=True, fields=True, seed=3)
+
+
+def test_alpha_clamp_gate(dev):
+    """Opacity 1 at pixel centres drives a onto the 1 - 1e-4 clamp, where the gradient is gated off."""
+    H = W = 32
+    mu, ls, col, op, bg, th = random_scene(200, H, W, seed=5, dev=dev, ls_mean_px=4.0)
+    mu = ((torch.floor(mu * H) + 0.5) / H).contiguous()
+    op = torch.ones_like(op)
+    run_case(mu, ls, col, op, bg, th, H, W, 8, odds=False, fields=False, seed=4)
+    run_case(mu, ls, col, op, bg, th, H, W, 8, odds=True, fields=False, seed=5)
+
+
+def test_c0_config(dev):
+    s = synth.config("c0").to(dev)
+    run_case(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.theta[:, :], s.H, s.W, 8, False, False, seed=6)
+
+
+@pytest.mark.parametrize("odds,fields", [(False, False), (True, True)])
+def test_c1_full_size(dev, odds, fields):
+    """The headline configuration: 768 x 768, 92,160 splats, forward and backward."""
+    s = synth.config("c2").to(dev)
+    run_case(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.theta, s.H, s.W, 8, odds, fields, seed=7)
