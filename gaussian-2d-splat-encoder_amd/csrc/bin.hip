@@ -155,9 +155,13 @@ __device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi
   return lo;
 }
 
+// keys[p] = tile of splat-major pair p. With `pair_splat` set (radix passes follow), vals[p] = p and
+// pair_splat[p] = its splat; otherwise (single-tile grid, no pass) vals[p] = splat is already the final
+// list and inv[p] = p.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
                                                           int N, int ntx, int tot, int dmask, int* __restrict__ keys,
-                                                          int* __restrict__ vals, int* __restrict__ hist, int nblocks) {
+                                                          int* __restrict__ vals, int* __restrict__ pair_splat,
+                                                          int* __restrict__ inv, int* __restrict__ hist, int nblocks) {
   __shared__ int s_off[kSortKeys + 1];
   __shared__ int s_hist[256];
   __shared__ int s_rng[2];
@@ -190,7 +194,13 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
     const int kx = k - ky * rc.z;
     const int tile = (rc.y + ky) * ntx + rc.x + kx;
     keys[p] = tile;
-    vals[p] = g;
+    if (pair_splat) {
+      vals[p] = p;
+      pair_splat[p] = g;
+    } else {
+      vals[p] = g;
+      if (inv) inv[p] = p;
+    }
     if (hist) atomicAdd(&s_hist[tile & dmask], 1);
   }
   if (!hist) return;
@@ -216,10 +226,13 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ k
 // walks them 64 at a time in index order; lanes holding the same digit are ranked among themselves with
 // ballots (lane order = index order), on top of the wave's running count for that digit. Wave counts are
 // then prefixed across the waves, and the block's base for each digit comes from the scanned histogram.
+// On the final pass (`pair_splat` set) the carried splat-major position v becomes the splat id
+// pair_splat[v] in the output, and inv[v] receives the pair's sorted position.
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
                                                           int tot, int shift, int dbits, const int* __restrict__ hist_scan,
                                                           int nblocks, int* __restrict__ keys_out,
-                                                          int* __restrict__ vals_out) {
+                                                          int* __restrict__ vals_out,
+                                                          const int* __restrict__ pair_splat, int* __restrict__ inv) {
   __shared__ int s_cnt[kWaves][256];
   __shared__ int s_base[256];
   const int dmask = (1 << dbits) - 1;
@@ -264,7 +277,12 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     const int d = (key[j] >> shift) & dmask;
     const int pos = s_cnt[wv][d] + rank[j];
     keys_out[pos] = key[j];
-    vals_out[pos] = val[j];
+    if (pair_splat) {
+      vals_out[pos] = pair_splat[val[j]];
+      if (inv) inv[val[j]] = pos;
+    } else {
+      vals_out[pos] = val[j];
+    }
   }
 }
 
@@ -353,6 +371,11 @@ __global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ 
     for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
 }
 
+__global__ void k_copy_i32(const int* __restrict__ src, int* __restrict__ dst, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
 __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) a[i] = v;
@@ -363,7 +386,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct PairsPlan {
   int nblk, passes, dbits, radix, nscan_part;
-  size_t off_keys_a, off_keys_b, off_vals_b, off_hist, off_part, total;
+  size_t off_keys_a, off_keys_b, off_vals_b, off_psplat, off_hist, off_part, total;
 };
 
 static PairsPlan plan_pairs(int nt, long long tot) {
@@ -380,6 +403,7 @@ static PairsPlan plan_pairs(int nt, long long tot) {
   p.off_keys_a = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_keys_b = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_vals_b = o; o += align256(sizeof(int) * (size_t)tot);
+  p.off_psplat = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_hist = o;   o += align256(sizeof(int) * (size_t)(nh > 0 ? nh : 1));
   p.off_part = o;   o += align256(sizeof(int) * (size_t)p.nscan_part);
   p.total = o;
@@ -441,7 +465,7 @@ size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
 }
 
 int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, long long tot, int* gid_sorted,
-                    int* tile_starts, void* ws, size_t ws_bytes, void* stream) {
+                    int* tile_starts, int* pair_splat, int* pair_inv, void* ws, size_t ws_bytes, void* stream) {
   if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
     return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
   if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
@@ -458,26 +482,33 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
   int* keys_a = (int*)(base + pl.off_keys_a);
   int* keys_b = (int*)(base + pl.off_keys_b);
   int* vals_b = (int*)(base + pl.off_vals_b);
+  int* psplat = pair_splat ? pair_splat : (int*)(base + pl.off_psplat);
   int* hist = (int*)(base + pl.off_hist);
   int* part = (int*)(base + pl.off_part);
   const int fin = pl.passes & 1;
   int* K[2];
   int* V[2];
-  K[fin] = keys_a; V[fin] = gid_sorted;
-  K[1 - fin] = keys_b; V[1 - fin] = vals_b;
+  // Pass k reads buffer k % 2 and writes (k + 1) % 2, so the final pass lands in buffer `fin`; with no
+  // pass the scatter's own output (buffer 0 = fin) is final.
+  K[fin] = keys_a; K[1 - fin] = keys_b;
+  V[fin] = gid_sorted; V[1 - fin] = vals_b;
   const int t = (int)tot;
   const int dmask = pl.radix - 1;
   k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, ntx, t, dmask, K[0], V[0],
-                                              pl.passes ? hist : nullptr, pl.nblk);
+                                              pl.passes ? psplat : nullptr, pair_inv, pl.passes ? hist : nullptr,
+                                              pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
+  if (pl.passes == 0 && pair_splat) k_copy_i32<<<div_up(t, 256), 256, 0, st>>>(gid_sorted, pair_splat, t);
   for (int pass = 0; pass < pl.passes; ++pass) {
     const int shift = pass * pl.dbits;
     const int src = pass & 1, dst = 1 - src;
+    const bool last = pass == pl.passes - 1;
     if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], t, shift, dmask, hist, pl.nblk);
     rc = scan_exclusive(hist, pl.radix * pl.nblk, part, st);
     if (rc) return rc;
-    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, pl.nblk, K[dst], V[dst]);
+    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, pl.nblk, K[dst], V[dst],
+                                                last ? psplat : nullptr, last ? pair_inv : nullptr);
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
   }

@@ -9,8 +9,11 @@
 //
 // Backward: one wave per tile, lane = pair. The tile's per-pixel upstream terms (dS_log, dS_a, dS_ac)
 // are derived once (lane = pixel) into LDS; each lane then walks the tile's pixels for its own pair and
-// accumulates ten per-pair sums in registers (the per-tile reduction), which go to per-splat accumulators
-// with one fp32 atomic each. A finalize pass turns the sums into parameter gradients:
+// accumulates the per-pair sums in registers (the per-tile reduction) and stores them in pair order.
+// No global atomics: a reduce pass walks the pairs in splat-major order (wave = 64 consecutive pairs,
+// gathered through the binning's inverse permutation), sums each splat's pairs with a segmented scan, and
+// a fix-up pass completes splats whose pairs span several waves. Deterministic. The sums become
+// parameter gradients by:
 //   q    = da * falloff where op * falloff < 1 - 1e-4 (0 on the clamp)      da: render_triton.py:688-697
 //   g_op = sum q,   Qu = sum q u,  Qv = sum q v,  Quu = sum q u^2,  Qvv = sum q v^2,  Quv = sum q u v
 //   g_sy = 2 ln2 op Quu / sy,  g_sx = 2 ln2 op Qvv / sx
@@ -27,7 +30,9 @@ namespace splat {
 template <int V>
 using IC = std::integral_constant<int, V>;
 
-constexpr int kAcc = 16;   // per-splat accumulator stride (floats): Q, Qu, Qv, Quu, Qvv, Quv, colour[4]
+constexpr int kAcc = 16;       // per-splat accumulator stride of the exact path (floats)
+constexpr int kPairRec = 12;   // per-pair sums record (floats, 48 B): Q, Qu, Qv, Quu, Qvv, Quv, colour[4], pad
+constexpr int kSums = 10;      // sums carried through the reduction
 
 __host__ __device__ constexpr int tile_threads(int tile) { return tile * tile > 64 ? tile * tile : 64; }
 
@@ -158,15 +163,11 @@ struct PairSums {
   }
 };
 
-// One pixel-pair of the backward, given whitened offsets u, v.
-template <int C, bool ODDS>
-__device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float one_m_op, const float4& col,
-                                               const float4& pa, const float4& pb, PairSums<C>& s) {
-  const float m = fmaf(u, u, v * v);
-  const float f = hw_exp2(-m);
-  const float fo = op * f;
-  const float a = fminf(fo, kClamp);
-  const float rr = hw_rcp(one_minus_alpha(1.f - a, fo, m, op, one_m_op));
+// Rest of one backward pixel-pair once the falloff f, alpha a and 1 / (1 - a) are known. GATED: some
+// lane may sit on the alpha clamp, where the gradient through alpha is zero (render_triton.py:686, 697).
+template <int C, bool ODDS, bool GATED>
+__device__ __forceinline__ void bwd_tail(float u, float v, float f, float a, float rr, bool live, const float4& col,
+                                         const float4& pa, const float4& pb, PairSums<C>& s) {
   float ct = pa.z * col.x;
   if (C > 1) ct = fmaf(pa.w, col.y, ct);
   if (C > 2) ct = fmaf(pb.x, col.z, ct);
@@ -183,7 +184,8 @@ __device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float
   if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
   if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
   if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
-  const float q = fo < kClamp ? da * f : 0.f;   // no gradient through the alpha clamp (:686, :697)
+  float q = da * f;
+  if (GATED) q = live ? q : 0.f;
   const float qu = q * u, qv = q * v;
   s.q += q;
   s.qu += qu;
@@ -193,24 +195,67 @@ __device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float
   s.quv = fmaf(qu, v, s.quv);
 }
 
+// One pixel-pair of the backward, given whitened offsets u, v. Unless some lane of the wave is near-opaque
+// (op * f > kNearOpaque), no lane can be on the clamp and 1 - a = 1 - op * f is accurate: the fast path.
+// Otherwise 1 - a is evaluated as in one_minus_alpha and the clamp gate applies. The branch is
+// wave-uniform; every lane of the wave must be executing.
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float one_m_op, const float4& col,
+                                               const float4& pa, const float4& pb, PairSums<C>& s) {
+  const float m = fmaf(u, u, v * v);
+  const float f = hw_exp2(-m);
+  const float fo = op * f;
+  if (__any(fo > kNearOpaque)) {
+    const float a = fminf(fo, kClamp);
+    const float x = m * kLn2;
+    float p = fmaf(x, 1.f / 120.f, -1.f / 24.f);
+    p = fmaf(p, x, 1.f / 6.f);
+    p = fmaf(p, x, -0.5f);
+    p = fmaf(p, x, 1.f);
+    const float acc = fmaxf(fmaf(op, p * x, one_m_op), 1.f - kClamp);
+    const float oma = fo > kNearOpaque ? acc : 1.f - a;
+    bwd_tail<C, ODDS, true>(u, v, f, a, hw_rcp(oma), fo < kClamp, col, pa, pb, s);
+  } else {
+    bwd_tail<C, ODDS, false>(u, v, f, fo, hw_rcp(1.f - fo), true, col, pa, pb, s);
+  }
+}
+
 template <int C>
-__device__ __forceinline__ void add_sums(float* __restrict__ dst, const PairSums<C>& s) {
-  atomicAdd(dst + 0, s.q);
-  atomicAdd(dst + 1, s.qu);
-  atomicAdd(dst + 2, s.qv);
-  atomicAdd(dst + 3, s.quu);
-  atomicAdd(dst + 4, s.qvv);
-  atomicAdd(dst + 5, s.quv);
+__device__ __forceinline__ void store_pair(float* __restrict__ dst, const PairSums<C>& s) {
+  float4* d = reinterpret_cast<float4*>(dst);
+  d[0] = make_float4(s.q, s.qu, s.qv, s.quu);
+  d[1] = make_float4(s.qvv, s.quv, s.gc[0], C > 1 ? s.gc[1] : 0.f);
+  d[2] = make_float4(C > 2 ? s.gc[2] : 0.f, C > 3 ? s.gc[3] : 0.f, 0.f, 0.f);
+}
+
+// Per-splat sums (Q, Qu, Qv, Quu, Qvv, Quv, colour[C]) -> parameter gradients (formulas at the top).
+template <int C>
+__device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec, const float* sums,
+                                            float* __restrict__ g_mu, float* __restrict__ g_scale,
+                                            float* __restrict__ g_theta, float* __restrict__ g_op,
+                                            float* __restrict__ g_col) {
+  const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+  const float op = r4[1].z;
+  const float4 r3 = r4[3];
+  const float sy = r3.x, sx = r3.y, cs = r3.z, sn = r3.w;
+  const float gry = -op * sums[1] / (kWhiten * sy);
+  const float grx = -op * sums[2] / (kWhiten * sx);
+  g_mu[2 * g + 0] = -(cs * gry - sn * grx);
+  g_mu[2 * g + 1] = -(sn * gry + cs * grx);
+  g_scale[2 * g + 0] = 2.f * kLn2 * op * sums[3] / sy;
+  g_scale[2 * g + 1] = 2.f * kLn2 * op * sums[4] / sx;
+  if (g_theta) g_theta[g] = -2.f * kLn2 * op * sums[5] * ((sx - sy) * (sx + sy) / (sx * sy));
+  g_op[g] = sums[0];
 #pragma unroll
-  for (int c = 0; c < C; ++c) atomicAdd(dst + 6 + c, s.gc[c]);
+  for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = sums[6 + c];
 }
 
 template <int C, bool FIELDS, bool ODDS, int TILE>
-__global__ __launch_bounds__(64) void k_bwd_cull(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
     int nt, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, const float* __restrict__ dslog,
-    const float* __restrict__ dsa, const float* __restrict__ dsac, float* __restrict__ acc,
+    const float* __restrict__ dsa, const float* __restrict__ dsac, float* __restrict__ psum,
     float* __restrict__ bg_part) {
   constexpr int NP = TILE * TILE;
   __shared__ float4 s_pa[NP];
@@ -267,8 +312,102 @@ __global__ __launch_bounds__(64) void k_bwd_cull(
         bwd_accumulate<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, omo, col, pa, pb, s);
       }
     }
-    if (act) add_sums<C>(acc + (size_t)g * kAcc, s);
+    if (act) store_pair<C>(psum + (size_t)i * kPairRec, s);
   }
+}
+
+// Sum each splat's per-pair records in splat-major order. Wave = 64 consecutive splat-major pairs (lane = pair,
+// its record gathered from sorted position pair_inv[q]); pair_splat is non-decreasing along the lanes, so a
+// suffix scan that only adds equal keys leaves each segment's total in its first lane. Segments complete in
+// the wave finish here; a segment cut by a wave boundary leaves its partial sum in pfirst (segment holding
+// lane 0) / plast (segment holding the wave's last pair) for k_reduce_fixup.
+template <int C>
+__global__ __launch_bounds__(256) void k_pair_reduce(const float* __restrict__ rec, const float* __restrict__ psum,
+                                                     const int* __restrict__ pair_splat, const int* __restrict__ pair_inv,
+                                                     const int* __restrict__ offsets, int tot, float* __restrict__ g_mu,
+                                                     float* __restrict__ g_scale, float* __restrict__ g_theta,
+                                                     float* __restrict__ g_op, float* __restrict__ g_col,
+                                                     float* __restrict__ pfirst, float* __restrict__ plast) {
+  const int lane = threadIdx.x & 63;
+  const int chunk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int q0 = chunk * 64;
+  if (q0 >= tot) return;
+  const int q = q0 + lane;
+  const bool act = q < tot;
+  const int g = act ? pair_splat[q] : -1;
+  float v[kSums];
+  {
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a, c = a;
+    if (act) {
+      const float4* p4 = reinterpret_cast<const float4*>(psum + (size_t)pair_inv[q] * kPairRec);
+      a = p4[0]; b = p4[1]; c = p4[2];
+    }
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y;
+    v[6] = b.z; v[7] = b.w; v[8] = c.x; v[9] = c.y;
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int og = __shfl_down(g, d, 64);
+    const bool take = lane + d < 64 && og == g;
+#pragma unroll
+    for (int k = 0; k < 6 + C; ++k) {
+      const float o = __shfl_down(v[k], d, 64);
+      if (take) v[k] += o;
+    }
+  }
+  const int gprev = __shfl_up(g, 1, 64);
+  if (!act || (lane > 0 && gprev == g)) return;
+  const int qs = offsets[g], qe = offsets[g + 1];
+  const bool starts_here = qs >= q0, ends_here = qe <= q0 + 64;
+  if (starts_here && ends_here) {
+    splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
+    return;
+  }
+  if (!starts_here)
+    for (int k = 0; k < kSums; ++k) pfirst[(size_t)chunk * kSums + k] = v[k];
+  if (!ends_here)
+    for (int k = 0; k < kSums; ++k) plast[(size_t)chunk * kSums + k] = v[k];
+}
+
+// Splats whose pairs span waves c0..c1 of k_pair_reduce: plast[c0] + pfirst[c0+1..c1], in order. Splats with
+// no pair get zero gradients. With g_bg set, the last workgroup also reduces the per-tile g_bg partials.
+template <int C>
+__global__ __launch_bounds__(256) void k_reduce_fixup(const float* __restrict__ rec, const int* __restrict__ offsets,
+                                                      int N, const float* __restrict__ pfirst,
+                                                      const float* __restrict__ plast, float* __restrict__ g_mu,
+                                                      float* __restrict__ g_scale, float* __restrict__ g_theta,
+                                                      float* __restrict__ g_op, float* __restrict__ g_col,
+                                                      const float* __restrict__ bg_part, int nparts,
+                                                      float* __restrict__ g_bg) {
+  if ((int)blockIdx.x >= (N + 255) / 256) {
+    __shared__ float s_w[4][kMaxC];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      float x = 0.f;
+      for (int i = threadIdx.x; i < nparts; i += 256) x += bg_part[(size_t)i * C + c];
+      x = wave_sum(x);
+      if (lane == 0) s_w[wv][c] = x;
+    }
+    __syncthreads();
+    if (threadIdx.x < C)
+      g_bg[threadIdx.x] = (s_w[0][threadIdx.x] + s_w[1][threadIdx.x]) + (s_w[2][threadIdx.x] + s_w[3][threadIdx.x]);
+    return;
+  }
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= N) return;
+  const int qs = offsets[g], qe = offsets[g + 1];
+  float v[kSums];
+  if (qe <= qs) {
+    for (int k = 0; k < kSums; ++k) v[k] = 0.f;
+  } else {
+    const int c0 = qs >> 6, c1 = (qe - 1) >> 6;
+    if (c0 == c1) return;
+    for (int k = 0; k < kSums; ++k) v[k] = plast[(size_t)c0 * kSums + k];
+    for (int c = c0 + 1; c <= c1; ++c)
+      for (int k = 0; k < kSums; ++k) v[k] += pfirst[(size_t)c * kSums + k];
+  }
+  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
 // Exact path backward (render_triton.py:161-266): lane = splat over every pixel; the per-pixel upstream
@@ -335,24 +474,23 @@ __global__ __launch_bounds__(256) void k_bg_partial(const float* __restrict__ go
                                                                      s_w[2][threadIdx.x] + s_w[3][threadIdx.x];
 }
 
-// Per-splat sums -> parameter gradients. With g_bg set, the last workgroup also reduces the nparts
-// per-tile (or per-chunk) partials of sum_p gout * T.
+// Exact path: per-splat sums (stride kAcc) -> parameter gradients. With g_bg set, the last workgroup also
+// reduces the nparts per-chunk partials of sum_p gout * T.
 template <int C>
-__global__ __launch_bounds__(256) void k_bwd_finalize(const float* __restrict__ rec, const float* __restrict__ acc, int N,
+__global__ __launch_bounds__(256) void k_acc_finalize(const float* __restrict__ rec, const float* __restrict__ acc, int N,
                                                       float* __restrict__ g_mu, float* __restrict__ g_scale,
                                                       float* __restrict__ g_theta, float* __restrict__ g_op,
                                                       float* __restrict__ g_col, const float* __restrict__ bg_part,
                                                       int nparts, float* __restrict__ g_bg) {
-  const int nb_splat = (N + 255) / 256;
-  if ((int)blockIdx.x >= nb_splat) {
+  if ((int)blockIdx.x >= (N + 255) / 256) {
     __shared__ float s_w[4][kMaxC];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      float v = 0.f;
-      for (int i = threadIdx.x; i < nparts; i += 256) v += bg_part[(size_t)i * C + c];
-      v = wave_sum(v);
-      if (lane == 0) s_w[wv][c] = v;
+      float x = 0.f;
+      for (int i = threadIdx.x; i < nparts; i += 256) x += bg_part[(size_t)i * C + c];
+      x = wave_sum(x);
+      if (lane == 0) s_w[wv][c] = x;
     }
     __syncthreads();
     if (threadIdx.x < C)
@@ -361,27 +499,9 @@ __global__ __launch_bounds__(256) void k_bwd_finalize(const float* __restrict__ 
   }
   const int g = blockIdx.x * 256 + threadIdx.x;
   if (g >= N) return;
-  const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
-  const float op = r4[1].z;
-  const float4 r3 = r4[3];
-  const float sy = r3.x, sx = r3.y, cs = r3.z, sn = r3.w;
-  const float* a = acc + (size_t)g * kAcc;
-  const float q = a[0], qu = a[1], qv = a[2], quu = a[3], qvv = a[4], quv = a[5];
-  const float gry = -op * qu / (kWhiten * sy);
-  const float grx = -op * qv / (kWhiten * sx);
-  g_mu[2 * g + 0] = -(cs * gry - sn * grx);
-  g_mu[2 * g + 1] = -(sn * gry + cs * grx);
-  g_scale[2 * g + 0] = 2.f * kLn2 * op * quu / sy;
-  g_scale[2 * g + 1] = 2.f * kLn2 * op * qvv / sx;
-  if (g_theta) g_theta[g] = -2.f * kLn2 * op * quv * ((sx - sy) * (sx + sy) / (sx * sy));
-  g_op[g] = q;
-#pragma unroll
-  for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = a[6 + c];
-}
-
-__global__ void k_fill_f32(float* __restrict__ a, size_t n, float v) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) a[i] = v;
+  float v[kSums];
+  for (int k = 0; k < kSums; ++k) v[k] = acc[(size_t)g * kAcc + k];
+  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
 // ---------------------------------------------------------------------------------------------------- dispatch
@@ -447,43 +567,71 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
   });
 }
 
-size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE) {
+struct BwdPlan {
+  size_t off_psum, off_first, off_last, off_bg, total;
+  int nchunk;
+};
+
+static BwdPlan plan_bwd(int C, int H, int W, int TILE, long long tot) {
+  BwdPlan b{};
   const int t = TILE > 0 ? TILE : 1;
   const size_t nt = (size_t)((W + t - 1) / t) * ((H + t - 1) / t);
-  return align256(sizeof(float) * kAcc * (size_t)(N > 0 ? N : 1)) + align256(sizeof(float) * nt * (C > 0 ? C : 1));
+  const size_t np = tot > 0 ? (size_t)tot : 1;
+  b.nchunk = (int)((np + 63) / 64);
+  size_t o = 0;
+  b.off_psum = o; o += align256(sizeof(float) * kPairRec * np);
+  b.off_first = o; o += align256(sizeof(float) * kSums * (size_t)b.nchunk);
+  b.off_last = o; o += align256(sizeof(float) * kSums * (size_t)b.nchunk);
+  b.off_bg = o; o += align256(sizeof(float) * nt * (C > 0 ? C : 1));
+  b.total = o;
+  return b;
 }
 
-int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, int N, int C, int H, int W,
-                     int TILE, int flags, const float* bg, const float* T, const float* asum, const float* fg,
-                     const float* gout, const float* dslog, const float* dsa, const float* dsac, float* g_mu,
-                     float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws,
-                     size_t ws_bytes, void* stream) {
-  if (N < 1 || H < 1 || W < 1) return set_error(kInvalid, "splat_render_bwd: N=%d H=%d W=%d", N, H, W);
-  if (!rec || !gid_sorted || !tile_starts || !g_mu || !g_scale || !g_op || !g_color)
+size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE, long long tot) {
+  (void)N;
+  return plan_bwd(C, H, W, TILE, tot).total;
+}
+
+int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, const int* offsets,
+                     const int* pair_splat, const int* pair_inv, long long tot, int N, int C, int H, int W, int TILE,
+                     int flags, const float* bg, const float* T, const float* asum, const float* fg, const float* gout,
+                     const float* dslog, const float* dsa, const float* dsac, float* g_mu, float* g_scale,
+                     float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws, size_t ws_bytes,
+                     void* stream) {
+  if (N < 1 || H < 1 || W < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
+    return set_error(kInvalid, "splat_render_bwd: N=%d H=%d W=%d tot=%lld", N, H, W, tot);
+  if (!rec || !gid_sorted || !tile_starts || !offsets || !pair_splat || !pair_inv || !g_mu || !g_scale || !g_op ||
+      !g_color)
     return set_error(kInvalid, "splat_render_bwd: null pointer");
   const bool fields = flags & kFlagFields;
   if (fields ? (!dslog || !dsa || !dsac) : (!bg || !T || !asum || !fg || !gout))
     return set_error(kInvalid, "splat_render_bwd: null upstream for flags=%d", flags);
-  if (ws_bytes < splat_render_bwd_workspace_bytes(N, C, H, W, TILE))
-    return set_error(kWorkspace, "splat_render_bwd: workspace too small");
+  const BwdPlan pl = plan_bwd(C, H, W, TILE, tot);
+  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_render_bwd: workspace %zu < %zu bytes", ws_bytes, pl.total);
   hipStream_t st = (hipStream_t)stream;
-  float* acc = (float*)ws;
-  float* bg_part = (float*)((char*)ws + align256(sizeof(float) * kAcc * (size_t)N));
-  const size_t nacc = (size_t)kAcc * N;
-  k_fill_f32<<<(unsigned)((nacc + 255) / 256), 256, 0, st>>>(acc, nacc, 0.f);
+  char* base = (char*)ws;
+  float* psum = (float*)(base + pl.off_psum);
+  float* pfirst = (float*)(base + pl.off_first);
+  float* plast = (float*)(base + pl.off_last);
+  float* bg_part = (float*)(base + pl.off_bg);
+  const int t = (int)tot;
   return with_c(C, [&](auto cc) {
     return with_tile(TILE, [&](auto tt) {
       return with_flags(flags, [&](auto fl, auto od) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
         constexpr bool FL = decltype(fl)::value != 0;
         const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
-        k_bwd_cull<CC, FL, decltype(od)::value != 0, TT><<<nt, 64, 0, st>>>(
-            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, acc,
-            (!FL && g_bg) ? bg_part : nullptr);
-        const int nbs = (N + 255) / 256;
         const bool want_bg = !FL && g_bg;
-        k_bwd_finalize<CC><<<nbs + (want_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op, g_color,
-                                                                   bg_part, nt, want_bg ? g_bg : nullptr);
+        k_bwd_cull<CC, FL, decltype(od)::value != 0, TT><<<nt, 64, 0, st>>>(
+            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, psum,
+            want_bg ? bg_part : nullptr);
+        if (t > 0)
+          k_pair_reduce<CC><<<(pl.nchunk + 3) / 4, 256, 0, st>>>(rec, psum, pair_splat, pair_inv, offsets, t, g_mu,
+                                                                 g_scale, g_theta, g_op, g_color, pfirst, plast);
+        const int nbs = (N + 255) / 256;
+        k_reduce_fixup<CC><<<nbs + (want_bg ? 1 : 0), 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale,
+                                                                    g_theta, g_op, g_color, bg_part, nt,
+                                                                    want_bg ? g_bg : nullptr);
         return check_launch("splat_render_bwd");
       });
     });
@@ -521,7 +669,7 @@ int splat_exact_bwd(const float* rec, int N, int C, const float* py, const float
     constexpr int CC = decltype(cc)::value;
     k_bwd_exact<CC><<<(N + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, T, asum, fg, gout, acc);
     if (g_bg) k_bg_partial<CC><<<nchunk, 256, 0, st>>>(gout, T, P, part);
-    k_bwd_finalize<CC><<<(N + 255) / 256 + (g_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op,
+    k_acc_finalize<CC><<<(N + 255) / 256 + (g_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op,
                                                                          g_color, part, nchunk, g_bg);
     return check_launch("splat_exact_bwd");
   });

@@ -85,26 +85,30 @@ kernel_timer = KernelTimer()
 
 class TileBins:
     """Per-batch binning result: decoded splat records, pair list ordered by (tile, splat) and CSR tile
-    starts. `gid_b`/`starts_b`/`ntx`/`nt` carry the meaning of the reference's `tiles` tuple."""
+    starts (`gid_b`/`starts_b`/`ntx`/`nt` carry the meaning of the reference's `tiles` tuple), plus the
+    splat-major pair maps the backward's per-splat reduction uses (offsets, pair -> splat, pair -> sorted
+    position)."""
 
-    def __init__(self, rec_b, gid_b, starts_b, tot_b, H, W, TILE, ntx, nt):
+    def __init__(self, rec_b, gid_b, starts_b, tot_b, H, W, TILE, ntx, nt, off_b=None, psplat_b=None, pinv_b=None):
         self.rec_b, self.gid_b, self.starts_b, self.tot_b = rec_b, gid_b, starts_b, tot_b
         self.H, self.W, self.TILE, self.ntx, self.nt = H, W, TILE, ntx, nt
+        self.off_b, self.psplat_b, self.pinv_b = off_b, psplat_b, pinv_b
 
     def as_tuple(self):
         return self.gid_b, self.starts_b, self.ntx, self.nt
 
 
-def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None) -> TileBins:
-    """Decode + bin every batch (render_triton.py:351-409). One host read of the per-batch pair totals."""
+def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True) -> TileBins:
+    """Decode + bin every batch (render_triton.py:351-409). One host read of the per-batch pair totals.
+    with_maps=False skips the pair maps only the backward needs (forward-only renders)."""
     _dev_check(mu, scale, color, opacity, theta)
     ev = kernel_timer.record("bin")
-    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs)
+    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps)
     kernel_timer.close("bin", ev)
     return bins
 
 
-def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs):
+def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps):
     B, N, C = color.shape
     dev = mu.device
     lib = _lib.load()
@@ -139,16 +143,18 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs):
                 f"_build_tiles: {worst} (tile,gaussian) pairs exceeds the {max_pairs} budget @ {H}x{W} "
                 f"TILE={TILE} cutoff={cutoff} N={N}. Route large splats through the low-res (octave) pass "
                 f"instead of culling at full res. Refusing to allocate.")
-    gid_b, starts_b = [], []
+    gid_b, starts_b, psplat_b, pinv_b = [], [], [], []
     for b in range(B):
         tot = tots[b]
         gid = torch.empty(max(tot, 1), dtype=torch.int32, device=dev)
         starts = torch.empty(nt + 1, dtype=torch.int32, device=dev)
+        psplat = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
+        pinv = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
         ws2 = _ws(lib.splat_bin_pairs_workspace_bytes(N, nt, tot), dev)
         check(lib.splat_bin_pairs(ptr(rect_b[b]), ptr(off_b[b]), N, H, W, TILE, tot, ptr(gid), ptr(starts),
-                                  ptr(ws2), ws2.numel(), stream), "splat_bin_pairs")
-        gid_b.append(gid); starts_b.append(starts)
-    return TileBins(rec_b, gid_b, starts_b, tots, H, W, TILE, ntx, nt)
+                                  ptr(psplat), ptr(pinv), ptr(ws2), ws2.numel(), stream), "splat_bin_pairs")
+        gid_b.append(gid); starts_b.append(starts); psplat_b.append(psplat); pinv_b.append(pinv)
+    return TileBins(rec_b, gid_b, starts_b, tots, H, W, TILE, ntx, nt, off_b, psplat_b, pinv_b)
 
 
 def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
@@ -156,7 +162,7 @@ def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
     B, N, _ = mu.shape
     dummy_col = torch.zeros((B, N, 1), device=mu.device)
     dummy_op = torch.zeros((B, N), device=mu.device)
-    return _bin(mu, scale, dummy_col, dummy_op, None, H, W, TILE, cutoff, max_pairs).as_tuple()
+    return _bin(mu, scale, dummy_col, dummy_op, None, H, W, TILE, cutoff, max_pairs, with_maps=False).as_tuple()
 
 
 # ----------------------------------------------------------------------------------------------- cull path
@@ -212,11 +218,12 @@ def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, 
     g_bg = _empty((B, C), dev)
     go, bgf = _f32(grad_out), _f32(bg)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
-    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE), dev)
+    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE, max(bins.tot_b)), dev)
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
         ev = kernel_timer.record("bwd")
-        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), N, C, H, W, TILE,
+        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), ptr(bins.off_b[b]),
+                                   ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), bins.tot_b[b], N, C, H, W, TILE,
                                    flags, ptr(bgf[b]), ptr(T[b]), ptr(asum[b]), ptr(fg[b]), ptr(go[b]), None, None,
                                    None, ptr(g_mu[b]), ptr(g_scale[b]), None if g_th is None else ptr(g_th[b]),
                                    ptr(g_op[b]), ptr(g_col[b]), ptr(g_bg[b]), ptr(ws), ws.numel(), stream),
@@ -235,10 +242,11 @@ def _backward_cull_fields(dS_log, dS_a, dS_ac, mu, scale, color, opacity, theta,
         return g_mu, g_scale, g_col, g_op, g_th
     dl, da, dc = _f32(dS_log), _f32(dS_a), _f32(dS_ac)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
-    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE), dev)
+    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE, max(bins.tot_b)), dev)
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     for b in range(B):
-        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), N, C, H, W, TILE,
+        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), ptr(bins.off_b[b]),
+                                   ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), bins.tot_b[b], N, C, H, W, TILE,
                                    flags, None, None, None, None, None, ptr(dl[b]), ptr(da[b]), ptr(dc[b]),
                                    ptr(g_mu[b]), ptr(g_scale[b]), None if g_th is None else ptr(g_th[b]),
                                    ptr(g_op[b]), ptr(g_col[b]), None, ptr(ws), ws.numel(), stream),

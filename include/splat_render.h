@@ -48,10 +48,14 @@ int splat_bin_count(const float *mu, const float *scale, const float *theta, con
 /* Binning phase 2: expand rects into pairs, stable radix sort on the tile id, CSR tile starts.
  * gid_sorted[max(tot,1)] lists splat ids ordered by (tile, splat id); tile_starts[nt+1].
  * tot == 0 gives gid_sorted = {0} and all-zero starts, as the reference does.
+ * Optional (NULL skips) maps over the splat-major pair order q (splat g owns q in [offsets[g], offsets[g+1])),
+ * used by the backward's per-splat reduction: pair_splat[tot] = splat of q, pair_inv[tot] = sorted position
+ * of q.
  * Replaces render_triton.py:392-409. */
 size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot);
 int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, int TILE, long long tot,
-                    int *gid_sorted, int *tile_starts, void *ws, size_t ws_bytes, void *stream);
+                    int *gid_sorted, int *tile_starts, int *pair_splat, int *pair_inv, void *ws,
+                    size_t ws_bytes, void *stream);
 
 /* Per-tile forward compositing over the binned pairs (TILE in {4, 8, 16}).
  * Composite (flags without FIELDS): out[P,C], T[P], asum[P], fg[P,C] with background bg[C].
@@ -61,19 +65,21 @@ int splat_render_fwd(const float *rec, const int *gid_sorted, const int *tile_st
                      int TILE, int flags, const float *bg, float *out, float *T, float *asum, float *fg,
                      float *slog, float *sa, float *sac, void *stream);
 
-/* Backward over the same pairs: gradients for every splat parameter, written (not accumulated).
+/* Backward over the same pairs: gradients for every splat parameter, written (not accumulated), with no
+ * global atomics (deterministic). Takes the binning's offsets, pair_splat and pair_inv.
  * Composite: upstream gout[P,C] with the forward's T, asum, fg and bg; g_bg[C] optional (NULL skips).
  * FIELDS: upstream dslog[P], dsa[P], dsac[P,C]; no g_bg.
  * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
  * g_op[N], g_color[N,C].
  * Replaces _render_bwd_cull_kernel + the index_add_ scatter and g_bg reduction,
  * render_triton.py:602-720 and :723-810. */
-size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE);
-int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, int N, int C, int H,
-                     int W, int TILE, int flags, const float *bg, const float *T, const float *asum,
-                     const float *fg, const float *gout, const float *dslog, const float *dsa,
-                     const float *dsac, float *g_mu, float *g_scale, float *g_theta, float *g_op,
-                     float *g_color, float *g_bg, void *ws, size_t ws_bytes, void *stream);
+size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE, long long tot);
+int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, const int *offsets,
+                     const int *pair_splat, const int *pair_inv, long long tot, int N, int C, int H, int W,
+                     int TILE, int flags, const float *bg, const float *T, const float *asum, const float *fg,
+                     const float *gout, const float *dslog, const float *dsa, const float *dsac,
+                     float *g_mu, float *g_scale, float *g_theta, float *g_op, float *g_color, float *g_bg,
+                     void *ws, size_t ws_bytes, void *stream);
 
 /* Exact (unculled) path: every pixel sums every splat; pixel centres py[P], px[P] supplied by the caller.
  * Replaces _render_fwd_kernel / _render_bwd_kernel and their wrappers, render_triton.py:58-303. */
