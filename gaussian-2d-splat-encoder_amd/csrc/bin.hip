@@ -145,8 +145,8 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, c
 }
 
 // ----------------------------------------------------------------------------------------------------
-// pair expansion: pair p belongs to the last splat g with offsets[g] <= p; its k = p - offsets[g] walks
-// the splat's rect row-major (render_triton.py:400-404).
+// pair expansion (render_triton.py:396-404): pair p belongs to the last splat g with offsets[g] <= p, and
+// k = p - offsets[g] walks that splat's rect row by row.
 __device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi, int p) {
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -155,52 +155,96 @@ __device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi
   return lo;
 }
 
-// keys[p] = tile of splat-major pair p. With `pair_splat` set (radix passes follow), vals[p] = p and
-// pair_splat[p] = its splat; otherwise (single-tile grid, no pass) vals[p] = splat is already the final
-// list and inv[p] = p.
+// Exclusive prefix of `v` over a 256-thread block (4 waves) with op = sum (MAX = false) or max (MAX = true,
+// identity -1). Returns the block total / maximum in `total`. Every thread must call it.
+template <bool MAX>
+__device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc = MAX ? max(inc, o) : inc + o;
+  }
+  if (lane == 63) s_w[wv] = inc;
+  __syncthreads();
+  int pre = MAX ? -1 : 0, tot = MAX ? -1 : 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int x = s_w[w];
+    if (w < wv) pre = MAX ? max(pre, x) : pre + x;
+    tot = MAX ? max(tot, x) : tot + x;
+  }
+  int ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = MAX ? -1 : 0;
+  total = tot;
+  __syncthreads();
+  return MAX ? max(pre, ex) : pre + ex;
+}
+
+// Block = 4096 consecutive pairs. Each splat with pairs in the block marks its first pair there with its
+// id; an inclusive max-scan over the block then gives every pair its owner (splat ids grow with p).
+// Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat (optional) and, with `hist` set, the
+// block's histogram of the first radix digit.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
                                                           int N, int ntx, int tot, int dmask, int* __restrict__ keys,
                                                           int* __restrict__ vals, int* __restrict__ pair_splat,
-                                                          int* __restrict__ inv, int* __restrict__ hist, int nblocks) {
-  __shared__ int s_off[kSortKeys + 1];
+                                                          int* __restrict__ hist, int nblocks) {
+  __shared__ int4 s_own4[kSortKeys / 4];
   __shared__ int s_hist[256];
+  __shared__ int s_w[kWaves];
   __shared__ int s_rng[2];
+  int* s_own = reinterpret_cast<int*>(s_own4);
   const int p_base = blockIdx.x * kSortKeys;
-  const int p_last = min(p_base + kSortKeys, tot) - 1;
+  const int n_here = min(kSortKeys, tot - p_base);
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
+  for (int i = threadIdx.x; i < kSortKeys / 4; i += kBlock) s_own4[i] = make_int4(-1, -1, -1, -1);
   if (threadIdx.x == 0) {
     s_rng[0] = last_le(offsets, 0, N - 1, p_base);
-    s_rng[1] = last_le(offsets, 0, N - 1, p_last);
+    s_rng[1] = last_le(offsets, 0, N - 1, p_base + n_here - 1);
   }
   __syncthreads();
   const int glo = s_rng[0], ghi = s_rng[1];
-  const int nwin = ghi - glo + 1;
-  const bool in_lds = nwin <= kSortKeys;
-  if (in_lds)
-    for (int i = threadIdx.x; i <= nwin; i += kBlock) s_off[i] = offsets[glo + i];
+  for (int g = glo + (int)threadIdx.x; g <= ghi; g += kBlock) {
+    const int o0 = offsets[g], o1 = offsets[g + 1];
+    if (o1 > o0) atomicMax(&s_own[max(o0, p_base) - p_base], g);   // o0 <= offsets[ghi] <= last pair here
+  }
+  __syncthreads();
+  {
+    // thread t scans entries [16 t, 16 t + 16)
+    int loc[16];
+    int run = -1;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int4 x = s_own4[threadIdx.x * 4 + k4];
+      run = max(run, x.x); loc[4 * k4 + 0] = run;
+      run = max(run, x.y); loc[4 * k4 + 1] = run;
+      run = max(run, x.z); loc[4 * k4 + 2] = run;
+      run = max(run, x.w); loc[4 * k4 + 3] = run;
+    }
+    int total;
+    const int ex = block256_excl<true>(run, s_w, total);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+      s_own4[threadIdx.x * 4 + k4] = make_int4(max(loc[4 * k4], ex), max(loc[4 * k4 + 1], ex),
+                                               max(loc[4 * k4 + 2], ex), max(loc[4 * k4 + 3], ex));
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll 4
   for (int j = 0; j < kItems; ++j) {
-    const int p = p_base + wv * kWaveKeys + j * 64 + lane;
-    if (p > p_last) continue;
-    int w0, o;
-    if (in_lds) { w0 = last_le(s_off, 0, nwin - 1, p); o = s_off[w0]; }
-    else { w0 = last_le(offsets + glo, 0, nwin - 1, p); o = offsets[glo + w0]; }
-    const int g = glo + w0;
-    const int k = p - o;
+    const int i = wv * kWaveKeys + j * 64 + lane;
+    if (i >= n_here) continue;
+    const int p = p_base + i;
+    const int g = s_own[i];
+    const int k = p - offsets[g];
     const int4 rc = rect[g];
     const int ky = k / rc.z;
     const int kx = k - ky * rc.z;
     const int tile = (rc.y + ky) * ntx + rc.x + kx;
     keys[p] = tile;
-    if (pair_splat) {
-      vals[p] = p;
-      pair_splat[p] = g;
-    } else {
-      vals[p] = g;
-      if (inv) inv[p] = p;
-    }
+    vals[p] = g;
+    if (pair_splat) pair_splat[p] = g;
     if (hist) atomicAdd(&s_hist[tile & dmask], 1);
   }
   if (!hist) return;
@@ -222,23 +266,51 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ k
   for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
 }
 
+// Workgroup d scans histogram row d (the counts of digit d in every block) in place into exclusive
+// per-block offsets within the digit, and stores the digit's total in rowtot[d].
+__global__ __launch_bounds__(kBlock) void k_hist_row_scan(int* __restrict__ hist, int nblocks, int* __restrict__ rowtot) {
+  __shared__ int s_w[kWaves];
+  int* row = hist + (size_t)blockIdx.x * nblocks;
+  int carry = 0;
+  for (int base = 0; base < nblocks; base += kBlock * 8) {
+    const int i0 = base + threadIdx.x * 8;
+    int v[8], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { v[k] = i0 + k < nblocks ? row[i0 + k] : 0; sum += v[k]; }
+    int total;
+    int run = carry + block256_excl<false>(sum, s_w, total);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (i0 + k < nblocks) row[i0 + k] = run;
+      run += v[k];
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0) rowtot[blockIdx.x] = carry;
+}
+
 // Stable scatter of one radix pass. Wave w of the block owns keys [base + w*1024, base + (w+1)*1024) and
 // walks them 64 at a time in index order; lanes holding the same digit are ranked among themselves with
 // ballots (lane order = index order), on top of the wave's running count for that digit. Wave counts are
-// then prefixed across the waves, and the block's base for each digit comes from the scanned histogram.
-// On the final pass (`pair_splat` set) the carried splat-major position v becomes the splat id
-// pair_splat[v] in the output, and inv[v] receives the pair's sorted position.
+// then prefixed across the waves; the block's base for a digit is the digit's global start (prefix of the
+// row totals) plus the block's offset within the digit (the row-scanned histogram).
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
                                                           int tot, int shift, int dbits, const int* __restrict__ hist_scan,
-                                                          int nblocks, int* __restrict__ keys_out,
-                                                          int* __restrict__ vals_out,
-                                                          const int* __restrict__ pair_splat, int* __restrict__ inv) {
+                                                          const int* __restrict__ rowtot, int nblocks,
+                                                          int* __restrict__ keys_out, int* __restrict__ vals_out) {
   __shared__ int s_cnt[kWaves][256];
   __shared__ int s_base[256];
+  __shared__ int s_w[kWaves];
   const int dmask = (1 << dbits) - 1;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < kWaves * 256; i += kBlock) (&s_cnt[0][0])[i] = 0;
-  for (int d = threadIdx.x; d <= dmask; d += kBlock) s_base[d] = hist_scan[d * nblocks + blockIdx.x];
+  {
+    const int d = threadIdx.x;   // kBlock == 256 >= radix
+    const int rt = d <= dmask ? rowtot[d] : 0;
+    int total;
+    const int dstart = block256_excl<false>(rt, s_w, total);
+    if (d <= dmask) s_base[d] = dstart + hist_scan[d * nblocks + blockIdx.x];
+  }
   __syncthreads();
   const unsigned long long lt = (1ull << lane) - 1ull;
   const int p0 = blockIdx.x * kSortKeys + wv * kWaveKeys + lane;
@@ -277,91 +349,17 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     const int d = (key[j] >> shift) & dmask;
     const int pos = s_cnt[wv][d] + rank[j];
     keys_out[pos] = key[j];
-    if (pair_splat) {
-      vals_out[pos] = pair_splat[val[j]];
-      if (inv) inv[val[j]] = pos;
-    } else {
-      vals_out[pos] = val[j];
-    }
+    vals_out[pos] = val[j];
   }
 }
 
-// ----------------------------------------------------------------------------------------------------
-// Exclusive scan of int32, used for the radix histograms (digit-major, so the scan yields each
-// (digit, block) its global base).
-constexpr int kScanItems = 4;
-constexpr int kScanBlock = 1024;
-constexpr int kScanChunk = kScanBlock * kScanItems;
-
-__device__ __forceinline__ int block_excl_scan_1024(int v, int* s_w, int& total) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int inc = wave_incl_scan(v, lane);
-  if (lane == 63) s_w[wv] = inc;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    int x = s_w[threadIdx.x];
-    for (int d = 1; d < 16; d <<= 1) {
-      int o = __shfl_up(x, d, 64);
-      if ((int)threadIdx.x >= d) x += o;
-    }
-    s_w[threadIdx.x] = x;
-  }
-  __syncthreads();
-  const int excl = (wv ? s_w[wv - 1] : 0) + inc - v;
-  total = s_w[15];
-  __syncthreads();
-  return excl;
-}
-
-// One workgroup scans a whole array (chunks of 4096 with a running carry), or with `partial` set, each
-// workgroup scans its 4096-chunk and adds partial[blockIdx].
-__global__ __launch_bounds__(kScanBlock) void k_scan_chunks(int* __restrict__ a, int n, const int* __restrict__ partial,
-                                                            int whole) {
-  __shared__ int s_w[16];
-  int carry = partial ? partial[blockIdx.x] : 0;
-  const int first = whole ? 0 : blockIdx.x * kScanChunk;
-  const int last = whole ? n : min(n, first + kScanChunk);
-  for (int base = first; base < last; base += kScanChunk) {
-    const int i0 = base + threadIdx.x * kScanItems;
-    int v[kScanItems], s = 0;
-#pragma unroll
-    for (int k = 0; k < kScanItems; ++k) { v[k] = (i0 + k < last) ? a[i0 + k] : 0; s += v[k]; }
-    int total;
-    int run = carry + block_excl_scan_1024(s, s_w, total);
-#pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-      if (i0 + k < last) a[i0 + k] = run;
-      run += v[k];
-    }
-    carry += total;
-  }
-}
-
-__global__ __launch_bounds__(kScanBlock) void k_scan_reduce(const int* __restrict__ a, int n, int* __restrict__ partial) {
-  __shared__ int s_w[16];
-  const int i0 = blockIdx.x * kScanChunk + threadIdx.x * kScanItems;
-  int s = 0;
-#pragma unroll
-  for (int k = 0; k < kScanItems; ++k) s += (i0 + k < n) ? a[i0 + k] : 0;
-  int total;
-  block_excl_scan_1024(s, s_w, total);
-  if (threadIdx.x == 0) partial[blockIdx.x] = total;
-}
-
-static int scan_exclusive(int* a, int n, int* partial, hipStream_t st) {
-  if (n <= 16 * kScanChunk) {
-    k_scan_chunks<<<1, kScanBlock, 0, st>>>(a, n, nullptr, 1);
-    return check_launch("k_scan_chunks");
-  }
-  const int nb = div_up(n, kScanChunk);
-  k_scan_reduce<<<nb, kScanBlock, 0, st>>>(a, n, partial);
-  k_scan_chunks<<<1, kScanBlock, 0, st>>>(partial, nb, nullptr, 1);
-  k_scan_chunks<<<nb, kScanBlock, 0, st>>>(a, n, partial, 0);
-  return check_launch("scan_exclusive");
-}
-
-// starts[t] = number of pairs with tile < t, from the sorted tile ids.
-__global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ keys, int tot, int nt, int* __restrict__ starts) {
+// From the sorted (tile, splat) list: CSR starts (starts[t] = number of pairs with tile < t,
+// render_triton.py:408) and, optionally, the inverse permutation inv[q] = sorted position of splat-major
+// pair q, where q = offsets[g] + (ty - ty0) * w + (tx - tx0) is the pair's index in its splat's rect walk.
+__global__ __launch_bounds__(kBlock) void k_tile_starts_inv(const int* __restrict__ keys, const int* __restrict__ gids,
+                                                            int tot, int nt, int ntx, const int4* __restrict__ rect,
+                                                            const int* __restrict__ offsets, int* __restrict__ starts,
+                                                            int* __restrict__ inv) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= tot) return;
   const int k = keys[i];
@@ -369,11 +367,12 @@ __global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ 
   for (int t = prev + 1; t <= k; ++t) starts[t] = i;
   if (i == tot - 1)
     for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
-}
-
-__global__ void k_copy_i32(const int* __restrict__ src, int* __restrict__ dst, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) dst[i] = src[i];
+  if (inv) {
+    const int g = gids[i];
+    const int4 rc = rect[g];
+    const int ty = k / ntx, tx = k - ty * ntx;
+    inv[offsets[g] + (ty - rc.y) * rc.z + (tx - rc.x)] = i;
+  }
 }
 
 __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
@@ -385,8 +384,8 @@ __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct PairsPlan {
-  int nblk, passes, dbits, radix, nscan_part;
-  size_t off_keys_a, off_keys_b, off_vals_b, off_psplat, off_hist, off_part, total;
+  int nblk, passes, dbits, radix;
+  size_t off_keys_a, off_keys_b, off_vals_b, off_hist, off_rowtot, total;
 };
 
 static PairsPlan plan_pairs(int nt, long long tot) {
@@ -398,14 +397,12 @@ static PairsPlan plan_pairs(int nt, long long tot) {
   p.dbits = p.passes ? (nbits + p.passes - 1) / p.passes : 0;
   p.radix = 1 << p.dbits;
   const long long nh = (long long)p.radix * p.nblk;
-  p.nscan_part = div_up(nh > 0 ? nh : 1, kScanChunk);
   size_t o = 0;
   p.off_keys_a = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_keys_b = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_vals_b = o; o += align256(sizeof(int) * (size_t)tot);
-  p.off_psplat = o; o += align256(sizeof(int) * (size_t)tot);
   p.off_hist = o;   o += align256(sizeof(int) * (size_t)(nh > 0 ? nh : 1));
-  p.off_part = o;   o += align256(sizeof(int) * (size_t)p.nscan_part);
+  p.off_rowtot = o; o += align256(sizeof(int) * 256);
   p.total = o;
   return p;
 }
@@ -482,38 +479,35 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
   int* keys_a = (int*)(base + pl.off_keys_a);
   int* keys_b = (int*)(base + pl.off_keys_b);
   int* vals_b = (int*)(base + pl.off_vals_b);
-  int* psplat = pair_splat ? pair_splat : (int*)(base + pl.off_psplat);
   int* hist = (int*)(base + pl.off_hist);
-  int* part = (int*)(base + pl.off_part);
+  int* rowtot = (int*)(base + pl.off_rowtot);
+  // Pass k reads buffer k % 2 and writes (k + 1) % 2, so the final pass lands in buffer `fin`; with no
+  // pass the scatter's own output (buffer 0 = fin) is final.
   const int fin = pl.passes & 1;
   int* K[2];
   int* V[2];
-  // Pass k reads buffer k % 2 and writes (k + 1) % 2, so the final pass lands in buffer `fin`; with no
-  // pass the scatter's own output (buffer 0 = fin) is final.
   K[fin] = keys_a; K[1 - fin] = keys_b;
   V[fin] = gid_sorted; V[1 - fin] = vals_b;
   const int t = (int)tot;
   const int dmask = pl.radix - 1;
   k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, ntx, t, dmask, K[0], V[0],
-                                              pl.passes ? psplat : nullptr, pair_inv, pl.passes ? hist : nullptr,
-                                              pl.nblk);
+                                              pair_splat, pl.passes ? hist : nullptr, pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
-  if (pl.passes == 0 && pair_splat) k_copy_i32<<<div_up(t, 256), 256, 0, st>>>(gid_sorted, pair_splat, t);
   for (int pass = 0; pass < pl.passes; ++pass) {
     const int shift = pass * pl.dbits;
     const int src = pass & 1, dst = 1 - src;
-    const bool last = pass == pl.passes - 1;
     if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], t, shift, dmask, hist, pl.nblk);
-    rc = scan_exclusive(hist, pl.radix * pl.nblk, part, st);
-    if (rc) return rc;
-    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, pl.nblk, K[dst], V[dst],
-                                                last ? psplat : nullptr, last ? pair_inv : nullptr);
+    k_hist_row_scan<<<pl.radix, kBlock, 0, st>>>(hist, pl.nblk, rowtot);
+    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, rowtot, pl.nblk, K[dst],
+                                                V[dst]);
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
   }
-  k_tile_starts<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], t, nt, tile_starts);
-  return check_launch("k_tile_starts");
+  k_tile_starts_inv<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, ntx,
+                                                          reinterpret_cast<const int4*>(rect), offsets, tile_starts,
+                                                          pair_inv);
+  return check_launch("k_tile_starts_inv");
 }
 
 }  // extern "C"

@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const float v = wave_sum(bgp[c]);
-      if (lane == 0) bg_part[(size_t)t * C + c] = v;
+      if (lane == 0) bg_part[(size_t)c * nt + t] = v;
     }
   }
   __syncthreads();
@@ -370,30 +370,13 @@ __global__ __launch_bounds__(256) void k_pair_reduce(const float* __restrict__ r
 }
 
 // Splats whose pairs span waves c0..c1 of k_pair_reduce: plast[c0] + pfirst[c0+1..c1], in order. Splats with
-// no pair get zero gradients. With g_bg set, the last workgroup also reduces the per-tile g_bg partials.
+// no pair get zero gradients.
 template <int C>
 __global__ __launch_bounds__(256) void k_reduce_fixup(const float* __restrict__ rec, const int* __restrict__ offsets,
                                                       int N, const float* __restrict__ pfirst,
                                                       const float* __restrict__ plast, float* __restrict__ g_mu,
                                                       float* __restrict__ g_scale, float* __restrict__ g_theta,
-                                                      float* __restrict__ g_op, float* __restrict__ g_col,
-                                                      const float* __restrict__ bg_part, int nparts,
-                                                      float* __restrict__ g_bg) {
-  if ((int)blockIdx.x >= (N + 255) / 256) {
-    __shared__ float s_w[4][kMaxC];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      float x = 0.f;
-      for (int i = threadIdx.x; i < nparts; i += 256) x += bg_part[(size_t)i * C + c];
-      x = wave_sum(x);
-      if (lane == 0) s_w[wv][c] = x;
-    }
-    __syncthreads();
-    if (threadIdx.x < C)
-      g_bg[threadIdx.x] = (s_w[0][threadIdx.x] + s_w[1][threadIdx.x]) + (s_w[2][threadIdx.x] + s_w[3][threadIdx.x]);
-    return;
-  }
+                                                      float* __restrict__ g_op, float* __restrict__ g_col) {
   const int g = blockIdx.x * 256 + threadIdx.x;
   if (g >= N) return;
   const int qs = offsets[g], qe = offsets[g + 1];
@@ -470,33 +453,41 @@ __global__ __launch_bounds__(256) void k_bg_partial(const float* __restrict__ go
     if (lane == 0) s_w[wv][c] = v;
   }
   __syncthreads();
-  if (threadIdx.x < C) part[(size_t)blockIdx.x * C + threadIdx.x] = s_w[0][threadIdx.x] + s_w[1][threadIdx.x] +
-                                                                     s_w[2][threadIdx.x] + s_w[3][threadIdx.x];
+  if (threadIdx.x < C) part[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = s_w[0][threadIdx.x] + s_w[1][threadIdx.x] +
+                                                                             s_w[2][threadIdx.x] + s_w[3][threadIdx.x];
 }
 
-// Exact path: per-splat sums (stride kAcc) -> parameter gradients. With g_bg set, the last workgroup also
-// reduces the nparts per-chunk partials of sum_p gout * T.
+// g_bg[c] = sum of the nparts channel-major partials part[c * nparts + i], one 1024-thread workgroup.
+template <int C>
+__global__ __launch_bounds__(1024) void k_bg_sum(const float* __restrict__ part, int nparts, float* __restrict__ g_bg) {
+  __shared__ float s_w[16][kMaxC];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float* row = part + (size_t)c * nparts;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int i = threadIdx.x;
+    for (; i + 3 * 1024 < nparts; i += 4 * 1024) {
+      a0 += row[i]; a1 += row[i + 1024]; a2 += row[i + 2048]; a3 += row[i + 3072];
+    }
+    for (; i < nparts; i += 1024) a0 += row[i];
+    const float x = wave_sum((a0 + a1) + (a2 + a3));
+    if (lane == 0) s_w[wv][c] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < C) {
+    float x = 0.f;
+    for (int w = 0; w < 16; ++w) x += s_w[w][threadIdx.x];
+    g_bg[threadIdx.x] = x;
+  }
+}
+
+// Exact path: per-splat sums (stride kAcc) -> parameter gradients.
 template <int C>
 __global__ __launch_bounds__(256) void k_acc_finalize(const float* __restrict__ rec, const float* __restrict__ acc, int N,
                                                       float* __restrict__ g_mu, float* __restrict__ g_scale,
                                                       float* __restrict__ g_theta, float* __restrict__ g_op,
-                                                      float* __restrict__ g_col, const float* __restrict__ bg_part,
-                                                      int nparts, float* __restrict__ g_bg) {
-  if ((int)blockIdx.x >= (N + 255) / 256) {
-    __shared__ float s_w[4][kMaxC];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      float x = 0.f;
-      for (int i = threadIdx.x; i < nparts; i += 256) x += bg_part[(size_t)i * C + c];
-      x = wave_sum(x);
-      if (lane == 0) s_w[wv][c] = x;
-    }
-    __syncthreads();
-    if (threadIdx.x < C)
-      g_bg[threadIdx.x] = (s_w[0][threadIdx.x] + s_w[1][threadIdx.x]) + (s_w[2][threadIdx.x] + s_w[3][threadIdx.x]);
-    return;
-  }
+                                                      float* __restrict__ g_col) {
   const int g = blockIdx.x * 256 + threadIdx.x;
   if (g >= N) return;
   float v[kSums];
@@ -628,10 +619,9 @@ int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_st
         if (t > 0)
           k_pair_reduce<CC><<<(pl.nchunk + 3) / 4, 256, 0, st>>>(rec, psum, pair_splat, pair_inv, offsets, t, g_mu,
                                                                  g_scale, g_theta, g_op, g_color, pfirst, plast);
-        const int nbs = (N + 255) / 256;
-        k_reduce_fixup<CC><<<nbs + (want_bg ? 1 : 0), 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale,
-                                                                    g_theta, g_op, g_color, bg_part, nt,
-                                                                    want_bg ? g_bg : nullptr);
+        k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta,
+                                                            g_op, g_color);
+        if (want_bg) k_bg_sum<CC><<<1, 1024, 0, st>>>(bg_part, nt, g_bg);
         return check_launch("splat_render_bwd");
       });
     });
@@ -668,9 +658,11 @@ int splat_exact_bwd(const float* rec, int N, int C, const float* py, const float
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
     k_bwd_exact<CC><<<(N + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, T, asum, fg, gout, acc);
-    if (g_bg) k_bg_partial<CC><<<nchunk, 256, 0, st>>>(gout, T, P, part);
-    k_acc_finalize<CC><<<(N + 255) / 256 + (g_bg ? 1 : 0), 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op,
-                                                                         g_color, part, nchunk, g_bg);
+    if (g_bg) {
+      k_bg_partial<CC><<<nchunk, 256, 0, st>>>(gout, T, P, part);
+      k_bg_sum<CC><<<1, 1024, 0, st>>>(part, nchunk, g_bg);
+    }
+    k_acc_finalize<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op, g_color);
     return check_launch("splat_exact_bwd");
   });
 }
