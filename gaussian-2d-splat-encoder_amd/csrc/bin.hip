@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     float4* r = rec + (size_t)g * 4;
     r[0] = make_float4(m.x, m.y, cs * ky, sn * ky);
     const float op = opacity[g];
-    r[1] = make_float4(-sn * kx, cs * kx, op, 1.f - op);
+    r[1] = make_float4(-sn * kx, cs * kx, op, log2f(op));
     r[2] = col;
     r[3] = make_float4(s.x, s.y, cs, sn);
     if (do_bin) {

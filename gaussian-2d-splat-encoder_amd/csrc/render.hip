@@ -36,23 +36,43 @@ constexpr int kSums = 10;      // sums carried through the reduction
 
 __host__ __device__ constexpr int tile_threads(int tile) { return tile * tile > 64 ? tile * tile : 64; }
 
-// One pixel-pair of the forward sums.
+// One pixel-pair of the forward: accumulates the colour weight and its colour sums, returns 1 - a for the
+// caller's transmittance product. op * falloff = exp2(log2(op) - m) with m = u^2 + v^2.
 template <int C, bool ODDS>
-__device__ __forceinline__ void fwd_accumulate(const float* __restrict__ r, float py, float px, float& sl, float& s_a,
-                                               float* sc) {
+__device__ __forceinline__ float fwd_pair(const float* __restrict__ r, float py, float px, float& s_a, float* sc) {
   const float dy = py - r[R_GY], dx = px - r[R_GX];
   const float u = fmaf(r[R_A], dy, r[R_B] * dx);
   const float v = fmaf(r[R_CC], dy, r[R_D] * dx);
-  const float m = fmaf(u, u, v * v);
-  const float fo = r[R_OP] * hw_exp2(-m);
+  const float fo = hw_exp2(-fmaf(u, u, fmaf(v, v, -r[R_LOP])));
   const float a = fminf(fo, kClamp);
   float oma = 1.f - a;
-  if (ODDS) oma = one_minus_alpha(oma, fo, m, r[R_OP], r[R_1MOP]);
-  sl += hw_log2(oma);
+  if (ODDS) oma = one_minus_alpha(oma, fo, fmaf(u, u, v * v), r[R_OP], 1.f - r[R_OP]);
   const float w = ODDS ? a * hw_rcp(oma) : a;
   s_a += w;
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = fmaf(w, r[R_COL + c], sc[c]);
+  return oma;
+}
+
+// Forward sums of one pixel over pairs [i0, i1) of the tile's list. S_log is accumulated in log2 units as
+// log2 of the product of four (1 - a) factors at a time (each factor >= 1e-4, so the product stays a
+// normal float); the four splats' ids and records are loaded together ahead of their use.
+template <int C, bool ODDS>
+__device__ __forceinline__ void fwd_pixel(const float* __restrict__ rec, const int* __restrict__ gid, int i0, int i1,
+                                          float py, float px, float& sl, float& s_a, float* sc) {
+  int i = i0;
+  for (; i + 4 <= i1; i += 4) {
+    const float* r0 = rec + (size_t)gid[i] * kRec;
+    const float* r1 = rec + (size_t)gid[i + 1] * kRec;
+    const float* r2 = rec + (size_t)gid[i + 2] * kRec;
+    const float* r3 = rec + (size_t)gid[i + 3] * kRec;
+    const float t0 = fwd_pair<C, ODDS>(r0, py, px, s_a, sc);
+    const float t1 = fwd_pair<C, ODDS>(r1, py, px, s_a, sc);
+    const float t2 = fwd_pair<C, ODDS>(r2, py, px, s_a, sc);
+    const float t3 = fwd_pair<C, ODDS>(r3, py, px, s_a, sc);
+    sl += hw_log2((t0 * t1) * (t2 * t3));
+  }
+  for (; i < i1; ++i) sl += hw_log2(fwd_pair<C, ODDS>(rec + (size_t)gid[i] * kRec, py, px, s_a, sc));
 }
 
 template <int C>
@@ -88,10 +108,7 @@ __global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_cull(
   float sl = 0.f, s_a = 0.f, sc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = 0.f;
-  for (int i = g0; i < g1; ++i) {
-    const float* r = rec + (size_t)gid[i] * kRec;
-    fwd_accumulate<C, ODDS>(r, py, px, sl, s_a, sc);
-  }
+  fwd_pixel<C, ODDS>(rec, gid, g0, g1, py, px, sl, s_a, sc);
   if (!valid) return;
   const int p = yp * W + xp;
   if (FIELDS) {
@@ -117,7 +134,7 @@ __global__ __launch_bounds__(64) void k_fwd_exact(const float* __restrict__ rec,
   float sl = 0.f, s_a = 0.f, sc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = 0.f;
-  for (int g = 0; g < N; ++g) fwd_accumulate<C, false>(rec + (size_t)g * kRec, py, px, sl, s_a, sc);
+  for (int g = 0; g < N; ++g) sl += hw_log2(fwd_pair<C, false>(rec + (size_t)g * kRec, py, px, s_a, sc));
   if (valid) store_composite<C>(p, sl, s_a, sc, bg, out, Tout, asum_out, fg_out);
 }
 
@@ -163,11 +180,29 @@ struct PairSums {
   }
 };
 
-// Rest of one backward pixel-pair once the falloff f, alpha a and 1 / (1 - a) are known. GATED: some
-// lane may sit on the alpha clamp, where the gradient through alpha is zero (render_triton.py:686, 697).
-template <int C, bool ODDS, bool GATED>
-__device__ __forceinline__ void bwd_tail(float u, float v, float f, float a, float rr, bool live, const float4& col,
-                                         const float4& pa, const float4& pb, PairSums<C>& s) {
+// One pixel-pair of the backward, given whitened offsets u, v. Fast path: a = op * f (no lane of the wave
+// can be on the clamp while op * f <= kNearOpaque < 1 - 1e-4). When some lane of the wave is near-opaque,
+// a is clamped, 1 - a is evaluated as in one_minus_alpha, and the clamp gates the falloff that multiplies
+// da (render_triton.py:686, 697). The branch is wave-uniform; every lane of the wave must be executing.
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_px(float u, float v, float op, const float4& col, const float4& pa,
+                                       const float4& pb, PairSums<C>& s) {
+  const float m = fmaf(u, u, v * v);
+  const float f = hw_exp2(-m);
+  const float fo = op * f;
+  float a = fo, oma = 1.f - fo, fq = f;
+  if (__any(fo > kNearOpaque)) {
+    a = fminf(fo, kClamp);
+    const float x = m * kLn2;
+    float p = fmaf(x, 1.f / 120.f, -1.f / 24.f);
+    p = fmaf(p, x, 1.f / 6.f);
+    p = fmaf(p, x, -0.5f);
+    p = fmaf(p, x, 1.f);
+    const float acc = fmaxf(fmaf(op, p * x, 1.f - op), 1.f - kClamp);
+    oma = fo > kNearOpaque ? acc : oma;
+    fq = fo < kClamp ? f : 0.f;
+  }
+  const float rr = hw_rcp(oma);
   float ct = pa.z * col.x;
   if (C > 1) ct = fmaf(pa.w, col.y, ct);
   if (C > 2) ct = fmaf(pb.x, col.z, ct);
@@ -184,8 +219,7 @@ __device__ __forceinline__ void bwd_tail(float u, float v, float f, float a, flo
   if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
   if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
   if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
-  float q = da * f;
-  if (GATED) q = live ? q : 0.f;
+  const float q = da * fq;
   const float qu = q * u, qv = q * v;
   s.q += q;
   s.qu += qu;
@@ -195,29 +229,16 @@ __device__ __forceinline__ void bwd_tail(float u, float v, float f, float a, flo
   s.quv = fmaf(qu, v, s.quv);
 }
 
-// One pixel-pair of the backward, given whitened offsets u, v. Unless some lane of the wave is near-opaque
-// (op * f > kNearOpaque), no lane can be on the clamp and 1 - a = 1 - op * f is accurate: the fast path.
-// Otherwise 1 - a is evaluated as in one_minus_alpha and the clamp gate applies. The branch is
-// wave-uniform; every lane of the wave must be executing.
-template <int C, bool ODDS>
-__device__ __forceinline__ void bwd_accumulate(float u, float v, float op, float one_m_op, const float4& col,
-                                               const float4& pa, const float4& pb, PairSums<C>& s) {
-  const float m = fmaf(u, u, v * v);
-  const float f = hw_exp2(-m);
-  const float fo = op * f;
-  if (__any(fo > kNearOpaque)) {
-    const float a = fminf(fo, kClamp);
-    const float x = m * kLn2;
-    float p = fmaf(x, 1.f / 120.f, -1.f / 24.f);
-    p = fmaf(p, x, 1.f / 6.f);
-    p = fmaf(p, x, -0.5f);
-    p = fmaf(p, x, 1.f);
-    const float acc = fmaxf(fmaf(op, p * x, one_m_op), 1.f - kClamp);
-    const float oma = fo > kNearOpaque ? acc : 1.f - a;
-    bwd_tail<C, ODDS, true>(u, v, f, a, hw_rcp(oma), fo < kClamp, col, pa, pb, s);
-  } else {
-    bwd_tail<C, ODDS, false>(u, v, f, fo, hw_rcp(1.f - fo), true, col, pa, pb, s);
-  }
+template <int C>
+__device__ __forceinline__ void xor_reduce(PairSums<C>& s, int d) {
+  s.q += __shfl_xor(s.q, d, 64);
+  s.qu += __shfl_xor(s.qu, d, 64);
+  s.qv += __shfl_xor(s.qv, d, 64);
+  s.quu += __shfl_xor(s.quu, d, 64);
+  s.qvv += __shfl_xor(s.qvv, d, 64);
+  s.quv += __shfl_xor(s.quv, d, 64);
+#pragma unroll
+  for (int c = 0; c < C; ++c) s.gc[c] += __shfl_xor(s.gc[c], d, 64);
 }
 
 template <int C>
@@ -251,7 +272,7 @@ __device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec
 }
 
 template <int C, bool FIELDS, bool ODDS, int TILE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_bwd_cull(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
     int nt, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, const float* __restrict__ dslog,
@@ -286,13 +307,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
   }
   __syncthreads();
   const int g0 = starts[t], g1 = starts[t + 1];
-  for (int i0 = g0; i0 < g1; i0 += 64) {
+  const int n = g1 - g0;
+  // full chunks: lane = pair, every pixel of the tile, row / column terms factored out of u and v
+  for (int i0 = g0; i0 + 64 <= g1; i0 += 64) {
     const int i = i0 + lane;
-    const bool act = i < g1;
-    const int g = act ? gid[i] : 0;
+    const int g = gid[i];
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z, omo = r1.w;
+    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
     float bdx[TILE], ddx[TILE];
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
@@ -309,10 +331,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
         const int l = yy * TILE + xx;
         const float4 pa = s_pa[l];
         const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-        bwd_accumulate<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, omo, col, pa, pb, s);
+        bwd_px<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, col, pa, pb, s);
       }
     }
-    if (act) store_pair<C>(psum + (size_t)i * kPairRec, s);
+    store_pair<C>(psum + (size_t)i * kPairRec, s);
+  }
+  // remainder of r < 64 pairs: L lanes per pair (largest power of two with r * L <= 64, L <= pixels),
+  // each lane covering NP / L consecutive pixels; the L partial sums are combined with xor shuffles.
+  const int r = n & 63;
+  if (r) {
+    int L = 1;
+    while (r * L * 2 <= 64 && L * 2 <= NP) L <<= 1;
+    const int pr = lane / L, sub = lane % L;
+    const bool act = pr < r;
+    const int i = g1 - r + pr;
+    const int g = act ? gid[i] : 0;
+    const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+    const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
+    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
+    const int npx = NP / L, j0 = sub * npx;
+    PairSums<C> s;
+    for (int jj = 0; jj < npx; ++jj) {
+      const int l = j0 + jj;
+      const float dy = s_py[l / TILE] - gy, dx = s_px[l % TILE] - gx;
+      const float4 pa = s_pa[l];
+      const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
+      bwd_px<C, ODDS>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, col, pa, pb, s);
+    }
+    for (int d = 1; d < L; d <<= 1) xor_reduce<C>(s, d);
+    if (act && sub == 0) store_pair<C>(psum + (size_t)i * kPairRec, s);
   }
 }
 
@@ -408,7 +455,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
   const int gs = g < N ? g : N - 1;
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)gs * 4;
   const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-  const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z, omo = r1.w;
+  const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
   PairSums<C> s;
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int p0 = 0; p0 < P; p0 += 64) {
@@ -428,7 +475,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
     for (int j = 0; j < np; ++j) {
       const float2 q = s_pyx[j];
       const float dy = q.x - gy, dx = q.y - gx;
-      bwd_accumulate<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, omo, col, s_pa[j],
+      bwd_px<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, col, s_pa[j],
                                C > 2 ? s_pb[j] : make_float4(0.f, 0.f, 0.f, 0.f), s);
     }
   }

@@ -13,13 +13,13 @@ namespace splat {
 //   2 A, 3 B, 4 Cc, 5 D        whitened rotation: u = A*dy + B*dx, v = Cc*dy + D*dx with
 //                              A = k*cos/sy, B = k*sin/sy, Cc = -k*sin/sx, D = k*cos/sx, k = kWhiten
 //   6 op                       opacity
-//   7 1 - op                   (exact for op >= 0.5, the only range it is used in)
+//   7 log2(op)                 (the forward evaluates op * falloff as exp2(log2(op) - m))
 //   8..11 colour               up to kMaxC channels
 //   12 sy, 13 sx, 14 cos, 15 sin   activated scale and rotation (backward only)
 constexpr int kRec = 16;
 constexpr int kMaxC = 4;
 enum RecSlot : int {
-  R_GY = 0, R_GX = 1, R_A = 2, R_B = 3, R_CC = 4, R_D = 5, R_OP = 6, R_1MOP = 7,
+  R_GY = 0, R_GX = 1, R_A = 2, R_B = 3, R_CC = 4, R_D = 5, R_OP = 6, R_LOP = 7,
   R_COL = 8, R_SY = 12, R_SX = 13, R_COS = 14, R_SIN = 15
 };
 
