@@ -60,6 +60,31 @@ def ppe_of(bins, H, W, TILE=8):
     return float((cnt * ph * pw).sum().item())
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (profiles/<kernel>_c2_traffic.md: a line `traffic_bytes_per_launch: <int>`), else None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_c2_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def copy_calibration(mib):
+    """A plain elementwise copy of `mib` MiB (reads and writes mib MiB), five launches: the known-size
+    kernel that scales FETCH_SIZE / WRITE_SIZE."""
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_mib": mib, "kernel": "vectorized_elementwise_kernel (mul)",
+                      "read_bytes": n * 4, "write_bytes": n * 4}), flush=True)
+
+
 def time_loop(fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -103,6 +128,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--odds", action="store_true", help="odds compositing instead of alpha")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a MIB-MiB copy kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -111,6 +138,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     dev = torch.device("cuda:0")
     s_cpu = synth.config("c2")
     s = s_cpu.to(dev)
@@ -168,6 +198,7 @@ def main():
     }
     dom = "bwd" if avg["bwd"] >= avg["fwd"] else "fwd"
     dk = kern[dom]
+    traffic = measured_traffic(f"k_{dom}_cull")
     mpix = P / 1e6
     line = {
         "metric": "render ms/frame + Mpix/s at 768x768, 92,160 splats (fwd, fwd+bwd); % roofline",
@@ -185,9 +216,9 @@ def main():
         "config": {"workload": "768x768 RGB, 92,160 splats, fwd+bwd, render_alpha_full_triton(cull=True, TILE=8, "
                                f"cutoff=3, odds={odds}); configs[2]",
                    "H": H, "W": W, "splats": N, "pairs": tot, "pixel_pairs": int(ppe)},
-        "roofline": {"bound": "valu", "kernel": f"k_{dom}_cull" + (" (+acc fill, finalize)" if dom == "bwd" else ""),
+        "roofline": {"bound": "valu", "kernel": f"k_{dom}_cull",
                      "achieved": round(dk["tflops"], 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(dk["tflops"] / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                     "frac": round(dk["tflops"] / PEAK_FP32_TFLOPS, 4), "traffic": traffic,
                      "flops_per_launch": fl_b if dom == "bwd" else fl_f, "avg_launch_ms": round(dk["ms"], 4),
                      "hbm_achieved_gbs": round(dk["gbs"], 1),
                      "hbm_frac": round(dk["gbs"] / PEAK_HBM_GBS, 4)},

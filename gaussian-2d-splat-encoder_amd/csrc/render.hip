@@ -605,73 +605,65 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
   });
 }
 
-struct BwdPlan {
-  size_t off_psum, off_first, off_last, off_bg, total;
-  int nchunk;
-};
-
-static BwdPlan plan_bwd(int C, int H, int W, int TILE, long long tot) {
-  BwdPlan b{};
-  const int t = TILE > 0 ? TILE : 1;
-  const size_t nt = (size_t)((W + t - 1) / t) * ((H + t - 1) / t);
-  const size_t np = tot > 0 ? (size_t)tot : 1;
-  b.nchunk = (int)((np + 63) / 64);
-  size_t o = 0;
-  b.off_psum = o; o += align256(sizeof(float) * kPairRec * np);
-  b.off_first = o; o += align256(sizeof(float) * kSums * (size_t)b.nchunk);
-  b.off_last = o; o += align256(sizeof(float) * kSums * (size_t)b.nchunk);
-  b.off_bg = o; o += align256(sizeof(float) * nt * (C > 0 ? C : 1));
-  b.total = o;
-  return b;
+static size_t reduce_ws_bytes(long long tot) {
+  const size_t nchunk = (size_t)((tot > 0 ? tot : 1) + 63) / 64;
+  return 2 * align256(sizeof(float) * kSums * nchunk);
 }
 
-size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE, long long tot) {
-  (void)N;
-  return plan_bwd(C, H, W, TILE, tot).total;
-}
+size_t splat_pair_sums_bytes(long long tot) { return sizeof(float) * kPairRec * (size_t)(tot > 0 ? tot : 1); }
 
-int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, const int* offsets,
-                     const int* pair_splat, const int* pair_inv, long long tot, int N, int C, int H, int W, int TILE,
-                     int flags, const float* bg, const float* T, const float* asum, const float* fg, const float* gout,
-                     const float* dslog, const float* dsa, const float* dsac, float* g_mu, float* g_scale,
-                     float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws, size_t ws_bytes,
-                     void* stream) {
-  if (N < 1 || H < 1 || W < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
-    return set_error(kInvalid, "splat_render_bwd: N=%d H=%d W=%d tot=%lld", N, H, W, tot);
-  if (!rec || !gid_sorted || !tile_starts || !offsets || !pair_splat || !pair_inv || !g_mu || !g_scale || !g_op ||
-      !g_color)
-    return set_error(kInvalid, "splat_render_bwd: null pointer");
+int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, long long tot, int C, int H,
+                     int W, int TILE, int flags, const float* bg, const float* T, const float* asum, const float* fg,
+                     const float* gout, const float* dslog, const float* dsa, const float* dsac, float* pair_sums,
+                     float* bg_part, void* stream) {
+  if (H < 1 || W < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
+    return set_error(kInvalid, "splat_render_bwd: H=%d W=%d tot=%lld", H, W, tot);
+  if (!rec || !gid_sorted || !tile_starts || !pair_sums) return set_error(kInvalid, "splat_render_bwd: null pointer");
   const bool fields = flags & kFlagFields;
   if (fields ? (!dslog || !dsa || !dsac) : (!bg || !T || !asum || !fg || !gout))
     return set_error(kInvalid, "splat_render_bwd: null upstream for flags=%d", flags);
-  const BwdPlan pl = plan_bwd(C, H, W, TILE, tot);
-  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_render_bwd: workspace %zu < %zu bytes", ws_bytes, pl.total);
+  if (fields && bg_part) return set_error(kInvalid, "splat_render_bwd: no background partials in FIELDS mode");
   hipStream_t st = (hipStream_t)stream;
-  char* base = (char*)ws;
-  float* psum = (float*)(base + pl.off_psum);
-  float* pfirst = (float*)(base + pl.off_first);
-  float* plast = (float*)(base + pl.off_last);
-  float* bg_part = (float*)(base + pl.off_bg);
-  const int t = (int)tot;
   return with_c(C, [&](auto cc) {
     return with_tile(TILE, [&](auto tt) {
       return with_flags(flags, [&](auto fl, auto od) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
         constexpr bool FL = decltype(fl)::value != 0;
         const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
-        const bool want_bg = !FL && g_bg;
         k_bwd_cull<CC, FL, decltype(od)::value != 0, TT><<<nt, 64, 0, st>>>(
-            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, psum,
-            want_bg ? bg_part : nullptr);
-        if (t > 0)
-          k_pair_reduce<CC><<<(pl.nchunk + 3) / 4, 256, 0, st>>>(rec, psum, pair_splat, pair_inv, offsets, t, g_mu,
-                                                                 g_scale, g_theta, g_op, g_color, pfirst, plast);
-        k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta,
-                                                            g_op, g_color);
-        if (want_bg) k_bg_sum<CC><<<1, 1024, 0, st>>>(bg_part, nt, g_bg);
-        return check_launch("splat_render_bwd");
+            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_sums, bg_part);
+        return check_launch("k_bwd_cull");
       });
     });
+  });
+}
+
+size_t splat_reduce_workspace_bytes(long long tot) { return reduce_ws_bytes(tot); }
+
+int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_splat, const int* pair_inv, long long tot,
+                       int N, int C, const float* pair_sums, const float* bg_part, int nparts, float* g_mu,
+                       float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws,
+                       size_t ws_bytes, void* stream) {
+  if (N < 1 || tot < 0 || tot > 0x7fffffffLL - 64) return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
+  if (!rec || !offsets || (tot > 0 && (!pair_splat || !pair_inv || !pair_sums)) || !g_mu || !g_scale || !g_op ||
+      !g_color || (g_bg && (!bg_part || nparts < 1)))
+    return set_error(kInvalid, "splat_reduce_pairs: null pointer");
+  if (ws_bytes < reduce_ws_bytes(tot)) return set_error(kWorkspace, "splat_reduce_pairs: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const size_t nchunk = (size_t)((tot > 0 ? tot : 1) + 63) / 64;
+  float* pfirst = (float*)ws;
+  float* plast = (float*)((char*)ws + align256(sizeof(float) * kSums * nchunk));
+  const int t = (int)tot;
+  return with_c(C, [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    if (t > 0)
+      k_pair_reduce<CC><<<(unsigned)((nchunk + 3) / 4), 256, 0, st>>>(rec, pair_sums, pair_splat, pair_inv, offsets, t,
+                                                                      g_mu, g_scale, g_theta, g_op, g_color, pfirst,
+                                                                      plast);
+    k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta, g_op,
+                                                        g_color);
+    if (g_bg) k_bg_sum<CC><<<1, 1024, 0, st>>>(bg_part, nparts, g_bg);
+    return check_launch("splat_reduce_pairs");
   });
 }
 

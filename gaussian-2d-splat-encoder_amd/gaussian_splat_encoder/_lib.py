@@ -30,9 +30,12 @@ _SIGS = {
     "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _LL]),
     "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
-    "splat_render_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _LL]),
-    "splat_render_bwd": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP, _VP,
-                              _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_pair_sums_bytes": (_SZ, [_LL]),
+    "splat_render_bwd": (_I, [_VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                              _VP, _VP, _VP]),
+    "splat_reduce_workspace_bytes": (_SZ, [_LL]),
+    "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP,
+                                _VP, _SZ, _VP]),
     "splat_exact_fwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_exact_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
     "splat_exact_bwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,

@@ -209,26 +209,41 @@ def _grads_out(B, N, C, dev, has_th):
             _empty((B, N), dev) if has_th else None)
 
 
+def _backward_pairs(bins, b, flags, C, H, W, TILE, upstream, grads, g_bg, lib, stream):
+    """Both backward steps for batch b: per-tile pair sums, then the per-splat reduction into `grads`."""
+    dev = bins.rec_b[b].device
+    tot = bins.tot_b[b]
+    N = bins.off_b[b].numel() - 1
+    sums = _empty((lib.splat_pair_sums_bytes(tot) // 4,), dev)
+    bg_part = _empty((C * bins.nt,), dev) if g_bg is not None else None
+    ev = kernel_timer.record("bwd")
+    check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), tot, C, H, W, TILE,
+                               flags, *[ptr(u) for u in upstream], ptr(sums), ptr(bg_part), stream),
+          "splat_render_bwd")
+    kernel_timer.close("bwd", ev)
+    ev = kernel_timer.record("reduce")
+    ws = _ws(lib.splat_reduce_workspace_bytes(tot), dev)
+    g_mu, g_scale, g_col, g_op, g_th = grads
+    check(lib.splat_reduce_pairs(ptr(bins.rec_b[b]), ptr(bins.off_b[b]), ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]),
+                                 tot, N, C, ptr(sums), ptr(bg_part), bins.nt, ptr(g_mu[b]), ptr(g_scale[b]),
+                                 None if g_th is None else ptr(g_th[b]), ptr(g_op[b]), ptr(g_col[b]), ptr(g_bg),
+                                 ptr(ws), ws.numel(), stream), "splat_reduce_pairs")
+    kernel_timer.close("reduce", ev)
+
+
 def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, bins, H, W, TILE=8, odds=False):
     """render_triton.py:723-765: grads for mu, scale, color, opacity, bg, theta (None without theta)."""
     B, N, C = color.shape
     dev = mu.device
-    has_th = theta is not None
-    g_mu, g_scale, g_col, g_op, g_th = _grads_out(B, N, C, dev, has_th)
+    grads = _grads_out(B, N, C, dev, theta is not None)
     g_bg = _empty((B, C), dev)
     go, bgf = _f32(grad_out), _f32(bg)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
-    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE, max(bins.tot_b)), dev)
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
-        ev = kernel_timer.record("bwd")
-        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), ptr(bins.off_b[b]),
-                                   ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), bins.tot_b[b], N, C, H, W, TILE,
-                                   flags, ptr(bgf[b]), ptr(T[b]), ptr(asum[b]), ptr(fg[b]), ptr(go[b]), None, None,
-                                   None, ptr(g_mu[b]), ptr(g_scale[b]), None if g_th is None else ptr(g_th[b]),
-                                   ptr(g_op[b]), ptr(g_col[b]), ptr(g_bg[b]), ptr(ws), ws.numel(), stream),
-              "splat_render_bwd")
-        kernel_timer.close("bwd", ev)
+        up = (bgf[b], T[b], asum[b], fg[b], go[b], None, None, None)
+        _backward_pairs(bins, b, flags, C, H, W, TILE, up, grads, g_bg[b], lib, stream)
+    g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
@@ -236,22 +251,16 @@ def _backward_cull_fields(dS_log, dS_a, dS_ac, mu, scale, color, opacity, theta,
     """render_triton.py:768-810: grads for mu, scale, color, opacity, theta from the fields' upstream grads."""
     B, N, C = color.shape
     dev = mu.device
-    has_th = theta is not None
-    g_mu, g_scale, g_col, g_op, g_th = _grads_out(B, N, C, dev, has_th)
+    grads = _grads_out(B, N, C, dev, theta is not None)
     if N == 0:
-        return g_mu, g_scale, g_col, g_op, g_th
+        return grads
     dl, da, dc = _f32(dS_log), _f32(dS_a), _f32(dS_ac)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
-    ws = _ws(lib.splat_render_bwd_workspace_bytes(N, C, H, W, TILE, max(bins.tot_b)), dev)
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     for b in range(B):
-        check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), ptr(bins.off_b[b]),
-                                   ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), bins.tot_b[b], N, C, H, W, TILE,
-                                   flags, None, None, None, None, None, ptr(dl[b]), ptr(da[b]), ptr(dc[b]),
-                                   ptr(g_mu[b]), ptr(g_scale[b]), None if g_th is None else ptr(g_th[b]),
-                                   ptr(g_op[b]), ptr(g_col[b]), None, ptr(ws), ws.numel(), stream),
-              "splat_render_bwd")
-    return g_mu, g_scale, g_col, g_op, g_th
+        up = (None, None, None, None, None, dl[b], da[b], dc[b])
+        _backward_pairs(bins, b, flags, C, H, W, TILE, up, grads, None, lib, stream)
+    return grads
 
 
 class _AlphaRenderCull(torch.autograd.Function):

@@ -65,21 +65,28 @@ int splat_render_fwd(const float *rec, const int *gid_sorted, const int *tile_st
                      int TILE, int flags, const float *bg, float *out, float *T, float *asum, float *fg,
                      float *slog, float *sa, float *sac, void *stream);
 
-/* Backward over the same pairs: gradients for every splat parameter, written (not accumulated), with no
- * global atomics (deterministic). Takes the binning's offsets, pair_splat and pair_inv.
- * Composite: upstream gout[P,C] with the forward's T, asum, fg and bg; g_bg[C] optional (NULL skips).
- * FIELDS: upstream dslog[P], dsa[P], dsac[P,C]; no g_bg.
+/* Backward, step 1: per-tile kernel over the same pairs. For every pair (sorted position i) it sums over
+ * the tile's pixels the terms the parameter gradients need and stores them in pair_sums[i] (12 floats,
+ * splat_pair_sums_bytes). Composite: upstream gout[P,C] with the forward's T, asum, fg and bg; with
+ * bg_part set ([C, nt] floats) it also writes per-tile partials of sum_p gout*T. FIELDS: upstream
+ * dslog[P], dsa[P], dsac[P,C] (bg_part must be NULL).
+ * Replaces _render_bwd_cull_kernel, render_triton.py:602-720 (per-pair grads, :612-614). */
+size_t splat_pair_sums_bytes(long long tot);
+int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, long long tot, int C,
+                     int H, int W, int TILE, int flags, const float *bg, const float *T, const float *asum,
+                     const float *fg, const float *gout, const float *dslog, const float *dsa,
+                     const float *dsac, float *pair_sums, float *bg_part, void *stream);
+
+/* Backward, step 2: per-splat reduction of the pair sums into parameter gradients, written (not
+ * accumulated), deterministic, no global atomics. Takes the binning's offsets, pair_splat and pair_inv.
  * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
- * g_op[N], g_color[N,C].
- * Replaces _render_bwd_cull_kernel + the index_add_ scatter and g_bg reduction,
- * render_triton.py:602-720 and :723-810. */
-size_t splat_render_bwd_workspace_bytes(int N, int C, int H, int W, int TILE, long long tot);
-int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, const int *offsets,
-                     const int *pair_splat, const int *pair_inv, long long tot, int N, int C, int H, int W,
-                     int TILE, int flags, const float *bg, const float *T, const float *asum, const float *fg,
-                     const float *gout, const float *dslog, const float *dsa, const float *dsac,
-                     float *g_mu, float *g_scale, float *g_theta, float *g_op, float *g_color, float *g_bg,
-                     void *ws, size_t ws_bytes, void *stream);
+ * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = nt per-tile partials of step 1.
+ * Replaces the index_add_ scatter and the g_bg reduction, render_triton.py:723-810. */
+size_t splat_reduce_workspace_bytes(long long tot);
+int splat_reduce_pairs(const float *rec, const int *offsets, const int *pair_splat, const int *pair_inv,
+                       long long tot, int N, int C, const float *pair_sums, const float *bg_part, int nparts,
+                       float *g_mu, float *g_scale, float *g_theta, float *g_op, float *g_color,
+                       float *g_bg, void *ws, size_t ws_bytes, void *stream);
 
 /* Exact (unculled) path: every pixel sums every splat; pixel centres py[P], px[P] supplied by the caller.
  * Replaces _render_fwd_kernel / _render_bwd_kernel and their wrappers, render_triton.py:58-303. */

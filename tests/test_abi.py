@@ -31,7 +31,8 @@ def test_workspace_queries_without_gpu():
     assert lib.splat_bin_count_workspace_bytes(92160) >= 8 * (92160 // 256)
     # three pair-sized int32 arrays for C1's pair count plus histograms
     assert lib.splat_bin_pairs_workspace_bytes(92160, 9216, 1_836_494) >= 3 * 4 * 1_836_494
-    assert lib.splat_render_bwd_workspace_bytes(92160, 3, 768, 768, 8, 1_836_494) >= 48 * 1_836_494
+    assert lib.splat_pair_sums_bytes(1_836_494) == 48 * 1_836_494
+    assert lib.splat_reduce_workspace_bytes(1_836_494) >= 2 * 40 * (1_836_494 // 64)
 
 
 def test_invalid_arguments_are_reported_not_launched():
