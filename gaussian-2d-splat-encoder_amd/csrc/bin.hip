@@ -26,15 +26,23 @@ constexpr int kWaveKeys = kSortKeys / kWaves;   // 1024 consecutive keys per wav
 constexpr long long kBadBit = 1LL << 62;        // marks a block holding an empty or inverted rect
 
 // ----------------------------------------------------------------------------------------------------
-// decode + rect + count
+// decode + level + rect + count. block_sums[blk * kSumCols + 0] = the block's pair count (| kBadBit),
+// block_sums[blk * kSumCols + 1 + l] = its pairs on level l.
+constexpr int kSumCols = 1 + kMaxLevels;
+
 template <int C>
 __global__ __launch_bounds__(kBlock) void k_decode_count(
     const float* __restrict__ mu, const float* __restrict__ scale, const float* __restrict__ theta,
-    const float* __restrict__ opacity, const float* __restrict__ color, int N, float fH, float fW, float fT,
-    float cutoff, float xmax, float ymax, int do_bin, float4* __restrict__ rec, int4* __restrict__ rect,
-    int* __restrict__ counts, long long* __restrict__ block_sums) {
+    const float* __restrict__ opacity, const float* __restrict__ color, int N, LevelTable L, Routing R, float fT,
+    float cutoff, int do_bin, float4* __restrict__ rec, int4* __restrict__ rect, int* __restrict__ counts,
+    long long* __restrict__ block_sums) {
   __shared__ long long s_part[kWaves];
+  __shared__ int s_lev[kMaxLevels];
   const int g = blockIdx.x * kBlock + threadIdx.x;
+  if (do_bin) {
+    for (int i = threadIdx.x; i < kMaxLevels; i += kBlock) s_lev[i] = 0;
+    __syncthreads();
+  }
   int cnt = 0;
   bool bad = false;
   if (g < N) {
@@ -55,6 +63,18 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     r[2] = col;
     r[3] = make_float4(s.x, s.y, cs, sn);
     if (do_bin) {
+      // level: render_triton.py:925-932 + 950-952 (octave), :904-913 (coarse/fine split)
+      int lev = 0;
+      if (R.mode == 1) {
+        const float px = fmaxf(s.x, s.y) * R.rep;
+        const float o = ceilf(log2f(fmaxf(px * R.inv_base, 1e-6f)));
+        lev = (int)fminf(fmaxf(o, 0.f), (float)R.max_oct);
+      } else if (R.mode == 2) {
+        lev = g < R.n_coarse ? 1 : 0;
+      }
+      const float fH = (float)L.H[lev], fW = (float)L.W[lev];
+      const float xmax = (float)(L.ntx[lev] - 1);
+      const float ymax = (float)((L.tbase[lev + 1] - L.tbase[lev]) / L.ntx[lev] - 1);
       // render_triton.py:367-377, one rounding per operation.
       const float cx = m.y * fW;
       const float cy = m.x * fH;
@@ -68,8 +88,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
       const int w = tx1 - tx0 + 1, h = ty1 - ty0 + 1;
       bad = (w < 1) || (h < 1);
       cnt = bad ? 0 : w * h;
-      rect[g] = make_int4(tx0, ty0, w, h);
+      rect[g] = make_int4(tx0, ty0, w, lev);   // the rect height is not needed past this point
       counts[g] = cnt;
+      if (cnt) atomicAdd(&s_lev[lev], cnt);
     }
   }
   if (!do_bin) return;
@@ -83,22 +104,33 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   if (threadIdx.x == 0) {
     long long t = 0, b = 0;
     for (int i = 0; i < kWaves; ++i) { t += s_part[i] & ~kBadBit; b |= s_part[i] & kBadBit; }
-    block_sums[blockIdx.x] = t | b;
+    block_sums[(size_t)blockIdx.x * kSumCols] = t | b;
   }
+  if (threadIdx.x < kMaxLevels) block_sums[(size_t)blockIdx.x * kSumCols + 1 + threadIdx.x] = s_lev[threadIdx.x];
 }
 
-// Exclusive scan of the per-block count sums in one workgroup; info[0] = total pairs, info[1] = error
-// bits (1: empty/inverted rect, 2: total exceeds int32).
-__global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums, int n, long long* __restrict__ info) {
+// Exclusive scan of the per-block count sums in one workgroup. info[0] = total pairs, info[1] = error bits
+// (1: empty/inverted rect, 2: total exceeds int32), info[2 + l] = pairs on level l < nlev.
+__global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums, int n, int nlev,
+                                                    long long* __restrict__ info) {
   __shared__ long long s_w[16];
   __shared__ long long s_carry;
   __shared__ long long s_bad;
+  __shared__ long long s_lev[kMaxLevels];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (threadIdx.x == 0) { s_carry = 0; s_bad = 0; }
+  if (threadIdx.x < kMaxLevels) s_lev[threadIdx.x] = 0;
   __syncthreads();
+  long long lev[kMaxLevels];
+#pragma unroll
+  for (int l = 0; l < kMaxLevels; ++l) lev[l] = 0;
   for (int base = 0; base < n; base += 1024) {
     const int i = base + threadIdx.x;
-    long long v = i < n ? sums[i] : 0;
+    long long v = i < n ? sums[(size_t)i * kSumCols] : 0;
+    if (i < n) {
+#pragma unroll
+      for (int l = 0; l < kMaxLevels; ++l) lev[l] += sums[(size_t)i * kSumCols + 1 + l];
+    }
     if (v & kBadBit) atomicOr((unsigned long long*)&s_bad, 1ull);
     v &= ~kBadBit;
     long long inc = wave_incl_scan(v, lane);
@@ -115,16 +147,24 @@ __global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums
     __syncthreads();
     const long long carry = s_carry;
     const long long excl = carry + (wv ? s_w[wv - 1] : 0) + inc - v;
-    if (i < n) sums[i] = excl;
+    if (i < n) sums[(size_t)i * kSumCols] = excl;
     __syncthreads();
     if (threadIdx.x == 0) s_carry = carry + s_w[15];
     __syncthreads();
   }
+#pragma unroll
+  for (int l = 0; l < kMaxLevels; ++l) {
+    long long x = lev[l];
+    for (int msk = 32; msk >= 1; msk >>= 1) x += __shfl_xor(x, msk, 64);
+    if (lane == 0 && x) atomicAdd((unsigned long long*)&s_lev[l], (unsigned long long)x);
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
     const long long tot = s_carry;
     info[0] = tot;
     info[1] = (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0);
   }
+  if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
 }
 
 // counts -> exclusive offsets in place; offsets[N] = total.
@@ -140,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, c
   int pre = 0;
   for (int i = 0; i < wv; ++i) pre += s_w[i];
   if (info[1] & 2) return;   // total overflows int32: the host raises, offsets are not used
-  if (g < N) offsets[g] = (int)block_pre[blockIdx.x] + pre + inc - c;
+  if (g < N) offsets[g] = (int)block_pre[(size_t)blockIdx.x * kSumCols] + pre + inc - c;
   if (g == N - 1) offsets[N] = (int)info[0];
 }
 
@@ -187,7 +227,7 @@ __device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
 // Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat (optional) and, with `hist` set, the
 // block's histogram of the first radix digit.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
-                                                          int N, int ntx, int tot, int dmask, int* __restrict__ keys,
+                                                          int N, LevelTable L, int tot, int dmask, int* __restrict__ keys,
                                                           int* __restrict__ vals, int* __restrict__ pair_splat,
                                                           int* __restrict__ hist, int nblocks) {
   __shared__ int4 s_own4[kSortKeys / 4];
@@ -241,7 +281,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
     const int4 rc = rect[g];
     const int ky = k / rc.z;
     const int kx = k - ky * rc.z;
-    const int tile = (rc.y + ky) * ntx + rc.x + kx;
+    const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;
     keys[p] = tile;
     vals[p] = g;
     if (pair_splat) pair_splat[p] = g;
@@ -355,9 +395,10 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
 
 // From the sorted (tile, splat) list: CSR starts (starts[t] = number of pairs with tile < t,
 // render_triton.py:408) and, optionally, the inverse permutation inv[q] = sorted position of splat-major
-// pair q, where q = offsets[g] + (ty - ty0) * w + (tx - tx0) is the pair's index in its splat's rect walk.
+// pair q, where q = offsets[g] + (ty - ty0) * w + (tx - tx0) is the pair's index in its splat's rect walk
+// (tile coordinates local to the splat's level).
 __global__ __launch_bounds__(kBlock) void k_tile_starts_inv(const int* __restrict__ keys, const int* __restrict__ gids,
-                                                            int tot, int nt, int ntx, const int4* __restrict__ rect,
+                                                            int tot, int nt, LevelTable L, const int4* __restrict__ rect,
                                                             const int* __restrict__ offsets, int* __restrict__ starts,
                                                             int* __restrict__ inv) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
@@ -370,7 +411,8 @@ __global__ __launch_bounds__(kBlock) void k_tile_starts_inv(const int* __restric
   if (inv) {
     const int g = gids[i];
     const int4 rc = rect[g];
-    const int ty = k / ntx, tx = k - ty * ntx;
+    const int lt = k - L.tbase[rc.w], ntx = L.ntx[rc.w];
+    const int ty = lt / ntx, tx = lt - ty * ntx;
     inv[offsets[g] + (ty - rc.y) * rc.z + (tx - rc.x)] = i;
   }
 }
@@ -413,7 +455,25 @@ using namespace splat;
 
 extern "C" {
 
-size_t splat_bin_count_workspace_bytes(int N) { return align256(sizeof(long long) * (size_t)(N > 0 ? div_up(N, kBlock) : 1)); }
+size_t splat_bin_count_workspace_bytes(int N) {
+  return align256(sizeof(long long) * kSumCols * (size_t)(N > 0 ? div_up(N, kBlock) : 1));
+}
+
+int splat_levels_geometry(int H, int W, int TILE, const splat_levels* lv, int* out, int cap) {
+  LevelTable L;
+  if (H < 1 || W < 1 || TILE < 1 || make_levels(H, W, TILE, lv, &L, nullptr))
+    return -set_error(kInvalid, "splat_levels_geometry: bad levels for H=%d W=%d TILE=%d", H, W, TILE);
+  if (out) {
+    if (cap < 5 * L.n + 2) return -set_error(kInvalid, "splat_levels_geometry: out holds %d < %d ints", cap, 5 * L.n + 2);
+    for (int l = 0; l < L.n; ++l) {
+      out[5 * l + 0] = L.H[l]; out[5 * l + 1] = L.W[l]; out[5 * l + 2] = L.ntx[l];
+      out[5 * l + 3] = L.tbase[l]; out[5 * l + 4] = L.pbase[l];
+    }
+    out[5 * L.n] = L.tbase[L.n];
+    out[5 * L.n + 1] = L.pbase[L.n];
+  }
+  return L.n;
+}
 
 int splat_decode(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
                  int C, int N, float* rec, void* stream) {
@@ -422,8 +482,10 @@ int splat_decode(const float* mu, const float* scale, const float* theta, const 
   if (!mu || !scale || !opacity || !color || !rec) return set_error(kInvalid, "splat_decode: null pointer");
   hipStream_t st = (hipStream_t)stream;
   const int nb = div_up(N, kBlock);
-#define SPLAT_DECODE(CC)                                                                                          \
-  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, 1.f, 1.f, 1.f, 0.f, 0.f, 0.f, 0, \
+  LevelTable L{};
+  Routing R{};
+#define SPLAT_DECODE(CC)                                                                                      \
+  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, 1.f, 0.f, 0,        \
                                             reinterpret_cast<float4*>(rec), nullptr, nullptr, nullptr)
   switch (C) { case 1: SPLAT_DECODE(1); break; case 2: SPLAT_DECODE(2); break;
                case 3: SPLAT_DECODE(3); break; default: SPLAT_DECODE(4); break; }
@@ -432,26 +494,27 @@ int splat_decode(const float* mu, const float* scale, const float* theta, const 
 }
 
 int splat_bin_count(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
-                    int C, int N, int H, int W, int TILE, float cutoff, float* rec, int* rect, int* offsets,
-                    long long* info, void* ws, size_t ws_bytes, void* stream) {
+                    int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, float* rec, int* rect,
+                    int* offsets, long long* info, void* ws, size_t ws_bytes, void* stream) {
   if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
     return set_error(kInvalid, "splat_bin_count: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
+  LevelTable L;
+  Routing R;
+  if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin_count: bad levels");
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
     return set_error(kInvalid, "splat_bin_count: null pointer");
   if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
   hipStream_t st = (hipStream_t)stream;
-  const int ntx = (W + TILE - 1) / TILE, nty = (H + TILE - 1) / TILE;
   const int nb = div_up(N, kBlock);
   long long* sums = (long long*)ws;
 #define SPLAT_DC(CC)                                                                                         \
-  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, (float)H, (float)W,       \
-                                            (float)TILE, cutoff, (float)(ntx - 1), (float)(nty - 1), 1,   \
+  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, (float)TILE, cutoff, 1, \
                                             reinterpret_cast<float4*>(rec), reinterpret_cast<int4*>(rect), \
                                             offsets, sums)
   switch (C) { case 1: SPLAT_DC(1); break; case 2: SPLAT_DC(2); break;
                case 3: SPLAT_DC(3); break; default: SPLAT_DC(4); break; }
 #undef SPLAT_DC
-  k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, info);
+  k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info);
   k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
   return check_launch("splat_bin_count");
 }
@@ -461,12 +524,15 @@ size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
   return plan_pairs(nt, tot).total;
 }
 
-int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, long long tot, int* gid_sorted,
-                    int* tile_starts, int* pair_splat, int* pair_inv, void* ws, size_t ws_bytes, void* stream) {
+int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, const splat_levels* lv,
+                    long long tot, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_inv, void* ws,
+                    size_t ws_bytes, void* stream) {
   if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
     return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
   if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
-  const int ntx = (W + TILE - 1) / TILE, nt = ntx * ((H + TILE - 1) / TILE);
+  LevelTable L;
+  if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_pairs: bad levels");
+  const int nt = L.tbase[L.n];
   const PairsPlan pl = plan_pairs(nt, tot);
   if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
   hipStream_t st = (hipStream_t)stream;
@@ -490,7 +556,7 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
   V[fin] = gid_sorted; V[1 - fin] = vals_b;
   const int t = (int)tot;
   const int dmask = pl.radix - 1;
-  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, ntx, t, dmask, K[0], V[0],
+  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, t, dmask, K[0], V[0],
                                               pair_splat, pl.passes ? hist : nullptr, pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
@@ -504,7 +570,7 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
   }
-  k_tile_starts_inv<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, ntx,
+  k_tile_starts_inv<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, L,
                                                           reinterpret_cast<const int4*>(rect), offsets, tile_starts,
                                                           pair_inv);
   return check_launch("k_tile_starts_inv");

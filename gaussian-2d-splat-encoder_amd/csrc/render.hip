@@ -91,31 +91,89 @@ __device__ __forceinline__ void store_composite(int p, float sl2, float s_a, con
   }
 }
 
-template <int C, bool FIELDS, bool ODDS, int TILE>
+// Bilinear samples (torch upsample_bilinear2d, align_corners=False) of the coarse levels' packed fields at
+// level-0 pixel (yp, xp), added to the running sums in the reference's order (level 1 first).
+template <int C>
+__device__ __forceinline__ void add_coarse(const LevelTable& L, int yp, int xp, const float* __restrict__ slog,
+                                           const float* __restrict__ sa, const float* __restrict__ sac, float& Sl,
+                                           float& Sa, float* Sc) {
+  for (int l = 1; l < L.n; ++l) {
+    if (!((L.mask >> l) & 1)) continue;
+    const int Hl = L.H[l], Wl = L.W[l];
+    int py1, px1;
+    float ly, lx;
+    const int y0 = bilinear_src(yp, Hl, (float)Hl / (float)L.H[0], &py1, &ly);
+    const int x0 = bilinear_src(xp, Wl, (float)Wl / (float)L.W[0], &px1, &lx);
+    const float h0 = 1.f - ly, w0 = 1.f - lx;
+    const size_t i00 = (size_t)L.pbase[l] + (size_t)y0 * Wl + x0, i01 = i00 + px1;
+    const size_t i10 = i00 + (size_t)py1 * Wl, i11 = i10 + px1;
+    Sl += h0 * (w0 * slog[i00] + lx * slog[i01]) + ly * (w0 * slog[i10] + lx * slog[i11]);
+    Sa += h0 * (w0 * sa[i00] + lx * sa[i01]) + ly * (w0 * sa[i10] + lx * sa[i11]);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      Sc[c] += h0 * (w0 * sac[i00 * C + c] + lx * sac[i01 * C + c]) + ly * (w0 * sac[i10 * C + c] + lx * sac[i11 * C + c]);
+  }
+}
+
+// Global tile t of a launch over tiles [tb0, tb0 + ntiles) (XCD-aware order), its level and coordinates.
+struct TileAt {
+  int t, l, tx, ty, H, W;
+};
+__device__ __forceinline__ TileAt tile_at(const LevelTable& L, int tb0, int ntiles) {
+  TileAt a;
+  a.t = tb0 + xcd_swizzle(blockIdx.x, ntiles);
+  a.l = level_of(L, a.t);
+  const int lt = a.t - L.tbase[a.l];
+  a.ty = lt / L.ntx[a.l];
+  a.tx = lt - a.ty * L.ntx[a.l];
+  a.H = L.H[a.l];
+  a.W = L.W[a.l];
+  return a;
+}
+
+// Forward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
+// FIELDS: raw sums into the packed per-level fields slog/sa/sac (slot pbase[l] + pixel).
+// Composite (level 0): out, T, asum, fg; with UPS the coarse levels' packed fields (inputs slog/sa/sac) are
+// upsampled and added first, and `asum` keeps the unclamped S_a (the clamp_min gradient needs it).
+template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
 __global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_cull(
-    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
-    int nt, const float* __restrict__ bg, float* __restrict__ out, float* __restrict__ Tout,
+    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
+    int ntiles, const float* __restrict__ bg, float* __restrict__ out, float* __restrict__ Tout,
     float* __restrict__ asum_out, float* __restrict__ fg_out, float* __restrict__ slog, float* __restrict__ sa,
     float* __restrict__ sac) {
-  const int t = xcd_swizzle(blockIdx.x, nt);
-  const int tx = t % ntx, ty = t / ntx;
+  const TileAt ta = tile_at(L, tb0, ntiles);
+  if (!((L.mask >> ta.l) & 1)) return;
   const int l = threadIdx.x;
-  const int yp = ty * TILE + l / TILE, xp = tx * TILE + l % TILE;
-  const bool valid = l < TILE * TILE && yp < H && xp < W;
-  const float py = ((float)yp + 0.5f) / (float)H;   // render_triton.py:455-456
-  const float px = ((float)xp + 0.5f) / (float)W;
-  const int g0 = starts[t], g1 = starts[t + 1];
+  const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
+  const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
+  const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
+  const float px = ((float)xp + 0.5f) / (float)ta.W;
+  const int g0 = starts[ta.t], g1 = starts[ta.t + 1];
   float sl = 0.f, s_a = 0.f, sc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = 0.f;
   fwd_pixel<C, ODDS>(rec, gid, g0, g1, py, px, sl, s_a, sc);
   if (!valid) return;
-  const int p = yp * W + xp;
+  const int p = yp * ta.W + xp;
   if (FIELDS) {
-    slog[p] = sl * kLn2;
-    sa[p] = s_a;
+    const size_t pp = (size_t)L.pbase[ta.l] + p;
+    slog[pp] = sl * kLn2;
+    sa[pp] = s_a;
 #pragma unroll
-    for (int c = 0; c < C; ++c) sac[(size_t)p * C + c] = sc[c];
+    for (int c = 0; c < C; ++c) sac[pp * C + c] = sc[c];
+  } else if (UPS) {
+    float Sl = sl * kLn2;
+    add_coarse<C>(L, yp, xp, slog, sa, sac, Sl, s_a, sc);
+    const float T = hw_exp2(Sl * kLog2e);
+    const float as = fmaxf(s_a, kAsumMin);
+    Tout[p] = T;
+    asum_out[p] = s_a;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float f = sc[c] / as;
+      fg_out[(size_t)p * C + c] = f;
+      out[(size_t)p * C + c] = (1.f - T) * f + T * bg[c];
+    }
   } else {
     store_composite<C>(p, sl, s_a, sc, bg, out, Tout, asum_out, fg_out);
   }
@@ -139,20 +197,25 @@ __global__ __launch_bounds__(64) void k_fwd_exact(const float* __restrict__ rec,
 }
 
 // Per-pixel upstream terms of the backward (render_triton.py:640-654). Masked pixels give zeros.
-template <int C, bool FIELDS>
-__device__ __forceinline__ void pixel_upstream(int p, const float* __restrict__ bg, const float* __restrict__ Tin,
-                                               const float* __restrict__ asum_in, const float* __restrict__ fg_in,
-                                               const float* __restrict__ gout, const float* __restrict__ dslog,
-                                               const float* __restrict__ dsa, const float* __restrict__ dsac,
-                                               float4& pa, float4& pb, float* bgp) {
+// FIELDS: loaded from the packed fields at slot pp. Composite: derived from T, asum, fg, gout and bg; with
+// UPS, `asum` holds the unclamped S_a and dS_a follows torch's clamp_min gradient (0 below 1e-8,
+// render_triton.py:976), and the terms are also stored at pixel p of dslog/dsa/dsac for the adjoint of
+// the coarse levels' upsample.
+template <int C, bool FIELDS, bool UPS>
+__device__ __forceinline__ void pixel_upstream(int p, size_t pp, const float* __restrict__ bg,
+                                               const float* __restrict__ Tin, const float* __restrict__ asum_in,
+                                               const float* __restrict__ fg_in, const float* __restrict__ gout,
+                                               float* __restrict__ dslog, float* __restrict__ dsa,
+                                               float* __restrict__ dsac, float4& pa, float4& pb, float* bgp) {
   float dl, da, dc[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   if (FIELDS) {
-    dl = dslog[p];
-    da = dsa[p];
+    dl = dslog[pp];
+    da = dsa[pp];
 #pragma unroll
-    for (int c = 0; c < C; ++c) dc[c] = dsac[(size_t)p * C + c];
+    for (int c = 0; c < C; ++c) dc[c] = dsac[pp * C + c];
   } else {
-    const float T = Tin[p], as = asum_in[p];
+    const float T = Tin[p], a_in = asum_in[p];
+    const float as = UPS ? fmaxf(a_in, kAsumMin) : a_in;
     float dTp = 0.f, sfg = 0.f;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -165,6 +228,13 @@ __device__ __forceinline__ void pixel_upstream(int p, const float* __restrict__ 
     }
     dl = dTp * T;
     da = -sfg / as;
+    if (UPS) {
+      if (!(a_in >= kAsumMin)) da = 0.f;
+      dslog[p] = dl;
+      dsa[p] = da;
+#pragma unroll
+      for (int c = 0; c < C; ++c) dsac[(size_t)p * C + c] = dc[c];
+    }
   }
   pa = make_float4(dl, da, dc[0], dc[1]);
   pb = make_float4(dc[2], dc[3], 0.f, 0.f);
@@ -271,38 +341,44 @@ __device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec
   for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = sums[6 + c];
 }
 
-template <int C, bool FIELDS, bool ODDS, int TILE>
+// Backward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
+// Composite (level 0): upstream from T/asum/fg/gout (see pixel_upstream for UPS); per-tile partials of
+// sum_p gout * T go to bg_part[c * ntiles + (t - tb0)]. FIELDS: upstream from the packed fields.
+template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_bwd_cull(
-    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, int H, int W, int ntx,
-    int nt, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
-    const float* __restrict__ fg_in, const float* __restrict__ gout, const float* __restrict__ dslog,
-    const float* __restrict__ dsa, const float* __restrict__ dsac, float* __restrict__ psum,
-    float* __restrict__ bg_part) {
+    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
+    int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
+    const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
+    float* __restrict__ dsa, float* __restrict__ dsac, float* __restrict__ psum, float* __restrict__ bg_part) {
   constexpr int NP = TILE * TILE;
   __shared__ float4 s_pa[NP];
   __shared__ float4 s_pb[NP];
   __shared__ float s_py[TILE], s_px[TILE];
-  const int t = xcd_swizzle(blockIdx.x, nt);
-  const int tx = t % ntx, ty = t / ntx;
+  const TileAt ta = tile_at(L, tb0, ntiles);
+  if (!((L.mask >> ta.l) & 1)) return;
+  const int t = ta.t;
   const int lane = threadIdx.x;
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int l = lane; l < NP; l += 64) {
-    const int yp = ty * TILE + l / TILE, xp = tx * TILE + l % TILE;
+    const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
-    if (yp < H && xp < W)
-      pixel_upstream<C, FIELDS>(yp * W + xp, bg, Tin, asum_in, fg_in, gout, dslog, dsa, dsac, pa, pb, bgp);
+    if (yp < ta.H && xp < ta.W) {
+      const int p = yp * ta.W + xp;
+      pixel_upstream<C, FIELDS, UPS>(p, (size_t)L.pbase[ta.l] + p, bg, Tin, asum_in, fg_in, gout, dslog, dsa, dsac,
+                                     pa, pb, bgp);
+    }
     s_pa[l] = pa;
     s_pb[l] = pb;
   }
   if (lane < TILE) {
-    s_py[lane] = ((float)(ty * TILE + lane) + 0.5f) / (float)H;
-    s_px[lane] = ((float)(tx * TILE + lane) + 0.5f) / (float)W;
+    s_py[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / (float)ta.H;
+    s_px[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / (float)ta.W;
   }
   if (!FIELDS && bg_part) {
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const float v = wave_sum(bgp[c]);
-      if (lane == 0) bg_part[(size_t)c * nt + t] = v;
+      if (lane == 0) bg_part[(size_t)c * ntiles + (t - tb0)] = v;
     }
   }
   __syncthreads();
@@ -463,7 +539,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
     float2 pyx = make_float2(0.f, 0.f);
     if (p < P) {
-      pixel_upstream<C, false>(p, bg, Tin, asum_in, fg_in, gout, nullptr, nullptr, nullptr, pa, pb, bgp);
+      pixel_upstream<C, false, false>(p, 0, bg, Tin, asum_in, fg_in, gout, nullptr, nullptr, nullptr, pa, pb, bgp);
       pyx = make_float2(pyv[p], pxv[p]);
     }
     __syncthreads();
@@ -542,6 +618,110 @@ __global__ __launch_bounds__(256) void k_acc_finalize(const float* __restrict__ 
   splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
+// ------------------------------------------------------------------------------------ upsample adjoint
+// The level-0 composite adds bilinear upsamples of the coarse levels' fields (torch upsample_bilinear2d,
+// align_corners=False, render_triton.py:864-876). Its exact adjoint maps the level-0 upstream dS_0 to each
+// coarse level: dS_l[i, j] = sum_{y, x} wy(y -> i) wx(x -> j) dS_0[y, x], computed as two gather passes
+// (columns, then rows) with no atomics. Terms per pixel: S_log, S_a and C colour sums, 2 + C in all.
+
+// Level-0 upsample weight of destination d on source texel i (scale = in / out).
+__device__ __forceinline__ float ups_weight(int d, int i, int in, float scale) {
+  int p1;
+  float l1;
+  const int i0 = bilinear_src(d, in, scale, &p1, &l1);
+  return (i0 == i ? 1.f - l1 : 0.f) + (i0 + p1 == i ? l1 : 0.f);
+}
+
+// Destinations d in [0, out) whose bilinear sources may include texel i: every d with src(d) in [i - 1, i + 1),
+// widened by one on each side against rounding (weights are evaluated exactly inside).
+__device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo, int* hi) {
+  const float inv = 1.f / scale;
+  const int a = (int)floorf(((float)i - 0.5f) * inv - 0.5f) - 1;
+  const int b = (int)ceilf(((float)i + 1.5f) * inv - 0.5f) + 1;
+  *lo = a > 0 ? a : 0;
+  *hi = b < out - 1 ? b : out - 1;
+}
+
+// Column slot of coarse level l: cbase(l) = sum of W[1..l-1].
+__device__ __forceinline__ int coarse_col_level(const LevelTable& L, int j, int* ix) {
+  int l = 1, base = 0;
+  while (l + 1 < L.n && j >= base + L.W[l]) {
+    base += L.W[l];
+    ++l;
+  }
+  *ix = j - base;
+  return l;
+}
+
+// Pass 1: workgroup = level-0 row y; tmp[k][y][j] = sum_x wx(x -> ix) dS_0[k][y, x] for every coarse column
+// slot j = cbase(l) + ix of the masked levels (the row stays in cache across the slots).
+template <int C>
+__global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const float* __restrict__ dslog,
+                                                  const float* __restrict__ dsa, const float* __restrict__ dsac,
+                                                  float* __restrict__ tmp) {
+  const int y = blockIdx.x, H0 = L.H[0], W0 = L.W[0];
+  const size_t plane = (size_t)H0 * ncols;
+  for (int j = threadIdx.x; j < ncols; j += 256) {
+    int ix;
+    const int l = coarse_col_level(L, j, &ix);
+    if (!((L.mask >> l) & 1)) continue;
+    const int Wl = L.W[l];
+    const float sx = (float)Wl / (float)W0;
+    int x0, x1;
+    ups_window(ix, W0, sx, &x0, &x1);
+    float al = 0.f, aa = 0.f, ac[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+    for (int x = x0; x <= x1; ++x) {
+      const float w = ups_weight(x, ix, Wl, sx);
+      if (w == 0.f) continue;
+      const size_t p = (size_t)y * W0 + x;
+      al += w * dslog[p];
+      aa += w * dsa[p];
+#pragma unroll
+      for (int c = 0; c < C; ++c) ac[c] += w * dsac[p * C + c];
+    }
+    const size_t o = (size_t)y * ncols + j;
+    tmp[o] = al;
+    tmp[plane + o] = aa;
+#pragma unroll
+    for (int c = 0; c < C; ++c) tmp[(2 + c) * plane + o] = ac[c];
+  }
+}
+
+// Pass 2: thread = coarse texel (l, iy, ix) of a masked level, q = packed slot - pbase[1];
+// dS_l[iy, ix] = sum_y wy(y -> iy) tmp[k][y][cbase(l) + ix], written to the packed fields at pbase[l].
+template <int C>
+__global__ __launch_bounds__(256) void k_adj_rows(LevelTable L, int ncols, const float* __restrict__ tmp,
+                                                  float* __restrict__ dslog, float* __restrict__ dsa,
+                                                  float* __restrict__ dsac) {
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  if (q >= L.pbase[L.n] - L.pbase[1]) return;
+  const int pp = L.pbase[1] + q;
+  const int l = level_of_slot(L, pp);
+  if (!((L.mask >> l) & 1)) return;
+  int cb = 0;
+  for (int k = 1; k < l; ++k) cb += L.W[k];
+  const int Hl = L.H[l], Wl = L.W[l], H0 = L.H[0];
+  const int r = pp - L.pbase[l], iy = r / Wl, ix = r - iy * Wl;
+  const float sy = (float)Hl / (float)H0;
+  const size_t plane = (size_t)H0 * ncols;
+  int y0, y1;
+  ups_window(iy, H0, sy, &y0, &y1);
+  float al = 0.f, aa = 0.f, ac[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+  for (int y = y0; y <= y1; ++y) {
+    const float w = ups_weight(y, iy, Hl, sy);
+    if (w == 0.f) continue;
+    const size_t o = (size_t)y * ncols + cb + ix;
+    al += w * tmp[o];
+    aa += w * tmp[plane + o];
+#pragma unroll
+    for (int c = 0; c < C; ++c) ac[c] += w * tmp[(2 + c) * plane + o];
+  }
+  dslog[pp] = al;
+  dsa[pp] = aa;
+#pragma unroll
+  for (int c = 0; c < C; ++c) dsac[(size_t)pp * C + c] = ac[c];
+}
+
 // ---------------------------------------------------------------------------------------------------- dispatch
 template <typename F>
 int with_c(int C, F&& f) {
@@ -564,14 +744,33 @@ int with_tile(int TILE, F&& f) {
   return set_error(kUnsupported, "TILE=%d not supported (4, 8 or 16)", TILE);
 }
 
+// FIELDS, ODDS, UPS (UPS only with the composite: the caller rejects FIELDS | UPS).
 template <typename F>
 int with_flags(int flags, F&& f) {
-  switch (flags & 3) {
-    case 0: return f(IC<0>{}, IC<0>{});
-    case 1: return f(IC<1>{}, IC<0>{});
-    case 2: return f(IC<0>{}, IC<1>{});
-    default: return f(IC<1>{}, IC<1>{});
+  switch (flags & 7) {
+    case 0: return f(IC<0>{}, IC<0>{}, IC<0>{});
+    case 1: return f(IC<1>{}, IC<0>{}, IC<0>{});
+    case 2: return f(IC<0>{}, IC<1>{}, IC<0>{});
+    case 3: return f(IC<1>{}, IC<1>{}, IC<0>{});
+    case 4: return f(IC<0>{}, IC<0>{}, IC<1>{});
+    default: return f(IC<0>{}, IC<1>{}, IC<1>{});
   }
+}
+
+// Host: level table and the tile range [tb0, tb0 + ntiles) of a launch over levels [lev_begin, lev_end).
+static int launch_levels(const char* who, int H, int W, int TILE, const splat_levels* lv, int lev_begin, int lev_end,
+                         unsigned levmask, int flags, LevelTable* L, int* tb0, int* ntiles) {
+  if (H < 1 || W < 1) return set_error(kInvalid, "%s: H=%d W=%d", who, H, W);
+  if ((flags & kFlagFields) && (flags & kFlagUps)) return set_error(kInvalid, "%s: FIELDS and UPS exclude each other", who);
+  if (make_levels(H, W, TILE, lv, L, nullptr)) return set_error(kInvalid, "%s: bad levels for H=%d W=%d", who, H, W);
+  if (lev_begin < 0 || lev_end > L->n || lev_begin >= lev_end)
+    return set_error(kInvalid, "%s: levels [%d, %d) outside [0, %d)", who, lev_begin, lev_end, L->n);
+  if (!(flags & kFlagFields) && (lev_begin != 0 || lev_end != 1))
+    return set_error(kInvalid, "%s: the composite renders level 0 only", who);
+  L->mask = levmask & L->mask;
+  *tb0 = L->tbase[lev_begin];
+  *ntiles = L->tbase[lev_end] - L->tbase[lev_begin];
+  return kOk;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -583,22 +782,28 @@ using namespace splat;
 extern "C" {
 
 int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_starts, int C, int H, int W, int TILE,
-                     int flags, const float* bg, float* out, float* T, float* asum, float* fg, float* slog, float* sa,
-                     float* sac, void* stream) {
-  if (H < 1 || W < 1) return set_error(kInvalid, "splat_render_fwd: H=%d W=%d", H, W);
+                     int flags, const splat_levels* lv, int lev_begin, int lev_end, unsigned levmask, const float* bg,
+                     float* out, float* T, float* asum, float* fg, float* slog, float* sa, float* sac, void* stream) {
+  LevelTable L;
+  int tb0, ntiles;
+  if (int e = launch_levels("splat_render_fwd", H, W, TILE, lv, lev_begin, lev_end, levmask, flags, &L, &tb0, &ntiles))
+    return e;
   if (!rec || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_render_fwd: null pair list");
   const bool fields = flags & kFlagFields;
-  if (fields ? (!slog || !sa || !sac) : (!bg || !out || !T || !asum || !fg))
+  const bool coarse_in = (flags & kFlagUps) && (L.mask & ~1u);
+  if (fields || coarse_in ? (!slog || !sa || !sac) : false)
+    return set_error(kInvalid, "splat_render_fwd: null fields for flags=%d", flags);
+  if (!fields && (!bg || !out || !T || !asum || !fg))
     return set_error(kInvalid, "splat_render_fwd: null output for flags=%d", flags);
+  if (ntiles == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   return with_c(C, [&](auto cc) {
     return with_tile(TILE, [&](auto tt) {
-      return with_flags(flags, [&](auto fl, auto od) {
+      return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
-        const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
-        k_fwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, TT>
-            <<<nt, tile_threads(TT), 0, st>>>(rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, out, T, asum, fg, slog,
-                                               sa, sac);
+        k_fwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
+            <<<ntiles, tile_threads(TT), 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg,
+                                                  slog, sa, sac);
         return check_launch("k_fwd_cull");
       });
     });
@@ -613,28 +818,67 @@ static size_t reduce_ws_bytes(long long tot) {
 size_t splat_pair_sums_bytes(long long tot) { return sizeof(float) * kPairRec * (size_t)(tot > 0 ? tot : 1); }
 
 int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, long long tot, int C, int H,
-                     int W, int TILE, int flags, const float* bg, const float* T, const float* asum, const float* fg,
-                     const float* gout, const float* dslog, const float* dsa, const float* dsac, float* pair_sums,
-                     float* bg_part, void* stream) {
-  if (H < 1 || W < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
-    return set_error(kInvalid, "splat_render_bwd: H=%d W=%d tot=%lld", H, W, tot);
+                     int W, int TILE, int flags, const splat_levels* lv, int lev_begin, int lev_end, unsigned levmask,
+                     const float* bg, const float* T, const float* asum, const float* fg, const float* gout,
+                     float* dslog, float* dsa, float* dsac, float* pair_sums, float* bg_part, void* stream) {
+  LevelTable L;
+  int tb0, ntiles;
+  if (int e = launch_levels("splat_render_bwd", H, W, TILE, lv, lev_begin, lev_end, levmask, flags, &L, &tb0, &ntiles))
+    return e;
+  if (tot < 0 || tot > 0x7fffffffLL - 64) return set_error(kInvalid, "splat_render_bwd: tot=%lld", tot);
   if (!rec || !gid_sorted || !tile_starts || !pair_sums) return set_error(kInvalid, "splat_render_bwd: null pointer");
   const bool fields = flags & kFlagFields;
-  if (fields ? (!dslog || !dsa || !dsac) : (!bg || !T || !asum || !fg || !gout))
+  if ((fields || (flags & kFlagUps)) && (!dslog || !dsa || !dsac))
+    return set_error(kInvalid, "splat_render_bwd: null upstream fields for flags=%d", flags);
+  if (!fields && (!bg || !T || !asum || !fg || !gout))
     return set_error(kInvalid, "splat_render_bwd: null upstream for flags=%d", flags);
   if (fields && bg_part) return set_error(kInvalid, "splat_render_bwd: no background partials in FIELDS mode");
+  if (ntiles == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   return with_c(C, [&](auto cc) {
     return with_tile(TILE, [&](auto tt) {
-      return with_flags(flags, [&](auto fl, auto od) {
+      return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
-        constexpr bool FL = decltype(fl)::value != 0;
-        const int ntx = (W + TT - 1) / TT, nt = ntx * ((H + TT - 1) / TT);
-        k_bwd_cull<CC, FL, decltype(od)::value != 0, TT><<<nt, 64, 0, st>>>(
-            rec, gid_sorted, tile_starts, H, W, ntx, nt, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_sums, bg_part);
+        k_bwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
+            <<<ntiles, 64, 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa,
+                                    dsac, pair_sums, bg_part);
         return check_launch("k_bwd_cull");
       });
     });
+  });
+}
+
+static int adjoint_cols(const LevelTable& L) {
+  int n = 0;
+  for (int l = 1; l < L.n; ++l) n += L.W[l];
+  return n;
+}
+
+size_t splat_upsample_adjoint_workspace_bytes(int C, int H, int W, int TILE, const splat_levels* lv) {
+  LevelTable L;
+  if (C < 1 || C > kMaxC || H < 1 || W < 1 || make_levels(H, W, TILE, lv, &L, nullptr)) return 0;
+  return align256(sizeof(float) * (size_t)(2 + C) * (size_t)L.H[0] * (size_t)(adjoint_cols(L) > 0 ? adjoint_cols(L) : 1));
+}
+
+int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels* lv, unsigned levmask, float* dslog,
+                           float* dsa, float* dsac, void* ws, size_t ws_bytes, void* stream) {
+  LevelTable L;
+  if (C < 1 || C > kMaxC || H < 1 || W < 1 || make_levels(H, W, TILE, lv, &L, nullptr))
+    return set_error(kInvalid, "splat_upsample_adjoint: C=%d H=%d W=%d or bad levels", C, H, W);
+  if (!dslog || !dsa || !dsac) return set_error(kInvalid, "splat_upsample_adjoint: null fields");
+  L.mask = levmask & L.mask & ~1u;
+  if (L.n < 2 || !L.mask) return kOk;
+  if (!ws || ws_bytes < splat_upsample_adjoint_workspace_bytes(C, H, W, TILE, lv))
+    return set_error(kWorkspace, "splat_upsample_adjoint: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int ncols = adjoint_cols(L);
+  const int ncoarse = L.pbase[L.n] - L.pbase[1];
+  float* tmp = (float*)ws;
+  return with_c(C, [&](auto cc) {
+    constexpr int CC = decltype(cc)::value;
+    k_adj_cols<CC><<<L.H[0], 256, 0, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+    k_adj_rows<CC><<<(ncoarse + 255) / 256, 256, 0, st>>>(L, ncols, tmp, dslog, dsa, dsac);
+    return check_launch("splat_upsample_adjoint");
   });
 }
 
@@ -644,9 +888,10 @@ int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_spl
                        int N, int C, const float* pair_sums, const float* bg_part, int nparts, float* g_mu,
                        float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws,
                        size_t ws_bytes, void* stream) {
-  if (N < 1 || tot < 0 || tot > 0x7fffffffLL - 64) return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
-  if (!rec || !offsets || (tot > 0 && (!pair_splat || !pair_inv || !pair_sums)) || !g_mu || !g_scale || !g_op ||
-      !g_color || (g_bg && (!bg_part || nparts < 1)))
+  if (N < 0 || tot < 0 || tot > 0x7fffffffLL - 64 || (N == 0 && tot > 0))
+    return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
+  if ((N > 0 && (!rec || !offsets || !g_mu || !g_scale || !g_op || !g_color)) ||
+      (tot > 0 && (!pair_splat || !pair_inv || !pair_sums)) || (g_bg && (!bg_part || nparts < 1)))
     return set_error(kInvalid, "splat_reduce_pairs: null pointer");
   if (ws_bytes < reduce_ws_bytes(tot)) return set_error(kWorkspace, "splat_reduce_pairs: workspace too small");
   hipStream_t st = (hipStream_t)stream;
@@ -660,8 +905,9 @@ int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_spl
       k_pair_reduce<CC><<<(unsigned)((nchunk + 3) / 4), 256, 0, st>>>(rec, pair_sums, pair_splat, pair_inv, offsets, t,
                                                                       g_mu, g_scale, g_theta, g_op, g_color, pfirst,
                                                                       plast);
-    k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta, g_op,
-                                                        g_color);
+    if (N > 0)
+      k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta,
+                                                          g_op, g_color);
     if (g_bg) k_bg_sum<CC><<<1, 1024, 0, st>>>(bg_part, nparts, g_bg);
     return check_launch("splat_reduce_pairs");
   });
@@ -686,22 +932,23 @@ size_t splat_exact_bwd_workspace_bytes(int N, int C, int P) {
 int splat_exact_bwd(const float* rec, int N, int C, const float* py, const float* px, int P, const float* bg,
                     const float* T, const float* asum, const float* fg, const float* gout, float* g_mu, float* g_scale,
                     float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws, size_t ws_bytes, void* stream) {
-  if (N < 1 || P < 1 || !rec || !py || !px || !bg || !T || !asum || !fg || !gout || !g_mu || !g_scale || !g_op ||
-      !g_color)
+  if (N < 0 || P < 1 || !py || !px || !bg || !T || !asum || !fg || !gout ||
+      (N > 0 && (!rec || !g_mu || !g_scale || !g_op || !g_color)))
     return set_error(kInvalid, "splat_exact_bwd: bad arguments N=%d P=%d", N, P);
   if (ws_bytes < splat_exact_bwd_workspace_bytes(N, C, P)) return set_error(kWorkspace, "splat_exact_bwd: workspace too small");
   hipStream_t st = (hipStream_t)stream;
   float* acc = (float*)ws;
-  float* part = (float*)((char*)ws + align256(sizeof(float) * kAcc * (size_t)N));
+  float* part = (float*)((char*)ws + align256(sizeof(float) * kAcc * (size_t)(N > 0 ? N : 1)));
   const int nchunk = (P + 255) / 256;
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
-    k_bwd_exact<CC><<<(N + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, T, asum, fg, gout, acc);
+    if (N > 0) k_bwd_exact<CC><<<(N + 63) / 64, 64, 0, st>>>(rec, N, py, px, P, bg, T, asum, fg, gout, acc);
     if (g_bg) {
       k_bg_partial<CC><<<nchunk, 256, 0, st>>>(gout, T, P, part);
       k_bg_sum<CC><<<1, 1024, 0, st>>>(part, nchunk, g_bg);
     }
-    k_acc_finalize<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op, g_color);
+    if (N > 0)
+      k_acc_finalize<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, acc, N, g_mu, g_scale, g_theta, g_op, g_color);
     return check_launch("splat_exact_bwd");
   });
 }

@@ -27,6 +27,7 @@ enum RecSlot : int {
 // falloff exp(-maha / 2) is exp2(-(u^2 + v^2)) on the hardware exp2.
 constexpr float kWhiten = 0.849321800288019f;
 constexpr float kLn2 = 0.693147180559945f;
+constexpr float kLog2e = 1.44269504088896f;
 // Alpha clamp 1 - 1e-4 rounded to float32 (0.99989998...), as the reference compares in fp32.
 constexpr float kClamp = 0.99989998340606689453125f;
 constexpr float kAsumMin = 1e-8f;
@@ -39,6 +40,7 @@ constexpr float kNearOpaque = 0.9f;
 // Render mode flags of the C-ABI.
 constexpr int kFlagFields = 1;   // write raw partial sums (S_log, S_a, S_ac) instead of the composite
 constexpr int kFlagOdds = 2;     // weight colour by the odds a / (1 - a) instead of a
+constexpr int kFlagUps = 4;      // composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a
 
 // Status codes of the C-ABI.
 enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2, kUnsupported = 3, kOverflow = 4, kWorkspace = 5 };
@@ -97,5 +99,116 @@ __device__ __forceinline__ T wave_incl_scan(T v, int lane) {
 }
 
 inline int div_up(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------------------------- levels
+// A render may place splats on several canvases ("levels"): level 0 is the native (H, W) canvas, the
+// others are coarser canvases whose fields are bilinearly upsampled onto level 0 (the octave and
+// coarse/fine renders of render_triton.py:879-980). Level l is tiled by TILE; its tiles take the global
+// tile ids [tbase[l], tbase[l+1]) and its pixels the packed field slots [pbase[l], pbase[l+1]).
+constexpr int kMaxLevels = 12;
+
+struct LevelTable {
+  int n;
+  unsigned mask;   // levels holding at least one pair; kernels skip the others
+  int H[kMaxLevels], W[kMaxLevels], ntx[kMaxLevels];
+  int tbase[kMaxLevels + 1], pbase[kMaxLevels + 1];
+};
+
+// Splat -> level routing, evaluated in the decode pass.
+struct Routing {
+  int mode;         // 0 single level, 1 octave by scale, 2 split by index
+  int max_oct;      // mode 1
+  float rep;        // mode 1: float(min(H, W))
+  float inv_base;   // mode 1: fp32 1 / base_texels (a tensor divided by a CPU scalar is a multiply by its reciprocal)
+  int n_coarse;     // mode 2: splats [0, n_coarse) are level 1
+};
+
+__device__ __forceinline__ int level_of(const LevelTable& L, int t) {
+  int l = 0;
+  while (l + 1 < L.n && t >= L.tbase[l + 1]) ++l;
+  return l;
+}
+
+// Level of packed pixel slot pp.
+__device__ __forceinline__ int level_of_slot(const LevelTable& L, int pp) {
+  int l = 0;
+  while (l + 1 < L.n && pp >= L.pbase[l + 1]) ++l;
+  return l;
+}
+
+// Bilinear source of output index d when upsampling `in` samples to `out` (torch upsample_bilinear2d with
+// align_corners=False: src = max(scale * (d + 0.5) - 0.5, 0) with scale = in / out in fp32). Returns the
+// first source index; *p1 is 1 when a second source exists, *l1 the weight of the second (the first gets
+// 1 - l1).
+__device__ __forceinline__ int bilinear_src(int d, int in, float scale, int* p1, float* l1) {
+  const float r = fmaxf(fmaf(scale, (float)d + 0.5f, -0.5f), 0.f);
+  const int i = (int)r;
+  *p1 = i < in - 1 ? 1 : 0;
+  *l1 = r - (float)i;
+  return i;
+}
+
+}  // namespace splat
+
+extern "C" {
+// C-ABI description of the levels of a render (mirrors include/splat_render.h).
+typedef struct splat_levels {
+  int mode;           // 0 single level (H, W); 1 octave routing; 2 coarse/fine split by index
+  int max_octaves;    // mode 1: levels 0..max_octaves, level o on (max(8, H >> o), max(8, W >> o))
+  float base_texels;  // mode 1: o = clamp(ceil(log2(max(max(sy, sx) * min(H, W) / base_texels, 1e-6))), 0, max_octaves)
+  int n_coarse;       // mode 2: splats [0, n_coarse) render on (coarse_H, coarse_W) as level 1, the rest on (H, W)
+  int coarse_H, coarse_W;
+} splat_levels;
+}
+
+namespace splat {
+
+// Host: level geometry of a render of the (H, W) canvas with tile size TILE. Returns 0 or a status.
+inline int make_levels(int H, int W, int TILE, const splat_levels* lv, LevelTable* L, Routing* R) {
+  LevelTable t{};
+  Routing r{};
+  int mode = lv ? lv->mode : 0;
+  if (mode == 0) {
+    t.n = 1;
+    t.H[0] = H; t.W[0] = W;
+  } else if (mode == 1) {
+    if (lv->max_octaves < 0 || !(lv->base_texels > 0.f)) return 1;
+    // Octaves at and past the first whose canvas is clamped to (8, 8) in both dims share that canvas; their
+    // fields are summed after the same upsample, so they are one level (routing clamps to it).
+    int osat = 0;
+    while ((H >> osat) > 8 || (W >> osat) > 8) ++osat;
+    t.n = (lv->max_octaves < osat ? lv->max_octaves : osat) + 1;
+    if (t.n > kMaxLevels) return 1;
+    for (int o = 0; o < t.n; ++o) {
+      t.H[o] = (H >> o) > 8 ? (H >> o) : 8;
+      t.W[o] = (W >> o) > 8 ? (W >> o) : 8;
+    }
+    if (t.H[0] != H || t.W[0] != W) return 1;   // octave 0 must be the native canvas (H, W >= 8)
+    r.max_oct = t.n - 1;
+    r.rep = (float)(H < W ? H : W);
+    r.inv_base = 1.0f / lv->base_texels;
+  } else if (mode == 2) {
+    if (lv->coarse_H < 1 || lv->coarse_W < 1 || lv->n_coarse < 0) return 1;
+    t.n = 2;
+    t.H[0] = H; t.W[0] = W;
+    t.H[1] = lv->coarse_H; t.W[1] = lv->coarse_W;
+    r.n_coarse = lv->n_coarse;
+  } else {
+    return 1;
+  }
+  r.mode = mode;
+  t.mask = (t.n >= 32) ? 0xffffffffu : ((1u << t.n) - 1u);
+  t.tbase[0] = 0;
+  t.pbase[0] = 0;
+  for (int l = 0; l < t.n; ++l) {
+    t.ntx[l] = (t.W[l] + TILE - 1) / TILE;
+    const long long nty = (t.H[l] + TILE - 1) / TILE;
+    t.tbase[l + 1] = (int)(t.tbase[l] + (long long)t.ntx[l] * nty);
+    t.pbase[l + 1] = (int)(t.pbase[l] + (long long)t.H[l] * t.W[l]);
+  }
+  *L = t;
+  if (R) *R = r;
+  return 0;
+}
 
 }  // namespace splat

@@ -20,19 +20,35 @@ _F = ctypes.c_float
 _SZ = ctypes.c_size_t
 _LL = ctypes.c_longlong
 
+
+
+class SplatLevels(ctypes.Structure):
+    """struct splat_levels: mode 0 single canvas, 1 octave routing, 2 coarse/fine split by index."""
+    _fields_ = [("mode", _I), ("max_octaves", _I), ("base_texels", _F), ("n_coarse", _I),
+                ("coarse_H", _I), ("coarse_W", _I)]
+
+
+_LV = ctypes.POINTER(SplatLevels)
+_U = ctypes.c_uint
+
 # name -> (restype, argtypes)
 _SIGS = {
     "splat_last_error": (ctypes.c_char_p, []),
     "splat_abi_version": (_I, []),
     "splat_decode": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "splat_bin_count_workspace_bytes": (_SZ, [_I]),
-    "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_levels_geometry": (_I, [_I, _I, _I, _LV, _VP, _I]),
+    "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _VP, _VP, _VP, _VP, _VP, _SZ,
+                             _VP]),
     "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _LL]),
-    "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
-    "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
-    "splat_pair_sums_bytes": (_SZ, [_LL]),
-    "splat_render_bwd": (_I, [_VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+    "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP, _VP,
                               _VP, _VP, _VP]),
+    "splat_pair_sums_bytes": (_SZ, [_LL]),
+    "splat_render_bwd": (_I, [_VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP,
+                              _VP, _VP, _VP, _VP, _VP, _VP]),
+    "splat_upsample_adjoint_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV]),
+    "splat_upsample_adjoint": (_I, [_I, _I, _I, _I, _LV, _U, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_reduce_workspace_bytes": (_SZ, [_LL]),
     "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP,
                                 _VP, _SZ, _VP]),
@@ -46,6 +62,7 @@ EXPORTED = tuple(_SIGS)
 
 FLAG_FIELDS = 1
 FLAG_ODDS = 2
+FLAG_UPS = 4
 
 _STATUS = {1: "invalid argument", 2: "HIP error", 3: "unsupported configuration", 4: "overflow",
            5: "workspace too small"}

@@ -22,7 +22,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from ._lib import FLAG_FIELDS, FLAG_ODDS, check, ptr
+from ._lib import FLAG_FIELDS, FLAG_ODDS, FLAG_UPS, SplatLevels, check, ptr
 from .params import activate_scale
 from .render import _pixels
 
@@ -87,39 +87,91 @@ class TileBins:
     """Per-batch binning result: decoded splat records, pair list ordered by (tile, splat) and CSR tile
     starts (`gid_b`/`starts_b`/`ntx`/`nt` carry the meaning of the reference's `tiles` tuple), plus the
     splat-major pair maps the backward's per-splat reduction uses (offsets, pair -> splat, pair -> sorted
-    position)."""
+    position).
 
-    def __init__(self, rec_b, gid_b, starts_b, tot_b, H, W, TILE, ntx, nt, off_b=None, psplat_b=None, pinv_b=None):
+    With levels (`lv` set) the tile ids are global over the levels: `geom[l] = (H_l, W_l, ntx_l, tbase_l,
+    pbase_l)`, `nt` / `npix` are the totals, `level_tot_b[b][l]` the pairs of level l and `rect_b[b][:, 3]`
+    each splat's level."""
+
+    def __init__(self, rec_b, gid_b, starts_b, tot_b, H, W, TILE, ntx, nt, off_b=None, psplat_b=None, pinv_b=None,
+                 lv=None, geom=None, npix=None, level_tot_b=None, rect_b=None):
         self.rec_b, self.gid_b, self.starts_b, self.tot_b = rec_b, gid_b, starts_b, tot_b
         self.H, self.W, self.TILE, self.ntx, self.nt = H, W, TILE, ntx, nt
         self.off_b, self.psplat_b, self.pinv_b = off_b, psplat_b, pinv_b
+        self.lv, self.geom, self.npix, self.level_tot_b, self.rect_b = lv, geom, npix, level_tot_b, rect_b
 
     def as_tuple(self):
         return self.gid_b, self.starts_b, self.ntx, self.nt
 
+    @property
+    def n_levels(self):
+        return 1 if self.geom is None else len(self.geom)
 
-def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True) -> TileBins:
+    @property
+    def ntiles0(self):
+        """Tiles of level 0 (the composite's canvas)."""
+        return self.nt if self.geom is None else self.geom[1][3] if len(self.geom) > 1 else self.nt
+
+    def level_mask(self, b):
+        """Levels of batch b holding pairs, with level 0 always set (the composite covers every pixel)."""
+        if self.level_tot_b is None:
+            return 1
+        m = 1
+        for l, n in enumerate(self.level_tot_b[b]):
+            if n > 0:
+                m |= 1 << l
+        return m
+
+
+def levels_geometry(H, W, TILE, lv):
+    """[(H_l, W_l, ntx_l, tbase_l, pbase_l)] per level, total tiles, total packed pixel slots."""
+    lib = _lib.load()
+    ref = None if lv is None else _lib.ctypes.byref(lv)
+    n = lib.splat_levels_geometry(H, W, TILE, ref, None, 0)
+    if n < 0:
+        check(-n, "splat_levels_geometry")
+    buf = (_lib.ctypes.c_int * (5 * n + 2))()
+    check(0 if lib.splat_levels_geometry(H, W, TILE, ref, buf, 5 * n + 2) == n else 1, "splat_levels_geometry")
+    geom = [tuple(buf[5 * l:5 * l + 5]) for l in range(n)]
+    return geom, buf[5 * n], buf[5 * n + 1]
+
+
+def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True, lv=None) -> TileBins:
     """Decode + bin every batch (render_triton.py:351-409). One host read of the per-batch pair totals.
-    with_maps=False skips the pair maps only the backward needs (forward-only renders)."""
+    with_maps=False skips the pair maps only the backward needs (forward-only renders). `lv` (a
+    _lib.SplatLevels) routes splats to levels (octave / coarse-fine renders, render_triton.py:879-980)."""
     _dev_check(mu, scale, color, opacity, theta)
     ev = kernel_timer.record("bin")
-    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps)
+    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv)
     kernel_timer.close("bin", ev)
     return bins
 
 
-def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps):
+def _budget_error(n, max_pairs, H, W, TILE, cutoff, N):
+    return PairBudgetExceeded(
+        f"_build_tiles: {n} (tile,gaussian) pairs exceeds the {max_pairs} budget @ {H}x{W} "
+        f"TILE={TILE} cutoff={cutoff} N={N}. Route large splats through the low-res (octave) pass "
+        f"instead of culling at full res. Refusing to allocate.")
+
+
+def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv):
     B, N, C = color.shape
     dev = mu.device
     lib = _lib.load()
+    lvr = None if lv is None else _lib.ctypes.byref(lv)
     mu_, sc_, col_, op_, th_ = _f32(mu), _f32(scale), _f32(color), _f32(opacity), _f32(theta)
-    ntx = (W + TILE - 1) // TILE
-    nt = ntx * ((H + TILE - 1) // TILE)
+    geom, nt, npix = levels_geometry(H, W, TILE, lv)
+    L = len(geom)
+    ntx = geom[0][2]
+    if lv is None:
+        geom = None
     stream = _lib.stream_ptr(dev)
     if N == 0:
-        return TileBins([_empty((0, 16), dev)] * B, [torch.zeros(1, dtype=torch.int32, device=dev)] * B,
-                        [torch.zeros(nt + 1, dtype=torch.int32, device=dev)] * B, [0] * B, H, W, TILE, ntx, nt)
-    info = torch.empty((B, 2), dtype=torch.int64, device=dev)
+        return TileBins([torch.zeros((1, 16), device=dev)] * B, [torch.zeros(1, dtype=torch.int32, device=dev)] * B,
+                        [torch.zeros(nt + 1, dtype=torch.int32, device=dev)] * B, [0] * B, H, W, TILE, ntx, nt,
+                        [torch.zeros(1, dtype=torch.int32, device=dev)] * B, [None] * B, [None] * B,
+                        lv, geom, npix, [[0] * L] * B, None)
+    info = torch.empty((B, 2 + L), dtype=torch.int64, device=dev)
     rec_b, rect_b, off_b = [], [], []
     ws1 = _ws(lib.splat_bin_count_workspace_bytes(N), dev)
     for b in range(B):
@@ -127,7 +179,7 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         rect = torch.empty((N, 4), dtype=torch.int32, device=dev)
         off = torch.empty(N + 1, dtype=torch.int32, device=dev)
         check(lib.splat_bin_count(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]),
-                                  ptr(col_[b]), C, N, H, W, TILE, float(cutoff), ptr(rec), ptr(rect), ptr(off),
+                                  ptr(col_[b]), C, N, H, W, TILE, float(cutoff), lvr, ptr(rec), ptr(rect), ptr(off),
                                   ptr(info[b]), ptr(ws1), ws1.numel(), stream), "splat_bin_count")
         rec_b.append(rec); rect_b.append(rect); off_b.append(off)
     info_h = info.cpu()                                                   # the one host sync of binning
@@ -136,13 +188,14 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     if bool((info_h[:, 1] & 2).any()):
         raise PairBudgetExceeded(f"binning: {int(info_h[:, 0].max())} pairs exceed the int32 pair index range")
     tots = [int(x) for x in info_h[:, 0]]
+    level_tots = [[int(x) for x in info_h[b, 2:2 + L]] for b in range(B)]
     if max_pairs is not None:
-        worst = max(tots)
-        if worst > max_pairs:
-            raise PairBudgetExceeded(
-                f"_build_tiles: {worst} (tile,gaussian) pairs exceeds the {max_pairs} budget @ {H}x{W} "
-                f"TILE={TILE} cutoff={cutoff} N={N}. Route large splats through the low-res (octave) pass "
-                f"instead of culling at full res. Refusing to allocate.")
+        # the reference checks each binned group (one canvas) per batch against the budget
+        for l in range(L):
+            worst = max(lt[l] for lt in level_tots)
+            if worst > max_pairs:
+                Hl, Wl = (H, W) if geom is None else geom[l][:2]
+                raise _budget_error(worst, max_pairs, Hl, Wl, TILE, cutoff, N)
     gid_b, starts_b, psplat_b, pinv_b = [], [], [], []
     for b in range(B):
         tot = tots[b]
@@ -151,10 +204,11 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         psplat = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
         pinv = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
         ws2 = _ws(lib.splat_bin_pairs_workspace_bytes(N, nt, tot), dev)
-        check(lib.splat_bin_pairs(ptr(rect_b[b]), ptr(off_b[b]), N, H, W, TILE, tot, ptr(gid), ptr(starts),
+        check(lib.splat_bin_pairs(ptr(rect_b[b]), ptr(off_b[b]), N, H, W, TILE, lvr, tot, ptr(gid), ptr(starts),
                                   ptr(psplat), ptr(pinv), ptr(ws2), ws2.numel(), stream), "splat_bin_pairs")
         gid_b.append(gid); starts_b.append(starts); psplat_b.append(psplat); pinv_b.append(pinv)
-    return TileBins(rec_b, gid_b, starts_b, tots, H, W, TILE, ntx, nt, off_b, psplat_b, pinv_b)
+    return TileBins(rec_b, gid_b, starts_b, tots, H, W, TILE, ntx, nt, off_b, psplat_b, pinv_b, lv, geom, npix,
+                    level_tots, rect_b)
 
 
 def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
@@ -166,6 +220,15 @@ def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
 
 
 # ----------------------------------------------------------------------------------------------- cull path
+def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
+    """splat_render_fwd for batch b over levels lev = (begin, end); comp = (bg, out, T, asum, fg) or Nones,
+    fields = (slog, sa, sac) or Nones."""
+    lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
+    check(lib.splat_render_fwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), C, bins.H, bins.W,
+                               bins.TILE, flags, lvr, lev[0], lev[1], mask, *[ptr(t) for t in comp],
+                               *[ptr(t) for t in fields], stream), "splat_render_fwd")
+
+
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False):
     """Composite forward (render_triton.py:538-567): out [B,P,C], (T, asum, fg), bins."""
     B, N, C = color.shape
@@ -178,9 +241,8 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     for b in range(B):
         ev = kernel_timer.record("fwd")
-        check(lib.splat_render_fwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), C, H, W, TILE,
-                                   flags, ptr(bgf[b]), ptr(out[b]), ptr(T[b]), ptr(asum[b]), ptr(fg[b]), None, None,
-                                   None, stream), "splat_render_fwd")
+        _render_fwd(lib, bins, b, C, flags, (0, 1), 1, (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None),
+                    stream)
         kernel_timer.close("fwd", ev)
     return out, (T, asum, fg), bins
 
@@ -195,13 +257,35 @@ def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     for b in range(B):
-        if N == 0:
-            slog[b].zero_(); sa[b].zero_(); sac[b].zero_()
-            continue
-        check(lib.splat_render_fwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), C, H, W, TILE,
-                                   flags, None, None, None, None, None, ptr(slog[b]), ptr(sa[b]), ptr(sac[b]), stream),
-              "splat_render_fwd")
+        _render_fwd(lib, bins, b, C, flags, (0, 1), 1, (None,) * 5, (slog[b], sa[b], sac[b]), stream)
     return slog, sa, sac, bins
+
+
+def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+    """Fused multi-level forward (render_triton.py:879-980 without the per-group torch glue): one binning
+    over every level, FIELDS renders of the coarse levels into packed fields, then the level-0 composite
+    adds their bilinear upsamples. Returns out [B,P,C], (T, asum unclamped, fg), bins."""
+    B, N, C = color.shape
+    P = H * W
+    dev = mu.device
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, lv=lv)
+    out, T, asum, fg = _empty((B, P, C), dev), _empty((B, P), dev), _empty((B, P), dev), _empty((B, P, C), dev)
+    L = bins.n_levels
+    # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
+    fl = (_empty((bins.npix,), dev), _empty((bins.npix,), dev), _empty((bins.npix, C), dev)) if L > 1 else \
+        (None, None, None)
+    bgf = _f32(bg)
+    odd = FLAG_ODDS if odds else 0
+    lib, stream = _lib.load(), _lib.stream_ptr(dev)
+    for b in range(B):
+        mask = bins.level_mask(b)
+        ev = kernel_timer.record("fwd")
+        if mask & ~1:
+            _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5, fl, stream)
+        _render_fwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], out[b], T[b], asum[b], fg[b]), fl,
+                    stream)
+        kernel_timer.close("fwd", ev)
+    return out, (T, asum, fg), bins
 
 
 def _grads_out(B, N, C, dev, has_th):
@@ -209,26 +293,41 @@ def _grads_out(B, N, C, dev, has_th):
             _empty((B, N), dev) if has_th else None)
 
 
-def _backward_pairs(bins, b, flags, C, H, W, TILE, upstream, grads, g_bg, lib, stream):
-    """Both backward steps for batch b: per-tile pair sums, then the per-splat reduction into `grads`."""
+def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stream):
+    """splat_render_bwd for batch b over levels lev = (begin, end); upstream = (bg, T, asum, fg, gout, dslog,
+    dsa, dsac) with Nones where unused."""
+    lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
+    check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), bins.tot_b[b], C,
+                               bins.H, bins.W, bins.TILE, flags, lvr, lev[0], lev[1], mask,
+                               *[ptr(u) for u in upstream], ptr(sums), ptr(bg_part), stream), "splat_render_bwd")
+
+
+def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream):
+    """Per-splat reduction of batch b's pair sums into `grads` (and g_bg from the level-0 tile partials)."""
     dev = bins.rec_b[b].device
     tot = bins.tot_b[b]
     N = bins.off_b[b].numel() - 1
-    sums = _empty((lib.splat_pair_sums_bytes(tot) // 4,), dev)
-    bg_part = _empty((C * bins.nt,), dev) if g_bg is not None else None
-    ev = kernel_timer.record("bwd")
-    check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), tot, C, H, W, TILE,
-                               flags, *[ptr(u) for u in upstream], ptr(sums), ptr(bg_part), stream),
-          "splat_render_bwd")
-    kernel_timer.close("bwd", ev)
     ev = kernel_timer.record("reduce")
     ws = _ws(lib.splat_reduce_workspace_bytes(tot), dev)
     g_mu, g_scale, g_col, g_op, g_th = grads
-    check(lib.splat_reduce_pairs(ptr(bins.rec_b[b]), ptr(bins.off_b[b]), ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]),
-                                 tot, N, C, ptr(sums), ptr(bg_part), bins.nt, ptr(g_mu[b]), ptr(g_scale[b]),
-                                 None if g_th is None else ptr(g_th[b]), ptr(g_op[b]), ptr(g_col[b]), ptr(g_bg),
+    sl = lambda t: None if (t is None or N == 0) else ptr(t[b])
+    check(lib.splat_reduce_pairs(ptr(bins.rec_b[b]) if N else None, ptr(bins.off_b[b]) if N else None,
+                                 ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), tot, N, C, ptr(sums), ptr(bg_part),
+                                 bins.ntiles0, sl(g_mu), sl(g_scale), sl(g_th), sl(g_op), sl(g_col), ptr(g_bg),
                                  ptr(ws), ws.numel(), stream), "splat_reduce_pairs")
     kernel_timer.close("reduce", ev)
+
+
+def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream):
+    """Both backward steps for batch b of a single-level render: per-tile pair sums, then the per-splat
+    reduction into `grads`."""
+    dev = bins.rec_b[b].device
+    sums = _empty((lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4,), dev)
+    bg_part = _empty((C * bins.nt,), dev) if g_bg is not None else None
+    ev = kernel_timer.record("bwd")
+    _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
+    kernel_timer.close("bwd", ev)
+    _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream)
 
 
 def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, bins, H, W, TILE=8, odds=False):
@@ -242,7 +341,7 @@ def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, 
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
         up = (bgf[b], T[b], asum[b], fg[b], go[b], None, None, None)
-        _backward_pairs(bins, b, flags, C, H, W, TILE, up, grads, g_bg[b], lib, stream)
+        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream)
     g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
@@ -259,8 +358,42 @@ def _backward_cull_fields(dS_log, dS_a, dS_ac, mu, scale, color, opacity, theta,
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     for b in range(B):
         up = (None, None, None, None, None, dl[b], da[b], dc[b])
-        _backward_pairs(bins, b, flags, C, H, W, TILE, up, grads, None, lib, stream)
+        _backward_pairs(bins, b, flags, C, up, grads, None, lib, stream)
     return grads
+
+
+def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds):
+    """Backward of _forward_levels: level-0 composite backward (clamp_min gradient of S_a, render_triton.py
+    :918 / :976) writing the pixel upstream, its exact adjoint through the upsample onto the coarse levels,
+    their FIELDS backward, then one per-splat reduction over the pairs of every level."""
+    B, N, C = color.shape
+    dev = color.device
+    grads = _grads_out(B, N, C, dev, has_theta)
+    g_bg = _empty((B, C), dev)
+    go, bgf = _f32(grad_out), _f32(bg)
+    lib, stream = _lib.load(), _lib.stream_ptr(dev)
+    odd = FLAG_ODDS if odds else 0
+    L = bins.n_levels
+    npix = bins.npix if L > 1 else bins.H * bins.W
+    dS = (_empty((npix,), dev), _empty((npix,), dev), _empty((npix, C), dev))    # reused across the batch
+    lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
+    adj_ws = _ws(lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr), dev) if L > 1 \
+        else None
+    for b in range(B):
+        mask = bins.level_mask(b)
+        sums = _empty((lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4,), dev)
+        bg_part = _empty((C * bins.ntiles0,), dev)
+        ev = kernel_timer.record("bwd")
+        _render_bwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], T[b], asum[b], fg[b], go[b], *dS), sums,
+                    bg_part, stream)
+        if mask & ~1:
+            check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
+                                             ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
+            _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5 + dS, sums, None, stream)
+        kernel_timer.close("bwd", ev)
+        _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream)
+    g_mu, g_scale, g_col, g_op, g_th = grads
+    return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
 class _AlphaRenderCull(torch.autograd.Function):
@@ -314,6 +447,28 @@ class _AlphaRenderCullFields(torch.autograd.Function):
         g_mu, g_scale, g_col, g_op, g_th = _backward_cull_fields(dS_log, dS_a, dS_ac, mu, scale, color, opacity, th,
                                                                  ctx.tiles, H, W, TILE, odds=ctx.odds)
         return g_mu, g_scale, g_col, g_op, g_th, None, None, None, None, None, None
+
+
+class _AlphaRenderLevels(torch.autograd.Function):
+    """Fused octave / coarse-fine render (render_triton.py:879-980) with the levels described by `lv`:
+    inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv) -> out [B,P,C]."""
+
+    @staticmethod
+    def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+        out, (T, asum, fg), bins = _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff,
+                                                   max_pairs, odds, lv)
+        ctx.has_theta = theta is not None
+        ctx.odds = odds
+        ctx.tiles = bins
+        ctx.save_for_backward(color, bg, T, asum, fg)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        color, bg, T, asum, fg = ctx.saved_tensors
+        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(grad_out, color, bg, ctx.has_theta, T, asum, fg,
+                                                                  ctx.tiles, ctx.odds)
+        return (g_mu, g_scale, g_col, g_op, g_bg, g_th) + (None,) * 7
 
 
 # ----------------------------------------------------------------------------------------------- exact path
@@ -424,30 +579,25 @@ def _composite_fields(slog, sa, sac, bg, B, H, W, C):
     return img.reshape(B, H, W, C).permute(0, 3, 1, 2)
 
 
+def _multires_levels(H, W, N, n_coarse, coarse_factor):
+    """render_triton.py:896-913: the coarse group [0, n_coarse) renders on (H // cf, W // cf) with
+    cf = min(coarse_factor, max(1, min(H, W) // 8)); without a split every splat renders at (H, W)."""
+    if n_coarse is None or n_coarse <= 0 or n_coarse >= N:
+        return SplatLevels(0, 0, 0.0, 0, 0, 0)
+    cf = min(coarse_factor, max(1, min(H, W) // 8))
+    return SplatLevels(2, 0, 0.0, int(n_coarse), max(1, H // cf), max(1, W // cf))
+
+
 def render_alpha_multires(mu, log_scale, color, opacity, bg, H, W, theta=None, n_coarse=None, coarse_factor=8,
                           cutoff=3.0, TILE=8, max_pairs=48_000_000, odds=False):
     """render_triton.py:879-922: coarse group [0, n_coarse) at H/cf, fine group at native resolution; the
-    fields are summed (bilinear upsample of the coarse ones) and composited once."""
+    fields are summed (bilinear upsample of the coarse ones) and composited once. Fused: one binning over
+    both canvases and one composite kernel that upsamples the coarse fields in its epilogue."""
     B, N, C = color.shape
     scale = activate_scale(log_scale)
-    has_th = theta is not None
-
-    def fields(lo, hi, H_, W_):
-        th = theta[:, lo:hi] if has_th else None
-        return _AlphaRenderCullFields.apply(mu[:, lo:hi], scale[:, lo:hi], color[:, lo:hi], opacity[:, lo:hi], th,
-                                            H_, W_, TILE, cutoff, max_pairs, odds)
-
-    if n_coarse is None or n_coarse <= 0 or n_coarse >= N:
-        slog, sa, sac = fields(0, N, H, W)
-    else:
-        cf = min(coarse_factor, max(1, min(H, W) // 8))
-        Hc = max(1, H // cf); Wc = max(1, W // cf)
-        slc, sac_a, sac_c = fields(0, n_coarse, Hc, Wc)
-        slf, saf, sacf = fields(n_coarse, N, H, W)
-        slog = slf + _upsample_field(slc, Hc, Wc, H, W)
-        sa = saf + _upsample_field(sac_a, Hc, Wc, H, W)
-        sac = sacf + _upsample_field(sac_c, Hc, Wc, H, W)
-    return _composite_fields(slog, sa, sac, bg, B, H, W, C)
+    lv = _multires_levels(H, W, N, n_coarse, coarse_factor)
+    out = _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
+    return out.reshape(B, H, W, C).permute(0, 3, 1, 2)
 
 
 def _octave_of(scale_px, base_texels=8.0, max_octaves=6):
@@ -456,35 +606,24 @@ def _octave_of(scale_px, base_texels=8.0, max_octaves=6):
     return o.clamp(0, max_octaves).to(torch.int64)
 
 
+def _octave_levels(H, W, base_texels, max_octaves):
+    if min(H, W) < 8:
+        raise ValueError(f"render_alpha_octave: octave 0 renders on (max(8, H), max(8, W)), which needs H, W >= 8 "
+                         f"(got {H}x{W})")
+    if max_octaves < 0:
+        raise ValueError(f"render_alpha_octave: max_octaves={max_octaves} < 0")
+    return SplatLevels(1, int(max_octaves), float(base_texels), 0, 0, 0)
+
+
 def render_alpha_octave(mu, log_scale, color, opacity, bg, H, W, theta=None, cutoff=3.0, TILE=8, base_texels=8.0,
                         max_octaves=6, max_pairs=48_000_000, odds=False):
     """render_triton.py:935-980: each splat renders at the octave H/2^o where its footprint spans a bounded
-    number of tiles; octave fields are upsampled to (H, W), summed and composited once."""
+    number of tiles; octave fields are upsampled to (H, W), summed and composited once. Fused: the routing
+    happens in the binning pass, every octave shares one pair list, and the level-0 composite kernel
+    upsamples the coarse octaves' fields in its epilogue (octaves whose canvas is clamped to 8x8 share one
+    level, which sums the same fields)."""
     B, N, C = color.shape
     scale = activate_scale(log_scale)
-    has_th = theta is not None
-    rep = float(min(H, W))
-    scale_px = scale.detach().amax(-1) * rep
-    oct = _octave_of(scale_px, base_texels, max_octaves)
-    P = H * W
-    slog_l, sa_l, sac_l = [], [], []
-    for b in range(B):
-        slog_b = mu.new_zeros(P); sa_b = mu.new_zeros(P); sac_b = mu.new_zeros(P, C)
-        ob = oct[b]
-        for o in range(max_octaves + 1):
-            idx = (ob == o).nonzero(as_tuple=True)[0]
-            if idx.numel() == 0:
-                continue
-            Ho = max(8, H >> o); Wo = max(8, W >> o)
-            m = mu[b:b + 1, idx]; s = scale[b:b + 1, idx]; cl = color[b:b + 1, idx]
-            op_ = opacity[b:b + 1, idx]; th = theta[b:b + 1, idx] if has_th else None
-            sl, saa, sc = _AlphaRenderCullFields.apply(m, s, cl, op_, th, Ho, Wo, TILE, cutoff, max_pairs, odds)
-            if o == 0:
-                slog_b = slog_b + sl[0]; sa_b = sa_b + saa[0]; sac_b = sac_b + sc[0]
-            else:
-                slog_b = slog_b + _upsample_field(sl, Ho, Wo, H, W)[0]
-                sa_b = sa_b + _upsample_field(saa, Ho, Wo, H, W)[0]
-                sac_b = sac_b + _upsample_field(sc, Ho, Wo, H, W)[0]
-        slog_l.append(slog_b); sa_l.append(sa_b); sac_l.append(sac_b)
-    slog = torch.stack(slog_l); sa = torch.stack(sa_l); sac = torch.stack(sac_l)
-    return _composite_fields(slog, sa, sac, bg, B, H, W, C)
+    lv = _octave_levels(H, W, base_texels, max_octaves)
+    out = _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
+    return out.reshape(B, H, W, C).permute(0, 3, 1, 2)

@@ -26,6 +26,31 @@ extern "C" {
 
 #define SPLAT_FLAG_FIELDS 1 /* forward writes raw sums (S_log, S_a, S_ac); backward takes dS_* upstream */
 #define SPLAT_FLAG_ODDS 2   /* colour weight a/(1-a) instead of a */
+#define SPLAT_FLAG_UPS 4    /* composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a */
+
+/* Levels of a render. A NULL splat_levels* (or mode 0) is the single canvas (H, W). Otherwise splats are
+ * routed to canvases ("levels"): level 0 is (H, W); coarser levels are rendered into packed fields and
+ * bilinearly upsampled (torch upsample_bilinear2d, align_corners=False) onto level 0 before compositing.
+ *   mode 1, octaves (render_triton.py:925-980): level o in 0..max_octaves is (max(8, H>>o), max(8, W>>o))
+ *     (H, W >= 8); splat goes to o = clamp(ceil(log2(max(max(sy, sx) * min(H, W) / base_texels, 1e-6))),
+ *     0, max_octaves), computed in fp32 from the activated scale. Octaves from the first whose canvas is
+ *     (8, 8) on share one level (their fields are summed after the same upsample); H, W <= 8 << 11.
+ *   mode 2, coarse/fine split (render_triton.py:879-922): splats [0, n_coarse) render on
+ *     (coarse_H, coarse_W) as level 1, the rest on (H, W).
+ * Level l takes global tile ids [tbase[l], tbase[l+1]) and packed pixel slots [pbase[l], pbase[l+1]) of
+ * the FIELDS buffers; splat_levels_geometry reports them. */
+typedef struct splat_levels {
+  int mode;
+  int max_octaves;
+  float base_texels;
+  int n_coarse;
+  int coarse_H, coarse_W;
+} splat_levels;
+
+/* Number of levels L (or a negative status). With out != NULL (cap >= 5L+2 ints) writes, per level l,
+ * out[5l..5l+4] = (H_l, W_l, tiles per row, tbase[l], pbase[l]) and then total tiles, total pixel slots.
+ * Replaces the per-octave canvas sizes of render_triton.py:957-961 and :896-898. */
+int splat_levels_geometry(int H, int W, int TILE, const splat_levels *lv, int *out, int cap);
 
 const char *splat_last_error(void);
 int splat_abi_version(void);
@@ -35,52 +60,74 @@ int splat_abi_version(void);
 int splat_decode(const float *mu, const float *scale, const float *theta, const float *opacity,
                  const float *color, int C, int N, float *rec, void *stream);
 
-/* Binning phase 1: decode + per-splat tile rect and pair count + exclusive scan of the counts.
- * Writes rec[N,16], rect[N,4] = (tx0, ty0, w, h), offsets[N+1] (offsets[N] = total pairs) and
- * info[2] (device int64): info[0] = total pairs, info[1] = error bits (1 empty rect, 2 int32 overflow).
- * The caller reads info once to size the pair buffers and to apply its pair budget.
- * Replaces render_triton.py:362-391 (_build_tiles up to the tot sync) and :520-535 (param gathers). */
+/* Binning phase 1: decode + level routing + per-splat tile rect and pair count + exclusive scan.
+ * Writes rec[N,16], rect[N,4] = (tx0, ty0, w, level) of the splat's tile rect, offsets[N+1]
+ * (offsets[N] = total pairs) and info[2 + L] (device int64): info[0] = total pairs, info[1] = error bits
+ * (1 empty rect, 2 int32 overflow), info[2 + l] = pairs of level l (L = number of levels).
+ * The caller reads info once to size the pair buffers and to apply its pair budget per level.
+ * Replaces render_triton.py:362-391 (_build_tiles up to the tot sync), :520-535 (param gathers) and the
+ * octave routing / index_select of :950-962. */
 size_t splat_bin_count_workspace_bytes(int N);
 int splat_bin_count(const float *mu, const float *scale, const float *theta, const float *opacity,
-                    const float *color, int C, int N, int H, int W, int TILE, float cutoff, float *rec,
-                    int *rect, int *offsets, long long *info, void *ws, size_t ws_bytes, void *stream);
+                    const float *color, int C, int N, int H, int W, int TILE, float cutoff,
+                    const splat_levels *lv, float *rec, int *rect, int *offsets, long long *info, void *ws,
+                    size_t ws_bytes, void *stream);
 
-/* Binning phase 2: expand rects into pairs, stable radix sort on the tile id, CSR tile starts.
- * gid_sorted[max(tot,1)] lists splat ids ordered by (tile, splat id); tile_starts[nt+1].
+/* Binning phase 2: expand rects into pairs, stable radix sort on the global tile id, CSR tile starts.
+ * gid_sorted[max(tot,1)] lists splat ids ordered by (tile, splat id); tile_starts[nt+1] with nt the total
+ * tile count over all levels (splat_levels_geometry).
  * tot == 0 gives gid_sorted = {0} and all-zero starts, as the reference does.
  * Optional (NULL skips) maps over the splat-major pair order q (splat g owns q in [offsets[g], offsets[g+1])),
  * used by the backward's per-splat reduction: pair_splat[tot] = splat of q, pair_inv[tot] = sorted position
  * of q.
  * Replaces render_triton.py:392-409. */
 size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot);
-int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, int TILE, long long tot,
-                    int *gid_sorted, int *tile_starts, int *pair_splat, int *pair_inv, void *ws,
-                    size_t ws_bytes, void *stream);
+int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, int TILE,
+                    const splat_levels *lv, long long tot, int *gid_sorted, int *tile_starts,
+                    int *pair_splat, int *pair_inv, void *ws, size_t ws_bytes, void *stream);
 
-/* Per-tile forward compositing over the binned pairs (TILE in {4, 8, 16}).
- * Composite (flags without FIELDS): out[P,C], T[P], asum[P], fg[P,C] with background bg[C].
- * FIELDS: slog[P], sa[P] (unclamped), sac[P,C]; every pixel is written, empty tiles get zeros.
- * Replaces _render_fwd_cull_kernel, render_triton.py:423-517 (+ launch loops :538-599). */
+/* Per-tile forward over the binned pairs of levels [lev_begin, lev_end) (TILE in {4, 8, 16}); levels
+ * whose bit in levmask is clear are skipped (their pixels are not written).
+ * Composite (no FIELDS; levels [0, 1) only): out[P,C], T[P], asum[P], fg[P,C] with background bg[C],
+ * P = H*W. With UPS, the masked coarse levels' packed fields slog/sa/sac (inputs, written by an earlier
+ * FIELDS call) are upsampled and added before compositing, and asum holds the unclamped S_a.
+ * FIELDS: raw sums into the packed fields slog[Pt], sa[Pt] (unclamped), sac[Pt,C] at slot pbase[l] + p.
+ * Replaces _render_fwd_cull_kernel, render_triton.py:423-517 (+ launch loops :538-599), and the
+ * per-octave render + upsample + sum + composite of render_triton.py:864-876, :900-918, :962-978. */
 int splat_render_fwd(const float *rec, const int *gid_sorted, const int *tile_starts, int C, int H, int W,
-                     int TILE, int flags, const float *bg, float *out, float *T, float *asum, float *fg,
+                     int TILE, int flags, const splat_levels *lv, int lev_begin, int lev_end,
+                     unsigned levmask, const float *bg, float *out, float *T, float *asum, float *fg,
                      float *slog, float *sa, float *sac, void *stream);
 
-/* Backward, step 1: per-tile kernel over the same pairs. For every pair (sorted position i) it sums over
- * the tile's pixels the terms the parameter gradients need and stores them in pair_sums[i] (12 floats,
- * splat_pair_sums_bytes). Composite: upstream gout[P,C] with the forward's T, asum, fg and bg; with
- * bg_part set ([C, nt] floats) it also writes per-tile partials of sum_p gout*T. FIELDS: upstream
- * dslog[P], dsa[P], dsac[P,C] (bg_part must be NULL).
- * Replaces _render_bwd_cull_kernel, render_triton.py:602-720 (per-pair grads, :612-614). */
+/* Backward, step 1: per-tile kernel over the pairs of levels [lev_begin, lev_end) (levmask as in the
+ * forward). For every pair (sorted position i) it sums over the tile's pixels the terms the parameter
+ * gradients need and stores them in pair_sums[i] (12 floats, splat_pair_sums_bytes).
+ * Composite (levels [0, 1)): upstream gout[P,C] with the forward's T, asum, fg and bg; with bg_part set
+ * ([C, ntiles0] floats, ntiles0 = level 0's tiles) it also writes per-tile partials of sum_p gout*T.
+ * With UPS the S_a gradient is torch's clamp_min one (zero where S_a < 1e-8) and the pixel upstream
+ * dS_log, dS_a, dS_ac is also written to dslog/dsa/dsac[0, P) for splat_upsample_adjoint.
+ * FIELDS: upstream from the packed dslog[Pt], dsa[Pt], dsac[Pt,C] (bg_part must be NULL).
+ * Replaces _render_bwd_cull_kernel, render_triton.py:602-720 (per-pair grads, :612-614), and the autograd
+ * of the octave / coarse-fine composite, render_triton.py:918, :976-978. */
 size_t splat_pair_sums_bytes(long long tot);
 int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, long long tot, int C,
-                     int H, int W, int TILE, int flags, const float *bg, const float *T, const float *asum,
-                     const float *fg, const float *gout, const float *dslog, const float *dsa,
-                     const float *dsac, float *pair_sums, float *bg_part, void *stream);
+                     int H, int W, int TILE, int flags, const splat_levels *lv, int lev_begin, int lev_end,
+                     unsigned levmask, const float *bg, const float *T, const float *asum, const float *fg,
+                     const float *gout, float *dslog, float *dsa, float *dsac, float *pair_sums,
+                     float *bg_part, void *stream);
+
+/* Backward of the upsample: the exact adjoint of the bilinear upsample of every masked coarse level,
+ * from the level-0 upstream dslog/dsa/dsac[0, P) into the coarse levels' packed slots, deterministic
+ * (two gather passes, no atomics). Replaces the autograd of F.interpolate at render_triton.py:864-876. */
+size_t splat_upsample_adjoint_workspace_bytes(int C, int H, int W, int TILE, const splat_levels *lv);
+int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels *lv, unsigned levmask,
+                           float *dslog, float *dsa, float *dsac, void *ws, size_t ws_bytes, void *stream);
 
 /* Backward, step 2: per-splat reduction of the pair sums into parameter gradients, written (not
  * accumulated), deterministic, no global atomics. Takes the binning's offsets, pair_splat and pair_inv.
  * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
- * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = nt per-tile partials of step 1.
+ * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = ntiles0 per-tile partials of step 1.
+ * One call covers the pairs of every level.
  * Replaces the index_add_ scatter and the g_bg reduction, render_triton.py:723-810. */
 size_t splat_reduce_workspace_bytes(long long tot);
 int splat_reduce_pairs(const float *rec, const int *offsets, const int *pair_splat, const int *pair_inv,

@@ -1,5 +1,6 @@
 """The C-ABI library loads on the CPU host and exports exactly what include/splat_render.h declares."""
 
+import ctypes
 import os
 import re
 
@@ -37,13 +38,68 @@ def test_workspace_queries_without_gpu():
 
 def test_invalid_arguments_are_reported_not_launched():
     lib = _lib.load()
-    rc = lib.splat_render_fwd(None, None, None, 3, 64, 64, 8, 0, None, None, None, None, None, None, None, None, None)
+    rc = lib.splat_render_fwd(None, None, None, 3, 64, 64, 8, 0, None, 0, 1, 1, None, None, None, None, None, None,
+                              None, None, None)
     assert rc == 1
     assert b"null" in lib.splat_last_error()
     with pytest.raises(_lib.SplatError, match="invalid argument"):
         _lib.check(rc, "splat_render_fwd")
-    assert lib.splat_bin_count(None, None, None, None, None, 9, 10, 8, 8, 8, 3.0, None, None, None, None, None, 0,
-                               None) == 1
+    assert lib.splat_bin_count(None, None, None, None, None, 9, 10, 8, 8, 8, 3.0, None, None, None, None, None,
+                               None, 0, None) == 1
+    oct6 = ctypes.byref(_lib.SplatLevels(1, 6, 8.0, 0, 0, 0))
+    # the composite renders level 0 only; FIELDS and UPS exclude each other; level range inside the table
+    assert lib.splat_render_fwd(None, None, None, 3, 64, 64, 8, 0, oct6, 1, 2, 3, *[None] * 9) == 1
+    assert b"level 0" in lib.splat_last_error()
+    assert lib.splat_render_fwd(None, None, None, 3, 64, 64, 8, 5, oct6, 0, 1, 3, *[None] * 9) == 1
+    assert b"exclude" in lib.splat_last_error()
+    assert lib.splat_render_bwd(None, None, None, 0, 3, 64, 64, 8, 1, oct6, 1, 9, 3, *[None] * 11) == 1
+    assert b"outside" in lib.splat_last_error()
+    # octave 0 must be the native canvas
+    assert lib.splat_levels_geometry(4, 64, 8, oct6, None, 0) < 0
+
+
+def geometry(H, W, TILE, lv):
+    from gaussian_splat_encoder.render_hip import levels_geometry
+    return levels_geometry(H, W, TILE, lv)
+
+
+def test_octave_levels_geometry():
+    """Level o of an octave render is (max(8, H >> o), max(8, W >> o)) (render_triton.py:957), tiled by
+    TILE; tile ids and packed pixel slots are concatenated level by level."""
+    for H, W, TILE, mo in [(768, 768, 8, 6), (100, 37, 8, 3), (64, 512, 16, 6), (2048, 2048, 8, 6)]:
+        geom, nt, npix = geometry(H, W, TILE, _lib.SplatLevels(1, mo, 8.0, 0, 0, 0))
+        tb = pb = 0
+        assert len(geom) == mo + 1
+        for o, (h, w, ntx, tbase, pbase) in enumerate(geom):
+            assert (h, w) == (max(8, H >> o), max(8, W >> o))
+            assert ntx == -(-w // TILE) and tbase == tb and pbase == pb
+            tb += ntx * -(-h // TILE)
+            pb += h * w
+        assert (nt, npix) == (tb, pb)
+
+
+def test_octave_levels_merge_clamped_canvases():
+    """Octaves past the first (8, 8) canvas render on the same canvas; they collapse into one level."""
+    geom, _, _ = geometry(64, 64, 8, _lib.SplatLevels(1, 10, 8.0, 0, 0, 0))
+    assert [g[:2] for g in geom] == [(64, 64), (32, 32), (16, 16), (8, 8)]
+    geom, _, _ = geometry(8, 8, 8, _lib.SplatLevels(1, 6, 8.0, 0, 0, 0))
+    assert [g[:2] for g in geom] == [(8, 8)]
+
+
+def test_split_and_single_levels_geometry():
+    geom, nt, npix = geometry(96, 80, 8, _lib.SplatLevels(2, 0, 0.0, 10, 12, 10))
+    assert [g[:2] for g in geom] == [(96, 80), (12, 10)]
+    assert nt == 12 * 10 + 2 * 2 and npix == 96 * 80 + 120
+    geom, nt, npix = geometry(33, 17, 8, None)
+    assert geom == [(33, 17, 3, 0, 0)] and nt == 15 and npix == 33 * 17
+
+
+def test_upsample_adjoint_workspace():
+    lib = _lib.load()
+    lv = _lib.SplatLevels(1, 6, 8.0, 0, 0, 0)
+    # (2 + C) terms x H0 rows x the coarse levels' columns
+    cols = sum(max(8, 768 >> o) for o in range(1, 7))
+    assert lib.splat_upsample_adjoint_workspace_bytes(3, 768, 768, 8, ctypes.byref(lv)) >= 4 * 5 * 768 * cols
 
 
 def test_host_rejects_cpu_tensors():
