@@ -1,13 +1,14 @@
 // Splat -> tile binning on gfx950, bit-exact with render_triton.py:351-409 (`_build_tiles`):
 //   k_decode_count   one coalesced pass over the splat parameters: the decoded render record, the tile
 //                    rect and the pair count of every splat, and per-block count sums
-//   k_scan_sums /    exclusive scan of the counts into per-splat pair offsets (offsets[N] = tot)
-//   k_offsets
+//   k_offsets_fused  exclusive scan of the counts into per-splat pair offsets (offsets[N] = tot);
+//                    k_scan_sums + k_offsets beyond kFusedScanBlocks blocks
 //   k_scatter_pairs  load-balanced expansion of every splat's rect into (tile, splat) pairs, splat-major
 //                    as the reference generates them (:396-404), fused with the first radix histogram
 //   k_radix_*        stable LSD radix sort on the tile id, splat id as the value: within a tile the
 //                    splats keep ascending order, the order of the reference's stable argsort (:405-407)
-//   k_tile_starts    CSR starts: starts[t] = number of pairs with tile < t (:408)
+//   k_tile_starts_q  CSR starts: starts[t] = number of pairs with tile < t (:408), and the map from
+//                    sorted position to splat-major pair index the backward stores by
 //
 // This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
 // operation separately (a fused mu*W - r*W changes floor() near tile edges).
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums
   if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
 }
 
-// counts -> exclusive offsets in place; offsets[N] = total.
+// counts -> exclusive offsets in place; offsets[N] = total. Block prefixes come from k_scan_sums.
 __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, const long long* __restrict__ block_pre,
                                                     int N, const long long* __restrict__ info) {
   __shared__ int s_w[kWaves];
@@ -184,6 +185,70 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, c
   if (g == N - 1) offsets[N] = (int)info[0];
 }
 
+// counts -> exclusive offsets in place without a separate scan launch (for up to kFusedScanBlocks blocks):
+// every block sums its predecessors' block totals itself (L2-resident, at most a few thousand loads per
+// block). The last block also writes info: total pairs, error bits and the per-level totals (l < nlev).
+constexpr int kFusedScanBlocks = 4096;
+
+__global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offsets,
+                                                          const long long* __restrict__ sums, int N, int nb,
+                                                          int nlev, long long* __restrict__ info) {
+  __shared__ long long s_r[kWaves];
+  __shared__ long long s_lev[kMaxLevels];
+  __shared__ int s_w[kWaves];
+  __shared__ int s_bad;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int blk = blockIdx.x;
+  const bool last = blk == nb - 1;
+  if (threadIdx.x == 0) s_bad = 0;
+  if (threadIdx.x < kMaxLevels) s_lev[threadIdx.x] = 0;
+  // prefix over predecessors (all blocks for the last one, to get the total and the error bits)
+  long long acc = 0;
+  int bad = 0;
+  const int upto = last ? nb : blk;
+  for (int b = threadIdx.x; b < upto; b += kBlock) {
+    const long long v = sums[(size_t)b * kSumCols];
+    if (b < blk) acc += v & ~kBadBit;
+    bad |= (v & kBadBit) ? 1 : 0;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (lane == 0) s_r[wv] = acc;
+  __syncthreads();
+  if (bad) atomicOr(&s_bad, 1);
+  long long pre_blk = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) pre_blk += s_r[w];
+  const int g = blk * kBlock + threadIdx.x;
+  const int c = g < N ? offsets[g] : 0;
+  const int inc = wave_incl_scan(c, lane);
+  if (lane == 63) s_w[wv] = inc;
+  __syncthreads();
+  int pre = 0, btot = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < wv) pre += s_w[i];
+    btot += s_w[i];
+  }
+  if (g < N) offsets[g] = (int)(pre_blk + pre + inc - c);   // garbage only when the total overflows int32
+  if (!last) return;
+  const long long tot = pre_blk + btot;
+  if (g == N - 1) offsets[N] = (int)tot;
+  for (int l = 0; l < nlev; ++l) {
+    long long x = 0;
+    for (int b = threadIdx.x; b < nb; b += kBlock) x += sums[(size_t)b * kSumCols + 1 + l];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+    if (lane == 0 && x) atomicAdd((unsigned long long*)&s_lev[l], (unsigned long long)x);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    info[0] = tot;
+    info[1] = (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0);
+  }
+  if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
+}
+
 // ----------------------------------------------------------------------------------------------------
 // pair expansion (render_triton.py:396-404): pair p belongs to the last splat g with offsets[g] <= p, and
 // k = p - offsets[g] walks that splat's rect row by row.
@@ -191,6 +256,30 @@ __device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (a[mid] <= p) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Block-cooperative last_le over a[0, n): 256 samples per round narrow the bracket 256-fold, so the
+// search costs ceil(log256 n) rounds of one load per thread instead of log2 n dependent loads.
+// Requires a[0] <= p. Every thread must call it; all get the result.
+__device__ __forceinline__ int block_last_le(const int* __restrict__ a, int n, int p, int* s_w) {
+  int lo = 0, hi = n - 1;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  while (hi > lo) {
+    const int step = (hi - lo + kBlock) / kBlock;          // ceil((hi - lo + 1) / kBlock)
+    const int idx = lo + (int)threadIdx.x * step;
+    const bool ok = idx <= hi && a[idx] <= p;               // true for a prefix of the threads (t = 0 always)
+    const unsigned long long m = __ballot(ok);
+    if (lane == 0) s_w[wv] = __popcll(m);
+    __syncthreads();
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) cnt += s_w[w];
+    __syncthreads();
+    const int nlo = lo + (cnt - 1) * step;
+    hi = min(hi, nlo + step - 1);
+    lo = nlo;
   }
   return lo;
 }
@@ -233,18 +322,14 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
   __shared__ int4 s_own4[kSortKeys / 4];
   __shared__ int s_hist[256];
   __shared__ int s_w[kWaves];
-  __shared__ int s_rng[2];
   int* s_own = reinterpret_cast<int*>(s_own4);
   const int p_base = blockIdx.x * kSortKeys;
   const int n_here = min(kSortKeys, tot - p_base);
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
   for (int i = threadIdx.x; i < kSortKeys / 4; i += kBlock) s_own4[i] = make_int4(-1, -1, -1, -1);
-  if (threadIdx.x == 0) {
-    s_rng[0] = last_le(offsets, 0, N - 1, p_base);
-    s_rng[1] = last_le(offsets, 0, N - 1, p_base + n_here - 1);
-  }
+  const int glo = block_last_le(offsets, N, p_base, s_w);
+  const int ghi = block_last_le(offsets, N, p_base + n_here - 1, s_w);
   __syncthreads();
-  const int glo = s_rng[0], ghi = s_rng[1];
   for (int g = glo + (int)threadIdx.x; g <= ghi; g += kBlock) {
     const int o0 = offsets[g], o1 = offsets[g + 1];
     if (o1 > o0) atomicMax(&s_own[max(o0, p_base) - p_base], g);   // o0 <= offsets[ghi] <= last pair here
@@ -331,15 +416,19 @@ __global__ __launch_bounds__(kBlock) void k_hist_row_scan(int* __restrict__ hist
 
 // Stable scatter of one radix pass. Wave w of the block owns keys [base + w*1024, base + (w+1)*1024) and
 // walks them 64 at a time in index order; lanes holding the same digit are ranked among themselves with
-// ballots (lane order = index order), on top of the wave's running count for that digit. Wave counts are
-// then prefixed across the waves; the block's base for a digit is the digit's global start (prefix of the
-// row totals) plus the block's offset within the digit (the row-scanned histogram).
+// ballots (lane order = index order), on top of the wave's running count for that digit. The block's keys
+// are then placed in LDS in (digit, index) order and written out by consecutive threads, so each digit's
+// run of the block lands in consecutive global positions: the digit's global start (prefix of the row
+// totals) plus the block's offset within the digit (the row-scanned histogram).
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
                                                           int tot, int shift, int dbits, const int* __restrict__ hist_scan,
                                                           const int* __restrict__ rowtot, int nblocks,
                                                           int* __restrict__ keys_out, int* __restrict__ vals_out) {
   __shared__ int s_cnt[kWaves][256];
-  __shared__ int s_base[256];
+  __shared__ int s_gbase[256];    // global position of the block's first key with digit d
+  __shared__ int s_lbase[256];    // LDS position of the block's first key with digit d
+  __shared__ int s_key[kSortKeys];
+  __shared__ int s_val[kSortKeys];
   __shared__ int s_w[kWaves];
   const int dmask = (1 << dbits) - 1;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -349,11 +438,13 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     const int rt = d <= dmask ? rowtot[d] : 0;
     int total;
     const int dstart = block256_excl<false>(rt, s_w, total);
-    if (d <= dmask) s_base[d] = dstart + hist_scan[d * nblocks + blockIdx.x];
+    if (d <= dmask) s_gbase[d] = dstart + hist_scan[d * nblocks + blockIdx.x];
   }
   __syncthreads();
   const unsigned long long lt = (1ull << lane) - 1ull;
-  const int p0 = blockIdx.x * kSortKeys + wv * kWaveKeys + lane;
+  const int p_base = blockIdx.x * kSortKeys;
+  const int n_here = min(kSortKeys, tot - p_base);
+  const int p0 = p_base + wv * kWaveKeys + lane;
   int key[kItems], val[kItems], rank[kItems];
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
@@ -378,29 +469,43 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     rank[j] = before + below;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d <= dmask; d += kBlock) {
-    int run = s_base[d];
-    for (int w = 0; w < kWaves; ++w) { const int c = s_cnt[w][d]; s_cnt[w][d] = run; run += c; }
+  {
+    // per digit: wave offsets within the block's run of that digit, and the run's LDS start
+    const int d = threadIdx.x;
+    int run = 0;
+    if (d <= dmask)
+      for (int w = 0; w < kWaves; ++w) { const int c = s_cnt[w][d]; s_cnt[w][d] = run; run += c; }
+    int total;
+    const int lstart = block256_excl<false>(d <= dmask ? run : 0, s_w, total);
+    if (d <= dmask) s_lbase[d] = lstart;
   }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     if (p0 + j * 64 >= tot) continue;
     const int d = (key[j] >> shift) & dmask;
-    const int pos = s_cnt[wv][d] + rank[j];
-    keys_out[pos] = key[j];
-    vals_out[pos] = val[j];
+    const int lpos = s_lbase[d] + s_cnt[wv][d] + rank[j];
+    s_key[lpos] = key[j];
+    s_val[lpos] = val[j];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_here; i += kBlock) {
+    const int k = s_key[i];
+    const int d = (k >> shift) & dmask;
+    const int pos = s_gbase[d] + (i - s_lbase[d]);
+    keys_out[pos] = k;
+    vals_out[pos] = s_val[i];
   }
 }
 
 // From the sorted (tile, splat) list: CSR starts (starts[t] = number of pairs with tile < t,
-// render_triton.py:408) and, optionally, the inverse permutation inv[q] = sorted position of splat-major
-// pair q, where q = offsets[g] + (ty - ty0) * w + (tx - tx0) is the pair's index in its splat's rect walk
-// (tile coordinates local to the splat's level).
-__global__ __launch_bounds__(kBlock) void k_tile_starts_inv(const int* __restrict__ keys, const int* __restrict__ gids,
-                                                            int tot, int nt, LevelTable L, const int4* __restrict__ rect,
-                                                            const int* __restrict__ offsets, int* __restrict__ starts,
-                                                            int* __restrict__ inv) {
+// render_triton.py:408) and, optionally, pair_q[i] = the splat-major index of sorted pair i:
+// q = offsets[g] + (ty - ty0) * w + (tx - tx0), the pair's index in its splat's rect walk (tile coordinates
+// local to the splat's level).
+__global__ __launch_bounds__(kBlock) void k_tile_starts_q(const int* __restrict__ keys, const int* __restrict__ gids,
+                                                          int tot, int nt, LevelTable L, const int4* __restrict__ rect,
+                                                          const int* __restrict__ offsets, int* __restrict__ starts,
+                                                          int* __restrict__ pair_q) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= tot) return;
   const int k = keys[i];
@@ -408,12 +513,12 @@ __global__ __launch_bounds__(kBlock) void k_tile_starts_inv(const int* __restric
   for (int t = prev + 1; t <= k; ++t) starts[t] = i;
   if (i == tot - 1)
     for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
-  if (inv) {
+  if (pair_q) {
     const int g = gids[i];
     const int4 rc = rect[g];
     const int lt = k - L.tbase[rc.w], ntx = L.ntx[rc.w];
     const int ty = lt / ntx, tx = lt - ty * ntx;
-    inv[offsets[g] + (ty - rc.y) * rc.z + (tx - rc.x)] = i;
+    pair_q[i] = offsets[g] + (ty - rc.y) * rc.z + (tx - rc.x);
   }
 }
 
@@ -493,18 +598,14 @@ int splat_decode(const float* mu, const float* scale, const float* theta, const 
   return check_launch("k_decode_count(decode)");
 }
 
-int splat_bin_count(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
-                    int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, float* rec, int* rect,
-                    int* offsets, long long* info, void* ws, size_t ws_bytes, void* stream) {
-  if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
-    return set_error(kInvalid, "splat_bin_count: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
-  LevelTable L;
-  Routing R;
-  if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin_count: bad levels");
-  if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
-    return set_error(kInvalid, "splat_bin_count: null pointer");
-  if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
-  hipStream_t st = (hipStream_t)stream;
+}  // extern "C"
+
+namespace {
+
+// Launches of the count phase (decode + route + count + offsets + info). Arguments already validated.
+int bin_count_launch(const float* mu, const float* scale, const float* theta, const float* opacity,
+                     const float* color, int C, int N, const LevelTable& L, const Routing& R, int TILE, float cutoff,
+                     float* rec, int* rect, int* offsets, long long* info, void* ws, hipStream_t st) {
   const int nb = div_up(N, kBlock);
   long long* sums = (long long*)ws;
 #define SPLAT_DC(CC)                                                                                         \
@@ -514,29 +615,21 @@ int splat_bin_count(const float* mu, const float* scale, const float* theta, con
   switch (C) { case 1: SPLAT_DC(1); break; case 2: SPLAT_DC(2); break;
                case 3: SPLAT_DC(3); break; default: SPLAT_DC(4); break; }
 #undef SPLAT_DC
-  k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info);
-  k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
+  if (nb <= kFusedScanBlocks) {
+    k_offsets_fused<<<nb, kBlock, 0, st>>>(offsets, sums, N, nb, L.n, info);
+  } else {
+    k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info);
+    k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
+  }
   return check_launch("splat_bin_count");
 }
 
-size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
-  (void)N;
-  return plan_pairs(nt, tot).total;
-}
-
-int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, const splat_levels* lv,
-                    long long tot, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_inv, void* ws,
-                    size_t ws_bytes, void* stream) {
-  if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
-    return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
-  if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
-  LevelTable L;
-  if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_pairs: bad levels");
+// Launches of the pair phase for `tot` pairs. Arguments already validated; ws holds plan_pairs(nt, tot).
+int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTable& L, int t, int* gid_sorted,
+                     int* tile_starts, int* pair_splat, int* pair_q, void* ws, hipStream_t st) {
   const int nt = L.tbase[L.n];
-  const PairsPlan pl = plan_pairs(nt, tot);
-  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
-  hipStream_t st = (hipStream_t)stream;
-  if (tot == 0) {
+  const PairsPlan pl = plan_pairs(nt, t);
+  if (t == 0) {
     k_fill_i32<<<div_up(nt + 1, 256), 256, 0, st>>>(tile_starts, nt + 1, 0);
     k_fill_i32<<<1, 64, 0, st>>>(gid_sorted, 1, 0);
     return check_launch("splat_bin_pairs(empty)");
@@ -554,7 +647,6 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
   int* V[2];
   K[fin] = keys_a; K[1 - fin] = keys_b;
   V[fin] = gid_sorted; V[1 - fin] = vals_b;
-  const int t = (int)tot;
   const int dmask = pl.radix - 1;
   k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, t, dmask, K[0], V[0],
                                               pair_splat, pl.passes ? hist : nullptr, pl.nblk);
@@ -570,10 +662,83 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
   }
-  k_tile_starts_inv<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, L,
-                                                          reinterpret_cast<const int4*>(rect), offsets, tile_starts,
-                                                          pair_inv);
-  return check_launch("k_tile_starts_inv");
+  k_tile_starts_q<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, L,
+                                                        reinterpret_cast<const int4*>(rect), offsets, tile_starts,
+                                                        pair_q);
+  return check_launch("k_tile_starts_q");
+}
+
+}  // namespace
+
+extern "C" {
+
+int splat_bin_count(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
+                    int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, float* rec, int* rect,
+                    int* offsets, long long* info, void* ws, size_t ws_bytes, void* stream) {
+  if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
+    return set_error(kInvalid, "splat_bin_count: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
+  LevelTable L;
+  Routing R;
+  if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin_count: bad levels");
+  if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
+    return set_error(kInvalid, "splat_bin_count: null pointer");
+  if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
+  return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, rec, rect, offsets, info, ws,
+                          (hipStream_t)stream);
+}
+
+size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
+  (void)N;
+  return plan_pairs(nt, tot).total;
+}
+
+int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, const splat_levels* lv,
+                    long long tot, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws,
+                    size_t ws_bytes, void* stream) {
+  if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
+    return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
+  if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
+  LevelTable L;
+  if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_pairs: bad levels");
+  const PairsPlan pl = plan_pairs(L.tbase[L.n], tot);
+  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
+  return bin_pairs_launch(rect, offsets, N, L, (int)tot, gid_sorted, tile_starts, pair_splat, pair_q, ws,
+                          (hipStream_t)stream);
+}
+
+int splat_bin(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color, int C,
+              int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, long long max_pairs, float* rec,
+              int* rect, int* offsets, long long* info, long long* info_host, void* ws_count, size_t ws_count_bytes,
+              long long pair_cap, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws_pairs,
+              size_t ws_pairs_bytes, void* stream) {
+  if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1 || pair_cap < 0)
+    return set_error(kInvalid, "splat_bin: N=%d C=%d H=%d W=%d TILE=%d cap=%lld", N, C, H, W, TILE, pair_cap);
+  LevelTable L;
+  Routing R;
+  if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin: bad levels");
+  if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info || !info_host)
+    return set_error(kInvalid, "splat_bin: null pointer");
+  if (ws_count_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin: count workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, rec, rect, offsets, info,
+                            ws_count, st);
+  if (rc) return rc;
+  // the one device -> host read of the render: totals and error bits, then wait for it
+  if (hipMemcpyAsync(info_host, info, sizeof(long long) * (2 + L.n), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return set_error(kHipError, "splat_bin: reading the pair totals failed");
+  const long long tot = info_host[0];
+  if (info_host[1] & 1) return set_error(kInvalid, "splat_bin: a splat has an empty tile rect (negative cutoff or scale)");
+  if (info_host[1] & 2) return set_error(kOverflow, "splat_bin: %lld pairs exceed the int32 pair index range", tot);
+  if (max_pairs >= 0)
+    for (int l = 0; l < L.n; ++l)
+      if (info_host[2 + l] > max_pairs)
+        return set_error(kBudget, "splat_bin: %lld pairs on level %d exceed the budget of %lld", info_host[2 + l], l,
+                         max_pairs);
+  if (tot > pair_cap) return set_error(kCapacity, "splat_bin: %lld pairs exceed the capacity %lld", tot, pair_cap);
+  if (!gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin: null pair buffers");
+  if (ws_pairs_bytes < plan_pairs(L.tbase[L.n], tot).total) return set_error(kWorkspace, "splat_bin: pair workspace too small");
+  return bin_pairs_launch(rect, offsets, N, L, (int)tot, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs, st);
 }
 
 }  // extern "C"

@@ -31,7 +31,9 @@ template <int V>
 using IC = std::integral_constant<int, V>;
 
 constexpr int kAcc = 16;       // per-splat accumulator stride of the exact path (floats)
-constexpr int kPairRec = 12;   // per-pair sums record (floats, 48 B): Q, Qu, Qv, Quu, Qvv, Quv, colour[4], pad
+constexpr int kPairRecMax = 10;   // per-pair sums record, at most (floats): Q, Qu, Qv, Quu, Qvv, Quv, colour[C]
+template <int C>
+__host__ __device__ constexpr int pair_rec() { return 6 + C; }   // record stride of C channels
 constexpr int kSums = 10;      // sums carried through the reduction
 
 __host__ __device__ constexpr int tile_threads(int tile) { return tile * tile > 64 ? tile * tile : 64; }
@@ -311,12 +313,12 @@ __device__ __forceinline__ void xor_reduce(PairSums<C>& s, int d) {
   for (int c = 0; c < C; ++c) s.gc[c] += __shfl_xor(s.gc[c], d, 64);
 }
 
+// Record of splat-major pair q at psum + q * pair_rec<C>() (4-byte aligned).
 template <int C>
 __device__ __forceinline__ void store_pair(float* __restrict__ dst, const PairSums<C>& s) {
-  float4* d = reinterpret_cast<float4*>(dst);
-  d[0] = make_float4(s.q, s.qu, s.qv, s.quu);
-  d[1] = make_float4(s.qvv, s.quv, s.gc[0], C > 1 ? s.gc[1] : 0.f);
-  d[2] = make_float4(C > 2 ? s.gc[2] : 0.f, C > 3 ? s.gc[3] : 0.f, 0.f, 0.f);
+  dst[0] = s.q; dst[1] = s.qu; dst[2] = s.qv; dst[3] = s.quu; dst[4] = s.qvv; dst[5] = s.quv;
+#pragma unroll
+  for (int c = 0; c < C; ++c) dst[6 + c] = s.gc[c];
 }
 
 // Per-splat sums (Q, Qu, Qv, Quu, Qvv, Quv, colour[C]) -> parameter gradients (formulas at the top).
@@ -349,7 +351,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
-    float* __restrict__ dsa, float* __restrict__ dsac, float* __restrict__ psum, float* __restrict__ bg_part) {
+    float* __restrict__ dsa, float* __restrict__ dsac, const int* __restrict__ pair_q, float* __restrict__ psum,
+    float* __restrict__ bg_part) {
   constexpr int NP = TILE * TILE;
   __shared__ float4 s_pa[NP];
   __shared__ float4 s_pb[NP];
@@ -388,6 +391,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
   for (int i0 = g0; i0 + 64 <= g1; i0 += 64) {
     const int i = i0 + lane;
     const int g = gid[i];
+    const int q = pair_q[i];
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
     const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
         bwd_px<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, col, pa, pb, s);
       }
     }
-    store_pair<C>(psum + (size_t)i * kPairRec, s);
+    store_pair<C>(psum + (size_t)q * pair_rec<C>(), s);
   }
   // remainder of r < 64 pairs: L lanes per pair (largest power of two with r * L <= 64, L <= pixels),
   // each lane covering NP / L consecutive pixels; the L partial sums are combined with xor shuffles.
@@ -435,85 +439,139 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
       bwd_px<C, ODDS>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, col, pa, pb, s);
     }
     for (int d = 1; d < L; d <<= 1) xor_reduce<C>(s, d);
-    if (act && sub == 0) store_pair<C>(psum + (size_t)i * kPairRec, s);
+    if (act && sub == 0) store_pair<C>(psum + (size_t)pair_q[i] * pair_rec<C>(), s);
   }
 }
 
-// Sum each splat's per-pair records in splat-major order. Wave = 64 consecutive splat-major pairs (lane = pair,
-// its record gathered from sorted position pair_inv[q]); pair_splat is non-decreasing along the lanes, so a
-// suffix scan that only adds equal keys leaves each segment's total in its first lane. Segments complete in
-// the wave finish here; a segment cut by a wave boundary leaves its partial sum in pfirst (segment holding
-// lane 0) / plast (segment holding the wave's last pair) for k_reduce_fixup.
+// Sum of per-tile partials part[c * nparts + i] over i for every channel, by one 256-thread workgroup
+// (fixed order: deterministic). Each thread keeps 8 independent loads in flight per step, so the workgroup
+// finishes in a few memory round trips even for tens of thousands of partials.
 template <int C>
-__global__ __launch_bounds__(256) void k_pair_reduce(const float* __restrict__ rec, const float* __restrict__ psum,
-                                                     const int* __restrict__ pair_splat, const int* __restrict__ pair_inv,
-                                                     const int* __restrict__ offsets, int tot, float* __restrict__ g_mu,
-                                                     float* __restrict__ g_scale, float* __restrict__ g_theta,
-                                                     float* __restrict__ g_op, float* __restrict__ g_col,
-                                                     float* __restrict__ pfirst, float* __restrict__ plast) {
+__device__ __forceinline__ void block_bg_sum(const float* __restrict__ part, int nparts, float* __restrict__ g_bg) {
+  __shared__ float s_w[4][kMaxC];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float acc[kMaxC][8];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[c][u] = 0.f;
+  for (int i0 = threadIdx.x; i0 < nparts; i0 += 256 * 8) {
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u * 256;
+        if (i < nparts) acc[c][u] += part[(size_t)c * nparts + i];
+      }
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float x = wave_sum(((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) +
+                             ((acc[c][4] + acc[c][5]) + (acc[c][6] + acc[c][7])));
+    if (lane == 0) s_w[wv][c] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < C) g_bg[threadIdx.x] = (s_w[0][threadIdx.x] + s_w[1][threadIdx.x]) + (s_w[2][threadIdx.x] + s_w[3][threadIdx.x]);
+}
+
+template <int C>
+__device__ __forceinline__ void zero_grads(int g, float* __restrict__ g_mu, float* __restrict__ g_scale,
+                                           float* __restrict__ g_theta, float* __restrict__ g_op,
+                                           float* __restrict__ g_col) {
+  g_mu[2 * g] = 0.f; g_mu[2 * g + 1] = 0.f;
+  g_scale[2 * g] = 0.f; g_scale[2 * g + 1] = 0.f;
+  if (g_theta) g_theta[g] = 0.f;
+  g_op[g] = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = 0.f;
+}
+
+// Per-splat reduction of the per-pair records (contiguous, splat-major: splat g owns q in
+// [offsets[g], offsets[g+1])) into parameter gradients, in one launch. Wave = 64 consecutive pairs (lane =
+// pair); pair_splat is non-decreasing along the lanes, so a suffix scan that only adds equal keys leaves each
+// segment's in-wave total in its first lane. The wave holding a splat's first pair finishes that splat: the
+// one segment that may run past the wave's end is completed by the whole wave reading the rest of its records
+// (load-balanced for splats of thousands of pairs). Splats with no pair (none for valid rects) get zeros.
+// With g_bg set, the grid's first workgroup sums the per-tile background partials instead.
+template <int C>
+__global__ __launch_bounds__(256) void k_splat_reduce(const float* __restrict__ rec, const float* __restrict__ psum,
+                                                      const int* __restrict__ pair_splat,
+                                                      const int* __restrict__ offsets, int tot, int N, int nchunk,
+                                                      float* __restrict__ g_mu, float* __restrict__ g_scale,
+                                                      float* __restrict__ g_theta, float* __restrict__ g_op,
+                                                      float* __restrict__ g_col, const float* __restrict__ bg_part,
+                                                      int nparts, float* __restrict__ g_bg) {
+  constexpr int R = pair_rec<C>();
+  if (g_bg && blockIdx.x == 0) {   // first, so it overlaps the pair waves
+    block_bg_sum<C>(bg_part, nparts, g_bg);
+    return;
+  }
   const int lane = threadIdx.x & 63;
-  const int chunk = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int chunk = (blockIdx.x - (g_bg ? 1 : 0)) * 4 + (threadIdx.x >> 6);
+  if (chunk >= nchunk) return;
   const int q0 = chunk * 64;
-  if (q0 >= tot) return;
   const int q = q0 + lane;
   const bool act = q < tot;
   const int g = act ? pair_splat[q] : -1;
   float v[kSums];
   {
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a, c = a;
-    if (act) {
-      const float4* p4 = reinterpret_cast<const float4*>(psum + (size_t)pair_inv[q] * kPairRec);
-      a = p4[0]; b = p4[1]; c = p4[2];
-    }
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y;
-    v[6] = b.z; v[7] = b.w; v[8] = c.x; v[9] = c.y;
+    const float* src = psum + (size_t)(act ? q : 0) * R;
+#pragma unroll
+    for (int k = 0; k < kSums; ++k) v[k] = (act && k < R) ? src[k] : 0.f;
   }
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int og = __shfl_down(g, d, 64);
     const bool take = lane + d < 64 && og == g;
 #pragma unroll
-    for (int k = 0; k < 6 + C; ++k) {
+    for (int k = 0; k < R; ++k) {
       const float o = __shfl_down(v[k], d, 64);
       if (take) v[k] += o;
     }
   }
-  const int gprev = __shfl_up(g, 1, 64);
-  if (!act || (lane > 0 && gprev == g)) return;
-  const int qs = offsets[g], qe = offsets[g + 1];
-  const bool starts_here = qs >= q0, ends_here = qe <= q0 + 64;
-  if (starts_here && ends_here) {
-    splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
-    return;
+  int gprev = __shfl_up(g, 1, 64);
+  if (lane == 0) gprev = q0 > 0 ? pair_splat[q0 - 1] : -1;
+  const bool start = act && gprev != g;
+  const int qe = start ? offsets[g + 1] : 0;
+  const unsigned long long tb = __ballot(start && qe > q0 + 64);
+  if (tb) {
+    const int src = __ffsll((long long)tb) - 1;
+    const int tqe = __shfl(qe, src, 64);
+    float t[kSums];
+#pragma unroll
+    for (int k = 0; k < kSums; ++k) t[k] = 0.f;
+    for (int j = q0 + 64 + lane; j < tqe; j += 64) {
+      const float* r = psum + (size_t)j * R;
+#pragma unroll
+      for (int k = 0; k < R; ++k) t[k] += r[k];
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      float x = t[k];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+      if (lane == src) v[k] += x;
+    }
   }
-  if (!starts_here)
-    for (int k = 0; k < kSums; ++k) pfirst[(size_t)chunk * kSums + k] = v[k];
-  if (!ends_here)
-    for (int k = 0; k < kSums; ++k) plast[(size_t)chunk * kSums + k] = v[k];
+  if (!start) return;
+  for (int gz = gprev + 1; gz < g; ++gz) zero_grads<C>(gz, g_mu, g_scale, g_theta, g_op, g_col);
+  if (qe == tot)
+    for (int gz = g + 1; gz < N; ++gz) zero_grads<C>(gz, g_mu, g_scale, g_theta, g_op, g_col);
+  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
-// Splats whose pairs span waves c0..c1 of k_pair_reduce: plast[c0] + pfirst[c0+1..c1], in order. Splats with
-// no pair get zero gradients.
+// Zero gradients for every splat (a render with no pairs), plus g_bg from the partials in the first block.
 template <int C>
-__global__ __launch_bounds__(256) void k_reduce_fixup(const float* __restrict__ rec, const int* __restrict__ offsets,
-                                                      int N, const float* __restrict__ pfirst,
-                                                      const float* __restrict__ plast, float* __restrict__ g_mu,
-                                                      float* __restrict__ g_scale, float* __restrict__ g_theta,
-                                                      float* __restrict__ g_op, float* __restrict__ g_col) {
-  const int g = blockIdx.x * 256 + threadIdx.x;
-  if (g >= N) return;
-  const int qs = offsets[g], qe = offsets[g + 1];
-  float v[kSums];
-  if (qe <= qs) {
-    for (int k = 0; k < kSums; ++k) v[k] = 0.f;
-  } else {
-    const int c0 = qs >> 6, c1 = (qe - 1) >> 6;
-    if (c0 == c1) return;
-    for (int k = 0; k < kSums; ++k) v[k] = plast[(size_t)c0 * kSums + k];
-    for (int c = c0 + 1; c <= c1; ++c)
-      for (int k = 0; k < kSums; ++k) v[k] += pfirst[(size_t)c * kSums + k];
+__global__ __launch_bounds__(256) void k_zero_grads(int N, float* __restrict__ g_mu, float* __restrict__ g_scale,
+                                                    float* __restrict__ g_theta, float* __restrict__ g_op,
+                                                    float* __restrict__ g_col, const float* __restrict__ bg_part,
+                                                    int nparts, float* __restrict__ g_bg) {
+  if (g_bg && blockIdx.x == 0) {
+    block_bg_sum<C>(bg_part, nparts, g_bg);
+    return;
   }
-  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
+  const int g = (blockIdx.x - (g_bg ? 1 : 0)) * 256 + threadIdx.x;
+  if (g < N) zero_grads<C>(g, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
 // Exact path backward (render_triton.py:161-266): lane = splat over every pixel; the per-pixel upstream
@@ -810,23 +868,20 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
   });
 }
 
-static size_t reduce_ws_bytes(long long tot) {
-  const size_t nchunk = (size_t)((tot > 0 ? tot : 1) + 63) / 64;
-  return 2 * align256(sizeof(float) * kSums * nchunk);
-}
+size_t splat_pair_sums_bytes(long long tot) { return sizeof(float) * kPairRecMax * (size_t)(tot > 0 ? tot : 1); }
 
-size_t splat_pair_sums_bytes(long long tot) { return sizeof(float) * kPairRec * (size_t)(tot > 0 ? tot : 1); }
-
-int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, long long tot, int C, int H,
-                     int W, int TILE, int flags, const splat_levels* lv, int lev_begin, int lev_end, unsigned levmask,
-                     const float* bg, const float* T, const float* asum, const float* fg, const float* gout,
-                     float* dslog, float* dsa, float* dsac, float* pair_sums, float* bg_part, void* stream) {
+int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, const int* pair_q, long long tot,
+                     int C, int H, int W, int TILE, int flags, const splat_levels* lv, int lev_begin, int lev_end,
+                     unsigned levmask, const float* bg, const float* T, const float* asum, const float* fg,
+                     const float* gout, float* dslog, float* dsa, float* dsac, float* pair_sums, float* bg_part,
+                     void* stream) {
   LevelTable L;
   int tb0, ntiles;
   if (int e = launch_levels("splat_render_bwd", H, W, TILE, lv, lev_begin, lev_end, levmask, flags, &L, &tb0, &ntiles))
     return e;
   if (tot < 0 || tot > 0x7fffffffLL - 64) return set_error(kInvalid, "splat_render_bwd: tot=%lld", tot);
-  if (!rec || !gid_sorted || !tile_starts || !pair_sums) return set_error(kInvalid, "splat_render_bwd: null pointer");
+  if (!rec || !gid_sorted || !tile_starts || !pair_sums || (tot > 0 && !pair_q))
+    return set_error(kInvalid, "splat_render_bwd: null pointer");
   const bool fields = flags & kFlagFields;
   if ((fields || (flags & kFlagUps)) && (!dslog || !dsa || !dsac))
     return set_error(kInvalid, "splat_render_bwd: null upstream fields for flags=%d", flags);
@@ -841,7 +896,7 @@ int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_st
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
         k_bwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
             <<<ntiles, 64, 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa,
-                                    dsac, pair_sums, bg_part);
+                                    dsac, pair_q, pair_sums, bg_part);
         return check_launch("k_bwd_cull");
       });
     });
@@ -882,33 +937,27 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels* lv
   });
 }
 
-size_t splat_reduce_workspace_bytes(long long tot) { return reduce_ws_bytes(tot); }
-
-int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_splat, const int* pair_inv, long long tot,
+int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_splat, long long tot,
                        int N, int C, const float* pair_sums, const float* bg_part, int nparts, float* g_mu,
-                       float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* ws,
-                       size_t ws_bytes, void* stream) {
+                       float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* stream) {
   if (N < 0 || tot < 0 || tot > 0x7fffffffLL - 64 || (N == 0 && tot > 0))
     return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
   if ((N > 0 && (!rec || !offsets || !g_mu || !g_scale || !g_op || !g_color)) ||
-      (tot > 0 && (!pair_splat || !pair_inv || !pair_sums)) || (g_bg && (!bg_part || nparts < 1)))
+      (tot > 0 && (!pair_splat || !pair_sums)) || (g_bg && (!bg_part || nparts < 1)))
     return set_error(kInvalid, "splat_reduce_pairs: null pointer");
-  if (ws_bytes < reduce_ws_bytes(tot)) return set_error(kWorkspace, "splat_reduce_pairs: workspace too small");
   hipStream_t st = (hipStream_t)stream;
-  const size_t nchunk = (size_t)((tot > 0 ? tot : 1) + 63) / 64;
-  float* pfirst = (float*)ws;
-  float* plast = (float*)((char*)ws + align256(sizeof(float) * kSums * nchunk));
+  const int nchunk = (int)((tot + 63) / 64);
   const int t = (int)tot;
+  const unsigned extra = g_bg ? 1u : 0u;
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
     if (t > 0)
-      k_pair_reduce<CC><<<(unsigned)((nchunk + 3) / 4), 256, 0, st>>>(rec, pair_sums, pair_splat, pair_inv, offsets, t,
-                                                                      g_mu, g_scale, g_theta, g_op, g_color, pfirst,
-                                                                      plast);
-    if (N > 0)
-      k_reduce_fixup<CC><<<(N + 255) / 256, 256, 0, st>>>(rec, offsets, N, pfirst, plast, g_mu, g_scale, g_theta,
-                                                          g_op, g_color);
-    if (g_bg) k_bg_sum<CC><<<1, 1024, 0, st>>>(bg_part, nparts, g_bg);
+      k_splat_reduce<CC><<<(unsigned)((nchunk + 3) / 4) + extra, 256, 0, st>>>(
+          rec, pair_sums, pair_splat, offsets, t, N, nchunk, g_mu, g_scale, g_theta, g_op, g_color, bg_part, nparts,
+          g_bg);
+    else if (N > 0 || g_bg)
+      k_zero_grads<CC><<<(unsigned)((N + 255) / 256) + extra, 256, 0, st>>>(N, g_mu, g_scale, g_theta, g_op,
+                                                                            g_color, bg_part, nparts, g_bg);
     return check_launch("splat_reduce_pairs");
   });
 }

@@ -43,7 +43,8 @@ constexpr int kFlagOdds = 2;     // weight colour by the odds a / (1 - a) instea
 constexpr int kFlagUps = 4;      // composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a
 
 // Status codes of the C-ABI.
-enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2, kUnsupported = 3, kOverflow = 4, kWorkspace = 5 };
+enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2, kUnsupported = 3, kOverflow = 4, kWorkspace = 5,
+                    kCapacity = 6, kBudget = 7 };
 
 // Error channel (thread-local last message), defined in capi.hip.
 int set_error(int code, const char* fmt, ...);

@@ -41,17 +41,17 @@ _SIGS = {
     "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _VP, _VP, _VP, _VP, _VP, _SZ,
                              _VP]),
     "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _LL]),
+    "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
+                       _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP, _VP,
                               _VP, _VP, _VP]),
     "splat_pair_sums_bytes": (_SZ, [_LL]),
-    "splat_render_bwd": (_I, [_VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP,
-                              _VP, _VP, _VP, _VP, _VP, _VP]),
+    "splat_render_bwd": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP,
+                              _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_upsample_adjoint_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV]),
     "splat_upsample_adjoint": (_I, [_I, _I, _I, _I, _LV, _U, _VP, _VP, _VP, _VP, _SZ, _VP]),
-    "splat_reduce_workspace_bytes": (_SZ, [_LL]),
-    "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP,
-                                _VP, _SZ, _VP]),
+    "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_exact_fwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_exact_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
     "splat_exact_bwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
@@ -63,9 +63,12 @@ EXPORTED = tuple(_SIGS)
 FLAG_FIELDS = 1
 FLAG_ODDS = 2
 FLAG_UPS = 4
+MAX_LEVELS = 12   # kMaxLevels of the library
 
+STATUS_CAPACITY = 6
+STATUS_BUDGET = 7
 _STATUS = {1: "invalid argument", 2: "HIP error", 3: "unsupported configuration", 4: "overflow",
-           5: "workspace too small"}
+           5: "workspace too small", 6: "pair capacity too small", 7: "pair budget exceeded"}
 
 _lib = None
 
@@ -103,4 +106,8 @@ def ptr(t) -> int | None:
 
 
 def stream_ptr(device=None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw hipStream_t of the current stream of `device` (torch's cheap accessor, no Stream object)."""
+    idx = device.index if isinstance(device, torch.device) else device
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

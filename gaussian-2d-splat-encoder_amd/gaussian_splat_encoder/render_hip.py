@@ -18,6 +18,8 @@ drives the per-batch calls on the current stream and does the octave / multires 
 
 from __future__ import annotations
 
+import threading
+
 import torch
 import torch.nn.functional as F
 
@@ -39,7 +41,11 @@ def _dev_check(*ts):
 
 
 def _f32(t):
-    return None if t is None else t.detach().contiguous().float()
+    if t is None:
+        return None
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t.detach()
+    return t.detach().contiguous().float()
 
 
 def _empty(shape, dev, dtype=torch.float32):
@@ -86,19 +92,63 @@ kernel_timer = KernelTimer()
 class TileBins:
     """Per-batch binning result: decoded splat records, pair list ordered by (tile, splat) and CSR tile
     starts (`gid_b`/`starts_b`/`ntx`/`nt` carry the meaning of the reference's `tiles` tuple), plus the
-    splat-major pair maps the backward's per-splat reduction uses (offsets, pair -> splat, pair -> sorted
-    position).
+    maps the backward uses between sorted and splat-major pair order (offsets, splat-major pair -> splat,
+    sorted pair -> splat-major index).
+
+    Each image's buffers live in two allocations (`blocks[b]`: rec, rect, offsets; `pairs[b]`: gid, starts,
+    pair_splat, pair_q); kernels take raw pointers (`p(b, name)`), tensor views are built on first use.
 
     With levels (`lv` set) the tile ids are global over the levels: `geom[l] = (H_l, W_l, ntx_l, tbase_l,
     pbase_l)`, `nt` / `npix` are the totals, `level_tot_b[b][l]` the pairs of level l and `rect_b[b][:, 3]`
     each splat's level."""
 
-    def __init__(self, rec_b, gid_b, starts_b, tot_b, H, W, TILE, ntx, nt, off_b=None, psplat_b=None, pinv_b=None,
-                 lv=None, geom=None, npix=None, level_tot_b=None, rect_b=None):
-        self.rec_b, self.gid_b, self.starts_b, self.tot_b = rec_b, gid_b, starts_b, tot_b
+    _SLOT = {"rec": (0, 0), "rect": (0, 1), "off": (0, 2), "gid": (1, 0), "starts": (1, 1), "psplat": (1, 2),
+             "pq": (1, 3)}
+
+    def __init__(self, N, tot_b, H, W, TILE, ntx, nt, blocks, pairs, with_maps, lv=None, geom=None, npix=None,
+                 level_tot_b=None):
+        self.N, self.tot_b = N, tot_b
         self.H, self.W, self.TILE, self.ntx, self.nt = H, W, TILE, ntx, nt
-        self.off_b, self.psplat_b, self.pinv_b = off_b, psplat_b, pinv_b
-        self.lv, self.geom, self.npix, self.level_tot_b, self.rect_b = lv, geom, npix, level_tot_b, rect_b
+        self.blocks, self.pairs, self.with_maps = blocks, pairs, with_maps
+        self.lv, self.geom, self.npix, self.level_tot_b = lv, geom, npix, level_tot_b
+        self._views = {}
+
+    def p(self, b, name):
+        """Device pointer of buffer `name` of image b (None for maps that were not built)."""
+        which, i = self._SLOT[name]
+        if which == 1 and i >= 2 and not self.with_maps:
+            return None
+        return (self.blocks if which == 0 else self.pairs)[b].ptr(i)
+
+    def _list(self, name):
+        v = self._views.get(name)
+        if v is None:
+            N, out = self.N, []
+            for b in range(len(self.tot_b)):
+                n = max(self.tot_b[b], 1)
+                blk, pb = self.blocks[b], self.pairs[b]
+                if name == "rec":
+                    out.append(blk.view(0, 16 * max(N, 1), torch.float32, (max(N, 1), 16)))
+                elif name == "rect":
+                    out.append(blk.view(1, 4 * N, torch.int32, (N, 4)))
+                elif name == "off":
+                    out.append(blk.view(2, N + 1, torch.int32))
+                elif name == "gid":
+                    out.append(pb.view(0, n, torch.int32))
+                elif name == "starts":
+                    out.append(pb.view(1, self.nt + 1, torch.int32))
+                else:
+                    out.append(pb.view(2 if name == "psplat" else 3, n, torch.int32) if self.with_maps else None)
+            v = self._views[name] = out
+        return v
+
+    rec_b = property(lambda self: self._list("rec"))
+    rect_b = property(lambda self: self._list("rect"))
+    off_b = property(lambda self: self._list("off"))
+    gid_b = property(lambda self: self._list("gid"))
+    starts_b = property(lambda self: self._list("starts"))
+    psplat_b = property(lambda self: self._list("psplat"))
+    pq_b = property(lambda self: self._list("pq"))
 
     def as_tuple(self):
         return self.gid_b, self.starts_b, self.ntx, self.nt
@@ -125,6 +175,10 @@ class TileBins:
 
 def levels_geometry(H, W, TILE, lv):
     """[(H_l, W_l, ntx_l, tbase_l, pbase_l)] per level, total tiles, total packed pixel slots."""
+    key = (H, W, TILE, _lv_key(lv))
+    hit = _GEOM.get(key)
+    if hit is not None:
+        return hit
     lib = _lib.load()
     ref = None if lv is None else _lib.ctypes.byref(lv)
     n = lib.splat_levels_geometry(H, W, TILE, ref, None, 0)
@@ -133,11 +187,57 @@ def levels_geometry(H, W, TILE, lv):
     buf = (_lib.ctypes.c_int * (5 * n + 2))()
     check(0 if lib.splat_levels_geometry(H, W, TILE, ref, buf, 5 * n + 2) == n else 1, "splat_levels_geometry")
     geom = [tuple(buf[5 * l:5 * l + 5]) for l in range(n)]
-    return geom, buf[5 * n], buf[5 * n + 1]
+    _GEOM[key] = hit = (geom, buf[5 * n], buf[5 * n + 1])
+    return hit
+
+
+def _lv_key(lv):
+    return None if lv is None else (lv.mode, lv.max_octaves, lv.base_texels, lv.n_coarse, lv.coarse_H, lv.coarse_W)
+
+
+_GEOM = {}          # (H, W, TILE, levels) -> levels_geometry result
+_PAIRS_HW = {}      # binning configuration -> most pairs one image needed so far (sizes the next capacity)
+_tls = threading.local()
+
+
+def _info_host():
+    """Pinned int64 landing buffer of the binning's one read-back (per thread, reused)."""
+    buf = getattr(_tls, "info", None)
+    if buf is None:
+        t = torch.empty(2 + _lib.MAX_LEVELS, dtype=torch.int64, pin_memory=True)
+        buf = _tls.info = (t, t.numpy())
+    return buf
+
+
+def _align(n):
+    return (n + 255) & ~255
+
+
+class _Carve:
+    """Sub-buffers of one uint8 device allocation (256-byte aligned)."""
+
+    def __init__(self, sizes, dev, zero=False):
+        self.off, o = [], 0
+        for n in sizes:
+            self.off.append(o)
+            o += _align(max(int(n), 1))
+        self.off.append(o)
+        self.buf = (torch.zeros if zero else torch.empty)(o, dtype=torch.uint8, device=dev)
+        self.base = self.buf.data_ptr()
+
+    def ptr(self, i):
+        return self.base + self.off[i]
+
+    def nbytes(self, i):
+        return self.off[i + 1] - self.off[i]
+
+    def view(self, i, n, dtype, shape=None):
+        t = self.buf[self.off[i]:self.off[i] + 4 * n].view(dtype)     # 4-byte element types only
+        return t if shape is None else t.view(shape)
 
 
 def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True, lv=None) -> TileBins:
-    """Decode + bin every batch (render_triton.py:351-409). One host read of the per-batch pair totals.
+    """Decode + bin every batch (render_triton.py:351-409). One host read of the pair totals per image.
     with_maps=False skips the pair maps only the backward needs (forward-only renders). `lv` (a
     _lib.SplatLevels) routes splats to levels (octave / coarse-fine renders, render_triton.py:879-980)."""
     _dev_check(mu, scale, color, opacity, theta)
@@ -154,6 +254,13 @@ def _budget_error(n, max_pairs, H, W, TILE, cutoff, N):
         f"instead of culling at full res. Refusing to allocate.")
 
 
+def _pair_buffers(lib, N, nt, cap, with_maps, dev):
+    """gid, starts, pair_splat, pair_q and the pair-phase workspace for up to `cap` pairs, one allocation."""
+    c = max(cap, 1)
+    m = c if with_maps else 0
+    return _Carve([4 * c, 4 * (nt + 1), 4 * m, 4 * m, lib.splat_bin_pairs_workspace_bytes(N, nt, cap)], dev)
+
+
 def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv):
     B, N, C = color.shape
     dev = mu.device
@@ -165,50 +272,53 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     ntx = geom[0][2]
     if lv is None:
         geom = None
-    stream = _lib.stream_ptr(dev)
     if N == 0:
-        return TileBins([torch.zeros((1, 16), device=dev)] * B, [torch.zeros(1, dtype=torch.int32, device=dev)] * B,
-                        [torch.zeros(nt + 1, dtype=torch.int32, device=dev)] * B, [0] * B, H, W, TILE, ntx, nt,
-                        [torch.zeros(1, dtype=torch.int32, device=dev)] * B, [None] * B, [None] * B,
-                        lv, geom, npix, [[0] * L] * B, None)
-    info = torch.empty((B, 2 + L), dtype=torch.int64, device=dev)
-    rec_b, rect_b, off_b = [], [], []
-    ws1 = _ws(lib.splat_bin_count_workspace_bytes(N), dev)
+        blk = _Carve([64, 0, 4], dev, zero=True)
+        pb = _Carve([4, 4 * (nt + 1), 0, 0], dev, zero=True)
+        return TileBins(0, [0] * B, H, W, TILE, ntx, nt, [blk] * B, [pb] * B, False, lv, geom, npix, [[0] * L] * B)
+    stream = _lib.stream_ptr(dev)
+    key = (N, H, W, TILE, float(cutoff), _lv_key(lv))
+    hw = _PAIRS_HW.get(key, 0)
+    cap = hw + (hw >> 4) + 1024 if hw else 0
+    info_t, info_np = _info_host()
+    info_p = info_t.data_ptr()
+    ws1_bytes = lib.splat_bin_count_workspace_bytes(N)
+    budget = -1 if max_pairs is None else int(max_pairs)
+    blocks, pairs, tots, level_tots = [], [], [], []
     for b in range(B):
-        rec = _empty((N, 16), dev)
-        rect = torch.empty((N, 4), dtype=torch.int32, device=dev)
-        off = torch.empty(N + 1, dtype=torch.int32, device=dev)
-        check(lib.splat_bin_count(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]),
-                                  ptr(col_[b]), C, N, H, W, TILE, float(cutoff), lvr, ptr(rec), ptr(rect), ptr(off),
-                                  ptr(info[b]), ptr(ws1), ws1.numel(), stream), "splat_bin_count")
-        rec_b.append(rec); rect_b.append(rect); off_b.append(off)
-    info_h = info.cpu()                                                   # the one host sync of binning
-    if bool((info_h[:, 1] & 1).any()):
-        raise ValueError("binning: a splat has an empty tile rect (negative cutoff or scale)")
-    if bool((info_h[:, 1] & 2).any()):
-        raise PairBudgetExceeded(f"binning: {int(info_h[:, 0].max())} pairs exceed the int32 pair index range")
-    tots = [int(x) for x in info_h[:, 0]]
-    level_tots = [[int(x) for x in info_h[b, 2:2 + L]] for b in range(B)]
-    if max_pairs is not None:
-        # the reference checks each binned group (one canvas) per batch against the budget
-        for l in range(L):
-            worst = max(lt[l] for lt in level_tots)
-            if worst > max_pairs:
-                Hl, Wl = (H, W) if geom is None else geom[l][:2]
-                raise _budget_error(worst, max_pairs, Hl, Wl, TILE, cutoff, N)
-    gid_b, starts_b, psplat_b, pinv_b = [], [], [], []
-    for b in range(B):
-        tot = tots[b]
-        gid = torch.empty(max(tot, 1), dtype=torch.int32, device=dev)
-        starts = torch.empty(nt + 1, dtype=torch.int32, device=dev)
-        psplat = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
-        pinv = torch.empty(max(tot, 1), dtype=torch.int32, device=dev) if with_maps else None
-        ws2 = _ws(lib.splat_bin_pairs_workspace_bytes(N, nt, tot), dev)
-        check(lib.splat_bin_pairs(ptr(rect_b[b]), ptr(off_b[b]), N, H, W, TILE, lvr, tot, ptr(gid), ptr(starts),
-                                  ptr(psplat), ptr(pinv), ptr(ws2), ws2.numel(), stream), "splat_bin_pairs")
-        gid_b.append(gid); starts_b.append(starts); psplat_b.append(psplat); pinv_b.append(pinv)
-    return TileBins(rec_b, gid_b, starts_b, tots, H, W, TILE, ntx, nt, off_b, psplat_b, pinv_b, lv, geom, npix,
-                    level_tots, rect_b)
+        blk = _Carve([64 * N, 16 * N, 4 * (N + 1), 8 * (2 + L), ws1_bytes], dev)
+        pb = _pair_buffers(lib, N, nt, cap, with_maps, dev) if cap else None
+        pp = (lambda i: None) if pb is None else pb.ptr
+        info_np[0] = info_np[1] = 0
+        rc = lib.splat_bin(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]), ptr(col_[b]),
+                           C, N, H, W, TILE, float(cutoff), lvr, budget, blk.ptr(0), blk.ptr(1), blk.ptr(2),
+                           blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0), pp(1),
+                           pp(2) if with_maps else None, pp(3) if with_maps else None, pp(4),
+                           0 if pb is None else pb.nbytes(4), stream)
+        tot = int(info_np[0])
+        lt = info_np[2:2 + L].tolist()
+        if rc == _lib.STATUS_BUDGET:
+            l = max(range(L), key=lambda i: lt[i])
+            Hl, Wl = (H, W) if geom is None else geom[l][:2]
+            raise _budget_error(lt[l], max_pairs, Hl, Wl, TILE, cutoff, N)
+        if rc == 1 and info_np[1] & 1:
+            raise ValueError("binning: a splat has an empty tile rect (negative cutoff or scale)")
+        if rc == 4:
+            raise PairBudgetExceeded(f"binning: {tot} pairs exceed the int32 pair index range")
+        if rc == _lib.STATUS_CAPACITY:
+            pb = _pair_buffers(lib, N, nt, tot, with_maps, dev)
+            check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), N, H, W, TILE, lvr, tot, pb.ptr(0), pb.ptr(1),
+                                      pb.ptr(2) if with_maps else None, pb.ptr(3) if with_maps else None, pb.ptr(4),
+                                      pb.nbytes(4), stream), "splat_bin_pairs")
+        else:
+            check(rc, "splat_bin")
+        if tot > hw:
+            _PAIRS_HW[key] = hw = tot
+        blocks.append(blk)
+        pairs.append(pb)
+        tots.append(tot)
+        level_tots.append(lt)
+    return TileBins(N, tots, H, W, TILE, ntx, nt, blocks, pairs, with_maps, lv, geom, npix, level_tots)
 
 
 def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
@@ -224,9 +334,17 @@ def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
     """splat_render_fwd for batch b over levels lev = (begin, end); comp = (bg, out, T, asum, fg) or Nones,
     fields = (slog, sa, sac) or Nones."""
     lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
-    check(lib.splat_render_fwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), C, bins.H, bins.W,
+    check(lib.splat_render_fwd(bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), C, bins.H, bins.W,
                                bins.TILE, flags, lvr, lev[0], lev[1], mask, *[ptr(t) for t in comp],
                                *[ptr(t) for t in fields], stream), "splat_render_fwd")
+
+
+def _composite_buffers(B, P, C, dev):
+    """out [B,P,C], T [B,P], asum [B,P], fg [B,P,C] as views of one allocation."""
+    buf = torch.empty(B * P * (2 * C + 2), device=dev)
+    n = B * P
+    return (buf[:n * C].view(B, P, C), buf[n * C:n * (C + 1)].view(B, P), buf[n * (C + 1):n * (C + 2)].view(B, P),
+            buf[n * (C + 2):].view(B, P, C))
 
 
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False):
@@ -235,7 +353,7 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     P = H * W
     dev = mu.device
     bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs)
-    out, T, asum, fg = _empty((B, P, C), dev), _empty((B, P), dev), _empty((B, P), dev), _empty((B, P, C), dev)
+    out, T, asum, fg = _composite_buffers(B, P, C, dev)
     bgf = _f32(bg)
     flags = FLAG_ODDS if odds else 0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
@@ -269,7 +387,7 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     P = H * W
     dev = mu.device
     bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, lv=lv)
-    out, T, asum, fg = _empty((B, P, C), dev), _empty((B, P), dev), _empty((B, P), dev), _empty((B, P, C), dev)
+    out, T, asum, fg = _composite_buffers(B, P, C, dev)
     L = bins.n_levels
     # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
     fl = (_empty((bins.npix,), dev), _empty((bins.npix,), dev), _empty((bins.npix, C), dev)) if L > 1 else \
@@ -297,33 +415,39 @@ def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stre
     """splat_render_bwd for batch b over levels lev = (begin, end); upstream = (bg, T, asum, fg, gout, dslog,
     dsa, dsac) with Nones where unused."""
     lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
-    check(lib.splat_render_bwd(ptr(bins.rec_b[b]), ptr(bins.gid_b[b]), ptr(bins.starts_b[b]), bins.tot_b[b], C,
+    check(lib.splat_render_bwd(bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), bins.p(b, "pq"),
+                               bins.tot_b[b], C,
                                bins.H, bins.W, bins.TILE, flags, lvr, lev[0], lev[1], mask,
                                *[ptr(u) for u in upstream], ptr(sums), ptr(bg_part), stream), "splat_render_bwd")
 
 
 def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream):
     """Per-splat reduction of batch b's pair sums into `grads` (and g_bg from the level-0 tile partials)."""
-    dev = bins.rec_b[b].device
     tot = bins.tot_b[b]
-    N = bins.off_b[b].numel() - 1
+    N = bins.N
     ev = kernel_timer.record("reduce")
-    ws = _ws(lib.splat_reduce_workspace_bytes(tot), dev)
     g_mu, g_scale, g_col, g_op, g_th = grads
     sl = lambda t: None if (t is None or N == 0) else ptr(t[b])
-    check(lib.splat_reduce_pairs(ptr(bins.rec_b[b]) if N else None, ptr(bins.off_b[b]) if N else None,
-                                 ptr(bins.psplat_b[b]), ptr(bins.pinv_b[b]), tot, N, C, ptr(sums), ptr(bg_part),
-                                 bins.ntiles0, sl(g_mu), sl(g_scale), sl(g_th), sl(g_op), sl(g_col), ptr(g_bg),
-                                 ptr(ws), ws.numel(), stream), "splat_reduce_pairs")
+    check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
+                                 bins.p(b, "psplat") if tot else None, tot, N, C, ptr(sums), ptr(bg_part),
+                                 bins.ntiles0, sl(g_mu),
+                                 sl(g_scale), sl(g_th), sl(g_op), sl(g_col), ptr(g_bg), stream), "splat_reduce_pairs")
     kernel_timer.close("reduce", ev)
+
+
+def _bwd_buffers(lib, bins, b, C, with_bg, dev):
+    """Per-pair sums and (optionally) the level-0 per-tile background partials, one allocation."""
+    ns = lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4
+    nb = C * bins.ntiles0 if with_bg else 0
+    buf = torch.empty(ns + nb, device=dev)
+    return buf[:ns], (buf[ns:] if with_bg else None)
 
 
 def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream):
     """Both backward steps for batch b of a single-level render: per-tile pair sums, then the per-splat
     reduction into `grads`."""
-    dev = bins.rec_b[b].device
-    sums = _empty((lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4,), dev)
-    bg_part = _empty((C * bins.nt,), dev) if g_bg is not None else None
+    dev = bins.blocks[b].buf.device
+    sums, bg_part = _bwd_buffers(lib, bins, b, C, g_bg is not None, dev)
     ev = kernel_timer.record("bwd")
     _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
     kernel_timer.close("bwd", ev)
@@ -381,8 +505,7 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds):
         else None
     for b in range(B):
         mask = bins.level_mask(b)
-        sums = _empty((lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4,), dev)
-        bg_part = _empty((C * bins.ntiles0,), dev)
+        sums, bg_part = _bwd_buffers(lib, bins, b, C, True, dev)
         ev = kernel_timer.record("bwd")
         _render_bwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], T[b], asum[b], fg[b], go[b], *dS), sums,
                     bg_part, stream)
@@ -503,9 +626,6 @@ def _backward(grad_out, mu, scale, color, opacity, bg, py, px, theta, T, asum, f
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     g_mu, g_scale, g_col, g_op, g_th = _grads_out(B, N, C, dev, has_th)
     g_bg = _empty((B, C), dev)
-    if N == 0:
-        g_bg.copy_((_f32(grad_out) * T.unsqueeze(-1)).sum(dim=1))
-        return g_mu, g_scale, g_col, g_op, g_bg, g_th
     if recs is None:
         recs = _forward(mu, scale, color, opacity, bg, py, px, theta)[4]
     go, bgf, pyf, pxf = _f32(grad_out), _f32(bg), _f32(py), _f32(px)

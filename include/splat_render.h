@@ -1,11 +1,13 @@
 /* C-ABI of the gfx950 tile-binned Gaussian-splat renderer (libsplat_hip.so).
  *
  * Every entry point takes raw device pointers (fp32 / int32, contiguous), sizes and a hipStream_t passed
- * as `void *stream`; all work is enqueued on that stream and no entry point synchronises or allocates.
+ * as `void *stream`; all work is enqueued on that stream. No entry point allocates; only splat_bin
+ * waits (for the one read-back of the pair totals that sizes the pair buffers).
  * Buffers are owned by the caller; scratch memory comes in as (ws, ws_bytes), sized by the matching
  * *_workspace_bytes query. Every call returns 0 on success or a status code, with a message available
  * from splat_last_error() (thread-local):
- *   1 invalid argument, 2 HIP launch error, 3 unsupported configuration, 4 overflow, 5 workspace too small.
+ *   1 invalid argument, 2 HIP launch error, 3 unsupported configuration, 4 overflow, 5 workspace too small,
+ *   6 pair capacity too small (splat_bin), 7 pair budget exceeded (splat_bin).
  *
  * Layouts (one image; callers loop over the batch like the reference does):
  *   mu[N,2] (y, x) in [0,1];  scale[N,2] (sy, sx) = softplus(log_scale) + 1e-4;  theta[N] or NULL;
@@ -77,14 +79,29 @@ int splat_bin_count(const float *mu, const float *scale, const float *theta, con
  * gid_sorted[max(tot,1)] lists splat ids ordered by (tile, splat id); tile_starts[nt+1] with nt the total
  * tile count over all levels (splat_levels_geometry).
  * tot == 0 gives gid_sorted = {0} and all-zero starts, as the reference does.
- * Optional (NULL skips) maps over the splat-major pair order q (splat g owns q in [offsets[g], offsets[g+1])),
- * used by the backward's per-splat reduction: pair_splat[tot] = splat of q, pair_inv[tot] = sorted position
- * of q.
+ * Optional (NULL skips) maps between the sorted order i and the splat-major pair order q (splat g owns
+ * q in [offsets[g], offsets[g+1]), walking its rect row by row), used by the backward:
+ * pair_splat[q] = splat of q, pair_q[i] = q of sorted pair i.
  * Replaces render_triton.py:392-409. */
 size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot);
 int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, int TILE,
                     const splat_levels *lv, long long tot, int *gid_sorted, int *tile_starts,
-                    int *pair_splat, int *pair_inv, void *ws, size_t ws_bytes, void *stream);
+                    int *pair_splat, int *pair_q, void *ws, size_t ws_bytes, void *stream);
+
+/* Binning in one call: phase 1 (splat_bin_count), one read of info into pinned host memory info_host
+ * (2 + L int64) with a wait on `stream`, then phase 2 (splat_bin_pairs) when the pairs fit. Statuses:
+ *   0 the pair phase ran into gid_sorted / tile_starts / pair_splat / pair_q (capacity pair_cap pairs;
+ *     ws_pairs sized by splat_bin_pairs_workspace_bytes(N, nt, pair_cap));
+ *   6 tot > pair_cap: nothing pair-sized was touched; the caller sizes buffers from info_host[0] and calls
+ *     splat_bin_pairs;
+ *   7 some level holds more than max_pairs pairs (max_pairs < 0: no budget), before any pair work;
+ *   1 / 4 the error bits of info (empty rect, int32 overflow).
+ * Replaces render_triton.py:351-409 with its one sync (:391) and budget check (:378-385). */
+int splat_bin(const float *mu, const float *scale, const float *theta, const float *opacity,
+              const float *color, int C, int N, int H, int W, int TILE, float cutoff, const splat_levels *lv,
+              long long max_pairs, float *rec, int *rect, int *offsets, long long *info, long long *info_host,
+              void *ws_count, size_t ws_count_bytes, long long pair_cap, int *gid_sorted, int *tile_starts,
+              int *pair_splat, int *pair_q, void *ws_pairs, size_t ws_pairs_bytes, void *stream);
 
 /* Per-tile forward over the binned pairs of levels [lev_begin, lev_end) (TILE in {4, 8, 16}); levels
  * whose bit in levmask is clear are skipped (their pixels are not written).
@@ -101,7 +118,8 @@ int splat_render_fwd(const float *rec, const int *gid_sorted, const int *tile_st
 
 /* Backward, step 1: per-tile kernel over the pairs of levels [lev_begin, lev_end) (levmask as in the
  * forward). For every pair (sorted position i) it sums over the tile's pixels the terms the parameter
- * gradients need and stores them in pair_sums[i] (12 floats, splat_pair_sums_bytes).
+ * gradients need and stores them, 6 + C floats, at pair_sums + pair_q[i] * (6 + C): splat-major order,
+ * so the reduction reads them contiguously (splat_pair_sums_bytes sizes the buffer for any C).
  * Composite (levels [0, 1)): upstream gout[P,C] with the forward's T, asum, fg and bg; with bg_part set
  * ([C, ntiles0] floats, ntiles0 = level 0's tiles) it also writes per-tile partials of sum_p gout*T.
  * With UPS the S_a gradient is torch's clamp_min one (zero where S_a < 1e-8) and the pixel upstream
@@ -110,11 +128,11 @@ int splat_render_fwd(const float *rec, const int *gid_sorted, const int *tile_st
  * Replaces _render_bwd_cull_kernel, render_triton.py:602-720 (per-pair grads, :612-614), and the autograd
  * of the octave / coarse-fine composite, render_triton.py:918, :976-978. */
 size_t splat_pair_sums_bytes(long long tot);
-int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, long long tot, int C,
-                     int H, int W, int TILE, int flags, const splat_levels *lv, int lev_begin, int lev_end,
-                     unsigned levmask, const float *bg, const float *T, const float *asum, const float *fg,
-                     const float *gout, float *dslog, float *dsa, float *dsac, float *pair_sums,
-                     float *bg_part, void *stream);
+int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, const int *pair_q,
+                     long long tot, int C, int H, int W, int TILE, int flags, const splat_levels *lv,
+                     int lev_begin, int lev_end, unsigned levmask, const float *bg, const float *T,
+                     const float *asum, const float *fg, const float *gout, float *dslog, float *dsa,
+                     float *dsac, float *pair_sums, float *bg_part, void *stream);
 
 /* Backward of the upsample: the exact adjoint of the bilinear upsample of every masked coarse level,
  * from the level-0 upstream dslog/dsa/dsac[0, P) into the coarse levels' packed slots, deterministic
@@ -124,16 +142,14 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels *lv
                            float *dslog, float *dsa, float *dsac, void *ws, size_t ws_bytes, void *stream);
 
 /* Backward, step 2: per-splat reduction of the pair sums into parameter gradients, written (not
- * accumulated), deterministic, no global atomics. Takes the binning's offsets, pair_splat and pair_inv.
+ * accumulated), deterministic, no global atomics, one launch. Takes the binning's offsets and pair_splat.
  * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
  * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = ntiles0 per-tile partials of step 1.
  * One call covers the pairs of every level.
  * Replaces the index_add_ scatter and the g_bg reduction, render_triton.py:723-810. */
-size_t splat_reduce_workspace_bytes(long long tot);
-int splat_reduce_pairs(const float *rec, const int *offsets, const int *pair_splat, const int *pair_inv,
-                       long long tot, int N, int C, const float *pair_sums, const float *bg_part, int nparts,
-                       float *g_mu, float *g_scale, float *g_theta, float *g_op, float *g_color,
-                       float *g_bg, void *ws, size_t ws_bytes, void *stream);
+int splat_reduce_pairs(const float *rec, const int *offsets, const int *pair_splat, long long tot, int N,
+                       int C, const float *pair_sums, const float *bg_part, int nparts, float *g_mu,
+                       float *g_scale, float *g_theta, float *g_op, float *g_color, float *g_bg, void *stream);
 
 /* Exact (unculled) path: every pixel sums every splat; pixel centres py[P], px[P] supplied by the caller.
  * Replaces _render_fwd_kernel / _render_bwd_kernel and their wrappers, render_triton.py:58-303. */
