@@ -21,9 +21,9 @@ namespace splat {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
-constexpr int kItems = 16;                      // keys per thread in the pair/sort kernels
-constexpr int kSortKeys = kBlock * kItems;      // 4096 keys per block
-constexpr int kWaveKeys = kSortKeys / kWaves;   // 1024 consecutive keys per wave
+constexpr int kItems = 8;                       // keys per thread in the pair/sort kernels
+constexpr int kSortKeys = kBlock * kItems;      // 2048 keys per block
+constexpr int kWaveKeys = kSortKeys / kWaves;   // 512 consecutive keys per wave
 constexpr long long kBadBit = 1LL << 62;        // marks a block holding an empty or inverted rect
 
 // ----------------------------------------------------------------------------------------------------
@@ -260,18 +260,25 @@ __device__ __forceinline__ int last_le(const int* __restrict__ a, int lo, int hi
   return lo;
 }
 
-// Block-cooperative last_le over a[0, n): 256 samples per round narrow the bracket 256-fold, so the
-// search costs ceil(log256 n) rounds of one load per thread instead of log2 n dependent loads.
-// Requires a[0] <= p. Every thread must call it; all get the result.
+// Block-cooperative last_le over a[0, n): 1024 samples per round (4 per thread) narrow the bracket
+// 1024-fold, so the search costs ceil(log1024 n) rounds of independent loads instead of log2 n dependent
+// loads. Requires a[0] <= p. Every thread must call it; all get the result.
 __device__ __forceinline__ int block_last_le(const int* __restrict__ a, int n, int p, int* s_w) {
+  constexpr int S = kBlock * 4;
   int lo = 0, hi = n - 1;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   while (hi > lo) {
-    const int step = (hi - lo + kBlock) / kBlock;          // ceil((hi - lo + 1) / kBlock)
-    const int idx = lo + (int)threadIdx.x * step;
-    const bool ok = idx <= hi && a[idx] <= p;               // true for a prefix of the threads (t = 0 always)
-    const unsigned long long m = __ballot(ok);
-    if (lane == 0) s_w[wv] = __popcll(m);
+    const int step = (hi - lo + S) / S;                      // ceil((hi - lo + 1) / S)
+    int cnt_t = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {                            // sample j = 4 t + k at lo + j * step
+      const int idx = lo + ((int)threadIdx.x * 4 + k) * step;
+      cnt_t += (idx <= hi && a[idx] <= p) ? 1 : 0;           // true for a prefix of the samples (j = 0 always)
+    }
+    int c = cnt_t;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
+    if (lane == 0) s_w[wv] = c;
     __syncthreads();
     int cnt = 0;
 #pragma unroll
@@ -311,37 +318,69 @@ __device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
   return MAX ? max(pre, ex) : pre + ex;
 }
 
-// Block = 4096 consecutive pairs. Each splat with pairs in the block marks its first pair there with its
+// Block = kSortKeys consecutive pairs. Each splat with pairs in the block marks its first pair there with its
 // id; an inclusive max-scan over the block then gives every pair its owner (splat ids grow with p).
-// Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat (optional) and, with `hist` set, the
-// block's histogram of the first radix digit.
+// The block's first splat comes from a cooperative search; when the block holds at most kBlock splats
+// (always at a few pairs per splat or more) their offsets and rects are loaded once, one per thread, into
+// LDS, and the pair loop reads only LDS. Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat
+// (optional) and, with `hist` set, the block's histogram of the first radix digit.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
                                                           int N, LevelTable L, int tot, int dmask, int* __restrict__ keys,
                                                           int* __restrict__ vals, int* __restrict__ pair_splat,
                                                           int* __restrict__ hist, int nblocks) {
   __shared__ int4 s_own4[kSortKeys / 4];
+  __shared__ int4 s_rect[kBlock];
+  __shared__ int s_o0[kBlock];
   __shared__ int s_hist[256];
   __shared__ int s_w[kWaves];
   int* s_own = reinterpret_cast<int*>(s_own4);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int p_base = blockIdx.x * kSortKeys;
   const int n_here = min(kSortKeys, tot - p_base);
+  const int p_last = p_base + n_here - 1;
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
   for (int i = threadIdx.x; i < kSortKeys / 4; i += kBlock) s_own4[i] = make_int4(-1, -1, -1, -1);
   const int glo = block_last_le(offsets, N, p_base, s_w);
-  const int ghi = block_last_le(offsets, N, p_base + n_here - 1, s_w);
+  // window of the next kBlock splats: offsets and rect, one per thread
+  const int gw = glo + (int)threadIdx.x;
+  int o0 = 0x7fffffff, o1 = 0x7fffffff;
+  int4 rw = make_int4(0, 0, 1, 0);
+  if (gw < N) {
+    o0 = offsets[gw];
+    o1 = offsets[gw + 1];
+    rw = rect[gw];
+  }
+  const bool in_win = o0 <= p_last;   // prefix of the threads
+  {
+    const unsigned long long m = __ballot(in_win);
+    if (lane == 0) s_w[wv] = __popcll(m);
+  }
+  s_o0[threadIdx.x] = o0;
+  s_rect[threadIdx.x] = rw;
   __syncthreads();
-  for (int g = glo + (int)threadIdx.x; g <= ghi; g += kBlock) {
-    const int o0 = offsets[g], o1 = offsets[g + 1];
-    if (o1 > o0) atomicMax(&s_own[max(o0, p_base) - p_base], g);   // o0 <= offsets[ghi] <= last pair here
+  int cnt = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) cnt += s_w[w];
+  // the window covers the block unless all kBlock splats start in it and more may follow
+  const bool fast = cnt < kBlock || glo + kBlock >= N;
+  __syncthreads();
+  if (fast) {
+    if (in_win && o1 > o0) atomicMax(&s_own[max(o0, p_base) - p_base], gw);
+  } else {
+    const int ghi = block_last_le(offsets, N, p_last, s_w);
+    for (int g = glo + (int)threadIdx.x; g <= ghi; g += kBlock) {
+      const int a0 = offsets[g], a1 = offsets[g + 1];
+      if (a1 > a0) atomicMax(&s_own[max(a0, p_base) - p_base], g);   // a0 <= offsets[ghi] <= last pair here
+    }
   }
   __syncthreads();
   {
-    // thread t scans entries [16 t, 16 t + 16)
-    int loc[16];
+    // thread t scans entries [8 t, 8 t + 8)
+    int loc[8];
     int run = -1;
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      const int4 x = s_own4[threadIdx.x * 4 + k4];
+    for (int k4 = 0; k4 < 2; ++k4) {
+      const int4 x = s_own4[threadIdx.x * 2 + k4];
       run = max(run, x.x); loc[4 * k4 + 0] = run;
       run = max(run, x.y); loc[4 * k4 + 1] = run;
       run = max(run, x.z); loc[4 * k4 + 2] = run;
@@ -350,20 +389,26 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
     int total;
     const int ex = block256_excl<true>(run, s_w, total);
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4)
-      s_own4[threadIdx.x * 4 + k4] = make_int4(max(loc[4 * k4], ex), max(loc[4 * k4 + 1], ex),
+    for (int k4 = 0; k4 < 2; ++k4)
+      s_own4[threadIdx.x * 2 + k4] = make_int4(max(loc[4 * k4], ex), max(loc[4 * k4 + 1], ex),
                                                max(loc[4 * k4 + 2], ex), max(loc[4 * k4 + 3], ex));
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll 4
+#pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const int i = wv * kWaveKeys + j * 64 + lane;
     if (i >= n_here) continue;
     const int p = p_base + i;
     const int g = s_own[i];
-    const int k = p - offsets[g];
-    const int4 rc = rect[g];
+    int k;
+    int4 rc;
+    if (fast) {
+      k = p - s_o0[g - glo];
+      rc = s_rect[g - glo];
+    } else {
+      k = p - offsets[g];
+      rc = rect[g];
+    }
     const int ky = k / rc.z;
     const int kx = k - ky * rc.z;
     const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;

@@ -98,3 +98,16 @@ def test_c1_full_size(dev, odds, fields):
     """The headline configuration: 768 x 768, 92,160 splats, forward and backward."""
     s = synth.config("c2").to(dev)
     run_case(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.theta, s.H, s.W, 8, odds, fields, seed=7)
+
+
+def test_heavy_tail_splats(dev):
+    """A C4-like heavy tail at small scale: 2 % of the splats at ~40 px (thousands of tile pairs each), whose
+    per-pair sums span many reduction waves; gradients against the oracle."""
+    H = W = 256
+    mu, ls, col, op, bg, th = random_scene(3000, H, W, seed=41, dev=dev, ls_mean_px=3.0, ls_std=0.5, op_max=0.9)
+    g = torch.Generator().manual_seed(42)
+    heavy = torch.rand(1, 3000, generator=g) < 0.02
+    big = float(np.log(40.0 / W)) + 0.3 * torch.randn(1, 3000, 2, generator=g)
+    ls = torch.where(heavy[..., None].to(dev), big.to(dev), ls)
+    run_case(mu, ls, col, op, bg, th, H, W, 8, odds=False, fields=False, seed=9)
+    run_case(mu, ls, col, op, bg, th, H, W, 8, odds=True, fields=True, seed=10)
