@@ -6,7 +6,8 @@ through render_alpha_full_triton(cull=True): softplus, binning (decode, count, s
 sort, tile starts), per-tile compositing, and the backward to every splat parameter. Inputs are resident
 in HBM before the timed region. `value` is frames/s x 0.589824 Mpix of the fwd+bwd step.
 
-Also reported: forward-only and the render_alpha_octave entry point, per-stage event times,
+Also reported: forward-only, the render_alpha_octave entry point, the 2048x2048 stress set
+(configs[4]: fwd and fwd+bwd, single-res and octave), per-stage event times,
 the roofline of the dominant kernel from HIP events around its launches (on the stream it runs on), and
 the reference's CPU renderer (render.py math) on a bounded band of the same frame, on the host cores.
 """
@@ -121,6 +122,43 @@ def cpu_baseline(s, rows=(368, 376), threads=None):
                       f"scaled to a full frame; forward only"}
 
 
+def stress_c4(steps, warmup, odds):
+    """2048x2048, 655,360 splats with a 2 % heavy tail; fwd and fwd+bwd, single-res cull and the
+    octave entry point. Reported next to the headline, not as `value`."""
+    s = synth.config("c4").to("cuda")
+    H, W = s.H, s.W
+    gout = s.grad_out.permute(0, 2, 3, 1).contiguous().permute(0, 3, 1, 2)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (s.mu, s.log_scale, s.color, s.opacity, s.bg,
+                                                                  s.theta)]
+
+    def run(octave, bwd):
+        def fn():
+            for t in leaves:
+                t.grad = None
+            with torch.set_grad_enabled(bwd):
+                if octave:
+                    out = RH.render_alpha_octave(*leaves[:5], H, W, theta=leaves[5], odds=odds)
+                else:
+                    out = RH.render_alpha_full_triton(*leaves[:5], H, W, theta=leaves[5], cull=True, odds=odds)
+                if bwd:
+                    out.backward(gout)
+        return fn
+
+    res = {"workload": "2048x2048 RGB, 655,360 splats (2 % heavy tail at ~40 px); configs[4]"}
+    for name, octave, bwd in (("fwd", False, False), ("fwd_bwd", False, True), ("octave_fwd", True, False),
+                              ("octave_fwd_bwd", True, True)):
+        ms, _ = time_loop(run(octave, bwd), steps, warmup)
+        res[name + "_ms"] = round(ms, 4)
+        res[name + "_mpix_s"] = round(H * W / 1e6 / (ms * 1e-3), 2)
+    with torch.no_grad():
+        sc = torch.nn.functional.softplus(s.log_scale) + 1e-4
+        bins = RH._bin(s.mu, sc, s.color, s.opacity, s.theta, H, W, 8, 3.0, with_maps=False)
+    res["pairs"] = bins.tot_b[0]
+    del bins, leaves, s
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,6 +166,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--odds", action="store_true", help="odds compositing instead of alpha")
+    ap.add_argument("--no-c4", action="store_true", help="skip the 2048x2048 stress configuration")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a MIB-MiB copy kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -230,6 +269,8 @@ def main():
         "octave_fwd_bwd_ms": round(ms_oct, 4),
         "wall_ms_per_step": round(wall_ms, 4),
     }
+    if not args.no_c4:
+        line["c4"] = stress_c4(max(5, args.steps // 5), max(2, args.warmup // 5), odds)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(s_cpu)
     print(json.dumps(line), flush=True)

@@ -137,24 +137,60 @@ __device__ __forceinline__ TileAt tile_at(const LevelTable& L, int tb0, int ntil
 // FIELDS: raw sums into the packed per-level fields slog/sa/sac (slot pbase[l] + pixel).
 // Composite (level 0): out, T, asum, fg; with UPS the coarse levels' packed fields (inputs slog/sa/sac) are
 // upsampled and added first, and `asum` keeps the unclamped S_a (the clamp_min gradient needs it).
+// Waves sharing one 8x8 tile in the forward: each composites a contiguous share of the tile's pair list for
+// the tile's 64 pixels, and the partial sums are added in wave order through LDS. More waves per tile hide
+// the scalar-load latency of the record stream and even out tiles of different lengths.
+#ifndef SPLAT_FWD_SPLIT
+#define SPLAT_FWD_SPLIT 4
+#endif
+template <int TILE>
+__host__ __device__ constexpr int fwd_split() { return TILE == 8 ? SPLAT_FWD_SPLIT : 1; }
+template <int TILE>
+__host__ __device__ constexpr int fwd_threads() { return tile_threads(TILE) * fwd_split<TILE>(); }
+
 template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
-__global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_cull(
+__global__ __launch_bounds__(fwd_threads<TILE>()) void k_fwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, float* __restrict__ out, float* __restrict__ Tout,
     float* __restrict__ asum_out, float* __restrict__ fg_out, float* __restrict__ slog, float* __restrict__ sa,
     float* __restrict__ sac) {
+  constexpr int S = fwd_split<TILE>();
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
-  const int l = threadIdx.x;
+  const int l = S > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+  const int wv = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;   // wave-uniform
   const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
   const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
   const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
   const float px = ((float)xp + 0.5f) / (float)ta.W;
-  const int g0 = starts[ta.t], g1 = starts[ta.t + 1];
+  int g0 = starts[ta.t], g1 = starts[ta.t + 1];
+  if (S > 1) {
+    const int chunk = ((g1 - g0 + S - 1) / S + 3) & ~3;
+    g0 = min(g1, g0 + wv * chunk);
+    g1 = min(g1, g0 + chunk);
+  }
   float sl = 0.f, s_a = 0.f, sc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = 0.f;
   fwd_pixel<C, ODDS>(rec, gid, g0, g1, py, px, sl, s_a, sc);
+  if (S > 1) {
+    __shared__ float s_part[S > 1 ? S - 1 : 1][2 + C][64];
+    if (wv > 0) {
+      s_part[wv - 1][0][l] = sl;
+      s_part[wv - 1][1][l] = s_a;
+#pragma unroll
+      for (int c = 0; c < C; ++c) s_part[wv - 1][2 + c][l] = sc[c];
+    }
+    __syncthreads();
+    if (wv > 0) return;
+#pragma unroll
+    for (int w = 0; w < S - 1; ++w) {
+      sl += s_part[w][0][l];
+      s_a += s_part[w][1][l];
+#pragma unroll
+      for (int c = 0; c < C; ++c) sc[c] += s_part[w][2 + c][l];
+    }
+  }
   if (!valid) return;
   const int p = yp * ta.W + xp;
   if (FIELDS) {
@@ -931,8 +967,8 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
       return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
         k_fwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
-            <<<ntiles, tile_threads(TT), 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg,
-                                                  slog, sa, sac);
+            <<<ntiles, fwd_threads<TT>(), 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum,
+                                                   fg, slog, sa, sac);
         return check_launch("k_fwd_cull");
       });
     });

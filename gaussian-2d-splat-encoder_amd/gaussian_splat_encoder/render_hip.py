@@ -347,12 +347,13 @@ def _composite_buffers(B, P, C, dev):
             buf[n * (C + 2):].view(B, P, C))
 
 
-def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False):
+def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
+                  with_maps=True):
     """Composite forward (render_triton.py:538-567): out [B,P,C], (T, asum, fg), bins."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     bgf = _f32(bg)
     flags = FLAG_ODDS if odds else 0
@@ -365,12 +366,13 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     return out, (T, asum, fg), bins
 
 
-def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False):
+def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
+                         with_maps=True):
     """FIELDS forward (render_triton.py:570-599): S_log [B,P], S_a [B,P] (unclamped), S_ac [B,P,C], bins."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps)
     slog, sa, sac = _empty((B, P), dev), _empty((B, P), dev), _empty((B, P, C), dev)
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
@@ -379,14 +381,14 @@ def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=
     return slog, sa, sac, bins
 
 
-def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, with_maps=True):
     """Fused multi-level forward (render_triton.py:879-980 without the per-group torch glue): one binning
     over every level, FIELDS renders of the coarse levels into packed fields, then the level-0 composite
     adds their bilinear upsamples. Returns out [B,P,C], (T, asum unclamped, fg), bins."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, lv=lv)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv=lv)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     L = bins.n_levels
     # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
@@ -524,7 +526,8 @@ class _AlphaRenderCull(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=False):
-        out, (T, asum, fg), bins = _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=odds)
+        out, (T, asum, fg), bins = _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=odds,
+                                                 with_maps=any(ctx.needs_input_grad[:6]))
         ctx.has_theta = theta is not None
         ctx.HW = (H, W, TILE)
         ctx.odds = odds
@@ -549,7 +552,8 @@ class _AlphaRenderCullFields(torch.autograd.Function):
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, odds=False):
         slog, sa, sac, bins = _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=TILE, cutoff=cutoff,
-                                                   max_pairs=max_pairs, odds=odds)
+                                                   max_pairs=max_pairs, odds=odds,
+                                                   with_maps=any(ctx.needs_input_grad[:5]))
         ctx.has_theta = theta is not None
         ctx.HW = (H, W, TILE)
         ctx.odds = odds
@@ -579,7 +583,7 @@ class _AlphaRenderLevels(torch.autograd.Function):
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
         out, (T, asum, fg), bins = _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff,
-                                                   max_pairs, odds, lv)
+                                                   max_pairs, odds, lv, any(ctx.needs_input_grad[:6]))
         ctx.has_theta = theta is not None
         ctx.odds = odds
         ctx.tiles = bins
