@@ -7,7 +7,8 @@ sort, tile starts), per-tile compositing, and the backward to every splat parame
 in HBM before the timed region. `value` is frames/s x 0.589824 Mpix of the fwd+bwd step.
 
 Also reported: forward-only, the render_alpha_octave entry point, the 2048x2048 stress set
-(configs[4]: fwd and fwd+bwd, single-res and octave), per-stage event times,
+(configs[4]: fwd and fwd+bwd, single-res and octave), the encoder end-to-end frame (configs[3]: per-stage
+ms), per-stage event times,
 the roofline of the dominant kernel from HIP events around its launches (on the stream it runs on), and
 the reference's CPU renderer (render.py math) on a bounded band of the same frame, on the host cores.
 """
@@ -101,7 +102,7 @@ def time_loop(fn, steps, warmup):
     return start.elapsed_time(end) / steps, wall
 
 
-def cpu_baseline(s, rows=(368, 376), threads=None):
+def cpu_baseline(s, rows=(368, 400), threads=None):
     """The reference's CPU renderer (render.py:90-110 math, fp32 torch, materialised falloff), restated in
     oracle/render_ref.py, over a band of rows of the same frame; scaled to a full frame."""
     sys.path.insert(0, ROOT)
@@ -159,6 +160,46 @@ def stress_c4(steps, warmup, odds):
     return res
 
 
+def e2e_c3(steps, warmup):
+    """the released checkpoint's encoder architecture with seeded random-init weights (the
+    checkpoint file is not shipped) on a seeded procedural 768x768 card, forward in inference mode as
+    examples/encode_and_render.py runs it: backbone, coarse 384^2 odds octave render, fine decoder + head, then
+    the full 768^2 odds octave render of all 92,160 splats. Per-stage ms are medians of HIP-event spans."""
+    from gaussian_splat_encoder.efficient_encoder import GOLDEN_D256, EfficientGaussianEncoder
+    torch.manual_seed(0)
+    enc = EfficientGaussianEncoder(**GOLDEN_D256).to("cuda").eval()
+    x = synth.procedural_image(768, 768).to("cuda")
+    marks = []
+
+    def mark(name):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        marks.append((name, ev))
+
+    enc.stage_marks = mark
+    spans = {}
+    with torch.inference_mode():
+        for it in range(warmup + steps):
+            marks.clear()
+            mark("start")
+            out = enc(x)
+            RH.render_alpha_octave(out["mu"], out["log_scale"], out["color"], out["opacity"], out["bg"], 768, 768,
+                                   theta=out["theta"], odds=enc.odds)
+            mark("full_render")
+            torch.cuda.synchronize()
+            if it >= warmup:
+                for (_, a), (name, b) in zip(marks[:-1], marks[1:]):
+                    spans.setdefault(name, []).append(a.elapsed_time(b))
+                spans.setdefault("total", []).append(marks[0][1].elapsed_time(marks[-1][1]))
+    med = lambda v: sorted(v)[len(v) // 2]
+    res = {"workload": "768x768 procedural card -> random-init 833,107-parameter adaptive encoder (d=256) -> "
+                       "odds octave renders (384^2 coarse, 768^2 full); configs[3]",
+           "splats": int(out["mu"].shape[1]), "stages_ms": {k: round(med(v), 4) for k, v in spans.items()}}
+    del enc, out, x
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +208,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--odds", action="store_true", help="odds compositing instead of alpha")
     ap.add_argument("--no-c4", action="store_true", help="skip the 2048x2048 stress configuration")
+    ap.add_argument("--no-c3", action="store_true", help="skip the encoder end-to-end configuration")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a MIB-MiB copy kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -271,6 +313,8 @@ def main():
     }
     if not args.no_c4:
         line["c4"] = stress_c4(max(5, args.steps // 5), max(2, args.warmup // 5), odds)
+    if not args.no_c3:
+        line["c3"] = e2e_c3(max(10, args.steps // 2), max(3, args.warmup // 2))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(s_cpu)
     print(json.dumps(line), flush=True)

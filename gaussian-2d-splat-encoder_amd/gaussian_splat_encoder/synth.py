@@ -12,6 +12,8 @@ Configurations:
   c4 : 2048x2048, 655,360 splats (10 per cell on a 256x256 grid) as c1, with 2 % of the splats
        re-drawn at log-scale ~ N(log 40 px, 0.3) (the heavy tail that stresses binning balance).
 "Log-scale ~ N(log k px, s)" means the raw log_scale = ln(k / H) + s * z, before softplus.
+  procedural_image : the encoder input of config c3, a seeded RGB card (linear gradient, filled circles and
+       rectangles) quantised to uint8 and returned as float in [0, 1].
 """
 
 from __future__ import annotations
@@ -99,3 +101,27 @@ def config(name: str, seed: int = 0) -> SplatSet:
     if name == "c4":
         return grid_set(2048, seed=seed, heavy_frac=0.02, with_grad=True)
     raise ValueError(f"unknown config {name!r}")
+
+
+def procedural_image(H: int, W: int, seed: int = 0, n_shapes: int = 24) -> torch.Tensor:
+    """[1, 3, H, W] float in [0, 1]: a linear colour gradient in a random direction with `n_shapes` filled
+    circles and axis-aligned rectangles of random colour on top, quantised to uint8 (config c3's input)."""
+    g = torch.Generator().manual_seed(seed)
+    yy, xx = torch.meshgrid((torch.arange(H) + 0.5) / H, (torch.arange(W) + 0.5) / W, indexing="ij")
+    c0, c1 = torch.rand(3, generator=g), torch.rand(3, generator=g)
+    ang = float(torch.rand(1, generator=g)) * 2 * math.pi
+    t = math.cos(ang) * xx + math.sin(ang) * yy
+    t = (t - t.min()) / (t.max() - t.min())
+    img = c0[:, None, None] * (1 - t) + c1[:, None, None] * t
+    for _ in range(n_shapes):
+        kind = int(torch.randint(0, 2, (1,), generator=g))
+        col = torch.rand(3, generator=g)
+        cy, cx = torch.rand(2, generator=g).tolist()
+        a, b = (0.02 + 0.15 * torch.rand(2, generator=g)).tolist()
+        if kind == 0:
+            m = (yy - cy) ** 2 + (xx - cx) ** 2 < a * a
+        else:
+            m = ((yy - cy).abs() < a) & ((xx - cx).abs() < b)
+        img[:, m] = col[:, None]
+    u8 = (img * 255).round().clamp(0, 255).to(torch.uint8)
+    return (u8.float() / 255).unsqueeze(0)

@@ -10,6 +10,7 @@ Reference map:
   exact                          render.py:34-58, 61-65, 90-110 (materialised, linspace pixel centres)
   odds_exact                     render_triton.py:1431-1457 (`_torch_odds_ref`)
   multires / octave              render_triton.py:864-922, 925-980
+  octave_forward_c               render_triton.py:935-980 forward with the C oracle's fields (full-size frames)
   render_alpha_full_f32          render.py:90-110 in float32: the CPU baseline (reference's own CPU path)
 """
 
@@ -238,3 +239,29 @@ def render_alpha_full_f32(mu, log_scale, color, opacity, bg, H, W, theta=None, c
         fg = torch.bmm(alpha, color) / asum[..., None]
         out.append((1.0 - T)[..., None] * fg + T[..., None] * bg[:, None])
     return torch.cat(out, 1)
+
+
+def octave_forward_c(mu, scale, color, opacity, bg, theta, H, W, cutoff=3.0, TILE=8, base_texels=8.0,
+                     max_octaves=6, odds=False):
+    """render_triton.py:935-980 forward for one batch with the fields from the float64 C oracle (fast enough
+    for full-size frames): octave routing on the fp32 activated `scale`, per-octave binning and fields, then
+    float64 upsample + sum + composite. Inputs are fp32 CPU tensors; returns the image [P, C] float64."""
+    from . import c_oracle
+    sc = scale.detach().float().cpu()
+    np32 = lambda t: None if t is None else t.detach().float().cpu().numpy()
+    mu_, sc_, col_, op_, th_ = np32(mu), sc.numpy(), np32(color), np32(opacity), np32(theta)
+    oct_ = octave_of(sc, H, W, base_texels, max_octaves).numpy()
+    P, C = H * W, col_.shape[-1]
+    S = [torch.zeros(P, dtype=f64), torch.zeros(P, dtype=f64), torch.zeros(P, C, dtype=f64)]
+    for o in range(max_octaves + 1):
+        idx = np.nonzero(oct_ == o)[0]
+        if idx.size == 0:
+            continue
+        Ho, Wo = max(8, H >> o), max(8, W >> o)
+        sub = lambda a: None if a is None else np.ascontiguousarray(a[idx])
+        gid, st = c_oracle.build_tiles(sub(mu_), sub(sc_), Ho, Wo, TILE, cutoff)
+        f = [torch.from_numpy(np.ascontiguousarray(x)) for x in
+             c_oracle.fwd_cull(sub(mu_), sub(sc_), sub(th_), sub(op_), sub(col_), gid, st, Ho, Wo, TILE, odds=odds,
+                               fields=True)]
+        S = [a + (b if o == 0 else upsample_field(b, Ho, Wo, H, W)) for a, b in zip(S, f)]
+    return composite(*S, torch.as_tensor(np32(bg), dtype=f64), straight_through=False)[0]
