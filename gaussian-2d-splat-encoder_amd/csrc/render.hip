@@ -288,46 +288,45 @@ struct PairSums {
   }
 };
 
-// One pixel-pair of the backward, given whitened offsets u, v. Fast path: a = op * f (no lane of the wave
-// can be on the clamp while op * f <= kNearOpaque < 1 - 1e-4). When some lane of the wave is near-opaque,
-// a is clamped, 1 - a is evaluated as in one_minus_alpha, and the clamp gates the falloff that multiplies
-// da (render_triton.py:686, 697). The branch is wave-uniform; every lane of the wave must be executing.
+// The backward evaluates 1 - a = 1 - op * f with one fma while op * f <= kNearOpaqueBwd: the rounding of
+// the hardware exp2 (about 1 ulp of f) then costs at most ~1.2e-5 of 1 - a, and of the 1 / (1 - a) factors
+// of the gradient. Above it (op * f within 1e-2 of 1, at most a few pixels around the centre of a
+// near-opaque splat) 1 - a is evaluated as (1 - op) + op (1 - f) with a series for 1 - f.
+constexpr float kNearOpaqueBwd = 0.99f;
+
+// Per-pair constants of the backward loop: opacity, the falloff above which op * f > kNearOpaqueBwd, and 1/op.
+struct PairOp {
+  float op, thr, rop;
+};
+__device__ __forceinline__ PairOp pair_op(float op) {
+  const float rop = hw_rcp(op);
+  return {op, kNearOpaqueBwd * rop, rop};
+}
+
+// Accumulation of one pixel-pair of the backward from its falloff f (0 for a lane on the clamp) and 1 - a.
+// The colour sums are accumulated as sum w' * dS_ac with w' = w / op (the caller multiplies by op once per
+// pair).
 template <int C, bool ODDS>
-__device__ __forceinline__ void bwd_px(float u, float v, float op, const float4& col, const float4& pa,
-                                       const float4& pb, PairSums<C>& s) {
-  const float m = fmaf(u, u, v * v);
-  const float f = hw_exp2(-m);
-  const float fo = op * f;
-  float a = fo, oma = 1.f - fo, fq = f;
-  if (__any(fo > kNearOpaque)) {
-    a = fminf(fo, kClamp);
-    const float x = m * kLn2;
-    float p = fmaf(x, 1.f / 120.f, -1.f / 24.f);
-    p = fmaf(p, x, 1.f / 6.f);
-    p = fmaf(p, x, -0.5f);
-    p = fmaf(p, x, 1.f);
-    const float acc = fmaxf(fmaf(op, p * x, 1.f - op), 1.f - kClamp);
-    oma = fo > kNearOpaque ? acc : oma;
-    fq = fo < kClamp ? f : 0.f;
-  }
+__device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, const float4& col, const float4& pa,
+                                        const float4& pb, PairSums<C>& s) {
   const float rr = hw_rcp(oma);
-  float ct = pa.z * col.x;
+  float ct = fmaf(pa.z, col.x, pa.y);   // dS_a + sum_c dS_ac[c] col[c]
   if (C > 1) ct = fmaf(pa.w, col.y, ct);
   if (C > 2) ct = fmaf(pb.x, col.z, ct);
   if (C > 3) ct = fmaf(pb.y, col.w, ct);
   float da, cw;
   if (ODDS) {
-    da = fmaf(-pa.x, rr, (pa.y + ct) * (rr * rr));
-    cw = a * rr;
+    da = fmaf(-pa.x, rr, ct * (rr * rr));
+    cw = f * rr;
   } else {
-    da = fmaf(-pa.x, rr, pa.y + ct);
-    cw = a;
+    da = fmaf(-pa.x, rr, ct);
+    cw = f;
   }
   s.gc[0] = fmaf(cw, pa.z, s.gc[0]);
   if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
   if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
   if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
-  const float q = da * fq;
+  const float q = da * f;
   const float qu = q * u, qv = q * v;
   s.q += q;
   s.qu += qu;
@@ -335,6 +334,46 @@ __device__ __forceinline__ void bwd_px(float u, float v, float op, const float4&
   s.quu = fmaf(qu, u, s.quu);
   s.qvv = fmaf(qv, v, s.qvv);
   s.quv = fmaf(qu, v, s.quv);
+}
+
+// One pixel-pair where some lane may be near-opaque (per-lane selection, no wave-level branch): 1 - a as in
+// one_minus_alpha above kNearOpaqueBwd; a lane on the clamp (a = 1 - 1e-4) has no gradient through the
+// falloff (render_triton.py:686, 697), so it adds its colour term here and continues with f = 0.
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_px_near(float u, float v, float m, float f, const PairOp& po, const float4& col,
+                                            const float4& pa, const float4& pb, PairSums<C>& s) {
+  const float fo = po.op * f;
+  float oma = fmaf(-po.op, f, 1.f);
+  if (fo > kNearOpaqueBwd) {
+    const float x = m * kLn2;
+    float p = fmaf(x, 1.f / 120.f, -1.f / 24.f);
+    p = fmaf(p, x, 1.f / 6.f);
+    p = fmaf(p, x, -0.5f);
+    p = fmaf(p, x, 1.f);
+    oma = fmaxf(fmaf(po.op, p * x, 1.f - po.op), 1.f - kClamp);
+    if (!(fo < kClamp)) {
+      const float cw = ODDS ? kClamp * po.rop * hw_rcp(oma) : kClamp * po.rop;   // min(op f, clamp) w / (a op)
+      s.gc[0] = fmaf(cw, pa.z, s.gc[0]);
+      if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
+      if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
+      if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
+      f = 0.f;
+    }
+  }
+  bwd_acc<C, ODDS>(u, v, f, oma, col, pa, pb, s);
+}
+
+// One pixel-pair of the backward, given whitened offsets u, v, with its own wave-uniform choice between the
+// one-fma 1 - a and bwd_px_near (every lane of the wave must be executing).
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_px(float u, float v, const PairOp& po, const float4& col, const float4& pa,
+                                       const float4& pb, PairSums<C>& s) {
+  const float m = fmaf(u, u, v * v);
+  const float f = hw_exp2(-m);
+  if (__any(f > po.thr))
+    bwd_px_near<C, ODDS>(u, v, m, f, po, col, pa, pb, s);
+  else
+    bwd_acc<C, ODDS>(u, v, f, fmaf(-po.op, f, 1.f), col, pa, pb, s);
 }
 
 template <int C>
@@ -349,12 +388,13 @@ __device__ __forceinline__ void xor_reduce(PairSums<C>& s, int d) {
   for (int c = 0; c < C; ++c) s.gc[c] += __shfl_xor(s.gc[c], d, 64);
 }
 
-// Record of splat-major pair q at psum + q * pair_rec<C>() (4-byte aligned).
+// Record of splat-major pair q at psum + q * pair_rec<C>() (4-byte aligned); the colour sums get the
+// pair's opacity factor here.
 template <int C>
-__device__ __forceinline__ void store_pair(float* __restrict__ dst, const PairSums<C>& s) {
+__device__ __forceinline__ void store_pair(float* __restrict__ dst, const PairSums<C>& s, float op) {
   dst[0] = s.q; dst[1] = s.qu; dst[2] = s.qv; dst[3] = s.quu; dst[4] = s.qvv; dst[5] = s.quv;
 #pragma unroll
-  for (int c = 0; c < C; ++c) dst[6 + c] = s.gc[c];
+  for (int c = 0; c < C; ++c) dst[6 + c] = op * s.gc[c];
 }
 
 // Per-splat sums (Q, Qu, Qv, Quu, Qvv, Quv, colour[C]) -> parameter gradients (formulas at the top).
@@ -379,11 +419,94 @@ __device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec
   for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = sums[6 + c];
 }
 
+// log2(kNearOpaqueBwd), and a margin on the exponent bound below that covers the rounding of m and of the
+// hardware exp2 (op * f > kNearOpaqueBwd needs m < log2(op) - log2(kNearOpaqueBwd); the clamp needs 0.0144
+// less than that).
+constexpr float kLog2NearOpaqueBwd = -0.014499569695115f;
+constexpr float kNearMargin = 1e-3f;
+
+// Whether op * falloff can exceed kNearOpaqueBwd at a pixel centre in the box [y0, y1] x [x0, x1]: with
+// m = u^2 + v^2 >= kWhiten^2 (dy^2 + dx^2) / max(sy, sx)^2, a splat centre farther than
+// max(sy, sx) sqrt(log2(op / kNearOpaqueBwd)) / kWhiten from the box cannot reach it.
+__device__ __forceinline__ bool near_possible(float op, float lop, float gy, float gx, float smax, float y0, float y1,
+                                              float x0, float x1) {
+  const float dy = fmaxf(fmaxf(y0 - gy, gy - y1), 0.f);
+  const float dx = fmaxf(fmaxf(x0 - gx, gx - x1), 0.f);
+  const float d2 = fmaf(dy, dy, dx * dx) * (kWhiten * kWhiten);
+  return op > kNearOpaqueBwd && d2 < smax * smax * (lop - kLog2NearOpaqueBwd + kNearMargin);
+}
+
+// Per-pair sums over the TILE x TILE pixels of a tile (lane = pair), with 1 - a = 1 - op f by one fma:
+// the caller has taken every pair that may be near-opaque in the tile (near_possible) out of the wave's
+// lanes. Straight-line, every pixel of a row unrolled; the row's first pixel index is copied into a VGPR
+// once per row, so the row's LDS reads take constant offsets from it.
+template <int C, bool ODDS, int TILE>
+__device__ __forceinline__ void pair_tile(float gy, float gx, float A, float B, float Cc, float D, float op,
+                                          const float4& col, const float* s_py, const float* s_px, const float4* s_pa,
+                                          const float4* s_pb, PairSums<C>& s) {
+  constexpr int kUnrollX = TILE < 8 ? TILE : 8;
+#pragma nounroll
+  for (int yy = 0; yy < TILE; ++yy) {
+    const float dy = s_py[yy] - gy;
+    const float uy = A * dy, vy = Cc * dy;
+    int row;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(row) : "s"(yy * TILE));
+    const float4* pa_row = s_pa + row;
+    const float4* pb_row = s_pb + row;
+#pragma unroll kUnrollX
+    for (int xx = 0; xx < TILE; ++xx) {
+      const float4 pa = pa_row[xx];
+      const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float dx = s_px[xx] - gx;
+      const float u = fmaf(B, dx, uy), v = fmaf(D, dx, vy);
+      const float f = hw_exp2(-fmaf(u, u, v * v));
+      bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, pa, pb, s);
+    }
+  }
+}
+
+// A lane whose pair was taken out: geometry for which u = 1e30 * (py + 16) is finite and u^2 overflows, so
+// the falloff is 0 at every pixel, 1 - a = 1 and every sum of the lane stays 0.
+__device__ __forceinline__ void mute_pair(bool mute, float& gy, float& A, float& B, float& Cc, float& D) {
+  if (mute) {
+    gy = -16.f;
+    A = 1e30f;
+    B = Cc = D = 0.f;
+  }
+}
+
+// Sums of pair g (wave-uniform) over the tile's pixels with lane = pixel and 1 - a evaluated carefully at
+// every pixel (bwd_px_near), reduced over the wave: every lane returns the totals. For the pairs taken out
+// of the lane-per-pair loops (a few near-opaque splats around their centre tile).
+template <int C, bool ODDS, int TILE>
+__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, const float* s_py,
+                                                    const float* s_px, const float4* s_pa, const float4* s_pb,
+                                                    int lane, float& op) {
+  const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+  const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
+  const PairOp po = pair_op(r1.z);
+  op = r1.z;
+  PairSums<C> s;
+  for (int l = lane; l < TILE * TILE; l += 64) {
+    const float dy = s_py[l / TILE] - r0.x, dx = s_px[l % TILE] - r0.y;
+    const float u = fmaf(r0.z, dy, r0.w * dx), v = fmaf(r1.x, dy, r1.y * dx);
+    const float m = fmaf(u, u, v * v);
+    const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
+    bwd_px_near<C, ODDS>(u, v, m, hw_exp2(-m), po, col, s_pa[l], pb, s);
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) xor_reduce<C>(s, d);
+  return s;
+}
+
 // Backward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
 // Composite (level 0): upstream from T/asum/fg/gout (see pixel_upstream for UPS); per-tile partials of
 // sum_p gout * T go to bg_part[c * ntiles + (t - tb0)]. FIELDS: upstream from the packed fields.
+// One wave per tile: the per-pixel upstream terms are staged in LDS, then the wave takes the tile's pairs
+// 64 at a time (lane = pair). At 6 waves per SIMD (at most 80 VGPRs) there are enough waves to cover the
+// latency of the VALU, LDS and transcendental pipes.
 template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_bwd_cull(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
@@ -423,34 +546,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
   __syncthreads();
   const int g0 = starts[t], g1 = starts[t + 1];
   const int n = g1 - g0;
+  const int nfull = n >> 6;
   // full chunks: lane = pair, every pixel of the tile, row / column terms factored out of u and v
-  for (int i0 = g0; i0 + 64 <= g1; i0 += 64) {
-    const int i = i0 + lane;
+  for (int k = 0; k < nfull; ++k) {
+    const int i = g0 + 64 * k + lane;
     const int g = gid[i];
     const int q = pair_q[i];
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
-    float bdx[TILE], ddx[TILE];
-#pragma unroll
-    for (int xx = 0; xx < TILE; ++xx) {
-      const float dx = s_px[xx] - gx;
-      bdx[xx] = B * dx;
-      ddx[xx] = D * dx;
-    }
+    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y;
+    const float op = r1.z;
+    const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
+    const bool near = near_possible(op, r1.w, gy, gx, fmaxf(sc.x, sc.y), s_py[0], s_py[TILE - 1], s_px[0],
+                                    s_px[TILE - 1]);
+    float mgy = gy, mA = A, mB = B, mCc = Cc, mD = D;
+    mute_pair(near, mgy, mA, mB, mCc, mD);
     PairSums<C> s;
-    for (int yy = 0; yy < TILE; ++yy) {
-      const float dy = s_py[yy] - gy;
-      const float uy = A * dy, vy = Cc * dy;
-#pragma unroll
-      for (int xx = 0; xx < TILE; ++xx) {
-        const int l = yy * TILE + xx;
-        const float4 pa = s_pa[l];
-        const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-        bwd_px<C, ODDS>(uy + bdx[xx], vy + ddx[xx], op, col, pa, pb, s);
-      }
+    pair_tile<C, ODDS, TILE>(mgy, gx, mA, mB, mCc, mD, op, col, s_py, s_px, s_pa, s_pb, s);
+    if (!near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
+    for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
+      const int j = __builtin_ctzll(nm);
+      float opj;
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_py, s_px, s_pa,
+                                                          s_pb, lane, opj);
+      if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
     }
-    store_pair<C>(psum + (size_t)q * pair_rec<C>(), s);
   }
   // remainder of r < 64 pairs: L lanes per pair (largest power of two with r * L <= 64, L <= pixels),
   // each lane covering NP / L consecutive pixels; the L partial sums are combined with xor shuffles.
@@ -464,18 +584,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     const int g = act ? gid[i] : 0;
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
+    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y;
+    const float op = r1.z;
+    const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
     const int npx = NP / L, j0 = sub * npx;
+    const bool near = act && near_possible(op, r1.w, gy, gx, fmaxf(sc.x, sc.y), s_py[0], s_py[TILE - 1], s_px[0],
+                                           s_px[TILE - 1]);
+    float mgy = gy, mA = A, mB = B, mCc = Cc, mD = D;
+    mute_pair(near, mgy, mA, mB, mCc, mD);
     PairSums<C> s;
     for (int jj = 0; jj < npx; ++jj) {
       const int l = j0 + jj;
-      const float dy = s_py[l / TILE] - gy, dx = s_px[l % TILE] - gx;
-      const float4 pa = s_pa[l];
+      const float dy = s_py[l / TILE] - mgy, dx = s_px[l % TILE] - gx;
       const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-      bwd_px<C, ODDS>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, col, pa, pb, s);
+      const float u = fmaf(mA, dy, mB * dx), v = fmaf(mCc, dy, mD * dx);
+      const float f = hw_exp2(-fmaf(u, u, v * v));
+      bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, s_pa[l], pb, s);
     }
     for (int d = 1; d < L; d <<= 1) xor_reduce<C>(s, d);
-    if (act && sub == 0) store_pair<C>(psum + (size_t)pair_q[i] * pair_rec<C>(), s);
+    const int q = act ? pair_q[i] : 0;
+    if (act && sub == 0 && !near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
+    for (unsigned long long nm = __ballot(near && sub == 0); nm; nm &= nm - 1) {
+      const int j = __builtin_ctzll(nm);
+      float opj;
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_py, s_px, s_pa,
+                                                          s_pb, lane, opj);
+      if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
+    }
   }
 }
 
@@ -696,7 +831,8 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
   const int gs = g < N ? g : N - 1;
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)gs * 4;
   const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-  const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y, op = r1.z;
+  const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y;
+  const PairOp po = pair_op(r1.z);
   PairSums<C> s;
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int p0 = 0; p0 < P; p0 += 64) {
@@ -716,7 +852,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
     for (int j = 0; j < np; ++j) {
       const float2 q = s_pyx[j];
       const float dy = q.x - gy, dx = q.y - gx;
-      bwd_px<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), op, col, s_pa[j],
+      bwd_px<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), po, col, s_pa[j],
                                C > 2 ? s_pb[j] : make_float4(0.f, 0.f, 0.f, 0.f), s);
     }
   }
@@ -724,7 +860,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
   float* dst = acc + (size_t)g * kAcc;
   dst[0] = s.q; dst[1] = s.qu; dst[2] = s.qv; dst[3] = s.quu; dst[4] = s.qvv; dst[5] = s.quv;
 #pragma unroll
-  for (int c = 0; c < C; ++c) dst[6 + c] = s.gc[c];
+  for (int c = 0; c < C; ++c) dst[6 + c] = po.op * s.gc[c];
 }
 
 // sum_p gout[p, c] * T[p] partials over 256-pixel chunks (the exact path's g_bg, render_triton.py:301).
