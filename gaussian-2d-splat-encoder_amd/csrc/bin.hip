@@ -249,6 +249,16 @@ __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offs
   if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
 }
 
+// Pair count of a pair-phase launch. With `info` (a launch queued before the host has read the count,
+// sized for `cap` pairs): the count written by the count phase, or 0 when it exceeds cap or the count phase
+// flagged an error (the launch then leaves an empty pair list and the host redoes the pair phase).
+// Without `info`: cap is the count.
+__device__ __forceinline__ int pair_count(const long long* __restrict__ info, int cap) {
+  if (!info) return cap;
+  const long long t = info[0];
+  return (t > cap || (info[1] & 3)) ? 0 : (int)t;
+}
+
 // ----------------------------------------------------------------------------------------------------
 // pair expansion (render_triton.py:396-404): pair p belongs to the last splat g with offsets[g] <= p, and
 // k = p - offsets[g] walks that splat's rect row by row.
@@ -325,7 +335,8 @@ __device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
 // LDS, and the pair loop reads only LDS. Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat
 // (optional) and, with `hist` set, the block's histogram of the first radix digit.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
-                                                          int N, LevelTable L, int tot, int dmask, int* __restrict__ keys,
+                                                          int N, LevelTable L, const long long* __restrict__ info,
+                                                          int cap, int dmask, int* __restrict__ keys,
                                                           int* __restrict__ vals, int* __restrict__ pair_splat,
                                                           int* __restrict__ hist, int nblocks) {
   __shared__ int4 s_own4[kSortKeys / 4];
@@ -335,7 +346,13 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
   __shared__ int s_w[kWaves];
   int* s_own = reinterpret_cast<int*>(s_own4);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tot = pair_count(info, cap);
   const int p_base = blockIdx.x * kSortKeys;
+  if (p_base >= tot) {   // a block past the pairs of this launch: an empty histogram column
+    if (hist)
+      for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = 0;
+    return;
+  }
   const int n_here = min(kSortKeys, tot - p_base);
   const int p_last = p_base + n_here - 1;
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
@@ -422,9 +439,11 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
   for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
 }
 
-__global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ keys, int tot, int shift, int dmask,
-                                                       int* __restrict__ hist, int nblocks) {
+__global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ keys, const long long* __restrict__ info,
+                                                       int cap, int shift, int dmask, int* __restrict__ hist,
+                                                       int nblocks) {
   __shared__ int s_hist[256];
+  const int tot = pair_count(info, cap);
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
   __syncthreads();
   const int p_base = blockIdx.x * kSortKeys;
@@ -466,7 +485,8 @@ __global__ __launch_bounds__(kBlock) void k_hist_row_scan(int* __restrict__ hist
 // run of the block lands in consecutive global positions: the digit's global start (prefix of the row
 // totals) plus the block's offset within the digit (the row-scanned histogram).
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
-                                                          int tot, int shift, int dbits, const int* __restrict__ hist_scan,
+                                                          const long long* __restrict__ info, int cap, int shift,
+                                                          int dbits, const int* __restrict__ hist_scan,
                                                           const int* __restrict__ rowtot, int nblocks,
                                                           int* __restrict__ keys_out, int* __restrict__ vals_out) {
   __shared__ int s_cnt[kWaves][256];
@@ -477,6 +497,8 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
   __shared__ int s_w[kWaves];
   const int dmask = (1 << dbits) - 1;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tot = pair_count(info, cap);
+  if ((int)blockIdx.x * kSortKeys >= tot) return;   // no keys here (uniform: before any barrier)
   for (int i = threadIdx.x; i < kWaves * 256; i += kBlock) (&s_cnt[0][0])[i] = 0;
   {
     const int d = threadIdx.x;   // kBlock == 256 >= radix
@@ -547,11 +569,18 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
 // render_triton.py:408) and, optionally, pair_q[i] = the splat-major index of sorted pair i:
 // q = offsets[g] + (ty - ty0) * w + (tx - tx0), the pair's index in its splat's rect walk (tile coordinates
 // local to the splat's level).
-__global__ __launch_bounds__(kBlock) void k_tile_starts_q(const int* __restrict__ keys, const int* __restrict__ gids,
-                                                          int tot, int nt, LevelTable L, const int4* __restrict__ rect,
+__global__ __launch_bounds__(kBlock) void k_tile_starts_q(const int* __restrict__ keys, int* __restrict__ gids,
+                                                          const long long* __restrict__ info, int cap, int nt,
+                                                          LevelTable L, const int4* __restrict__ rect,
                                                           const int* __restrict__ offsets, int* __restrict__ starts,
                                                           int* __restrict__ pair_q) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
+  const int tot = pair_count(info, cap);
+  if (tot == 0) {   // empty list: all starts 0 and gid_sorted = {0} (render_triton.py:392-394)
+    if (i <= nt) starts[i] = 0;
+    if (i == 0) gids[0] = 0;
+    return;
+  }
   if (i >= tot) return;
   const int k = keys[i];
   const int prev = i ? keys[i - 1] : -1;
@@ -669,9 +698,12 @@ int bin_count_launch(const float* mu, const float* scale, const float* theta, co
   return check_launch("splat_bin_count");
 }
 
-// Launches of the pair phase for `tot` pairs. Arguments already validated; ws holds plan_pairs(nt, tot).
-int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTable& L, int t, int* gid_sorted,
-                     int* tile_starts, int* pair_splat, int* pair_q, void* ws, hipStream_t st) {
+// Launches of the pair phase. Exact (dinfo NULL): `t` is the pair count. Speculative (dinfo = the count
+// phase's device info): `t` is the capacity the buffers and the grids are sized for, and the kernels take
+// the count from dinfo (an empty list when it exceeds t). Arguments already validated; ws holds
+// plan_pairs(nt, t).
+int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTable& L, int t, const long long* dinfo,
+                     int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws, hipStream_t st) {
   const int nt = L.tbase[L.n];
   const PairsPlan pl = plan_pairs(nt, t);
   if (t == 0) {
@@ -693,24 +725,34 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
   K[fin] = keys_a; K[1 - fin] = keys_b;
   V[fin] = gid_sorted; V[1 - fin] = vals_b;
   const int dmask = pl.radix - 1;
-  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, t, dmask, K[0], V[0],
-                                              pair_splat, pl.passes ? hist : nullptr, pl.nblk);
+  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, dmask, K[0],
+                                              V[0], pair_splat, pl.passes ? hist : nullptr, pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
   for (int pass = 0; pass < pl.passes; ++pass) {
     const int shift = pass * pl.dbits;
     const int src = pass & 1, dst = 1 - src;
-    if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], t, shift, dmask, hist, pl.nblk);
+    if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], dinfo, t, shift, dmask, hist, pl.nblk);
     k_hist_row_scan<<<pl.radix, kBlock, 0, st>>>(hist, pl.nblk, rowtot);
-    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], t, shift, pl.dbits, hist, rowtot, pl.nblk, K[dst],
-                                                V[dst]);
+    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk,
+                                                K[dst], V[dst]);
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
   }
-  k_tile_starts_q<<<div_up(t, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, t, nt, L,
-                                                        reinterpret_cast<const int4*>(rect), offsets, tile_starts,
-                                                        pair_q);
+  const int nthr = t > nt + 1 ? t : nt + 1;
+  k_tile_starts_q<<<div_up(nthr, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, dinfo, t, nt, L,
+                                                           reinterpret_cast<const int4*>(rect), offsets, tile_starts,
+                                                           pair_q);
   return check_launch("k_tile_starts_q");
+}
+
+// One event per thread and device, recorded after the read-back of the pair count (splat_bin).
+hipEvent_t readback_event() {
+  static thread_local hipEvent_t ev[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!ev[dev] && hipEventCreateWithFlags(&ev[dev], hipEventDisableTiming) != hipSuccess) ev[dev] = nullptr;
+  return ev[dev];
 }
 
 }  // namespace
@@ -747,7 +789,7 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
   if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_pairs: bad levels");
   const PairsPlan pl = plan_pairs(L.tbase[L.n], tot);
   if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
-  return bin_pairs_launch(rect, offsets, N, L, (int)tot, gid_sorted, tile_starts, pair_splat, pair_q, ws,
+  return bin_pairs_launch(rect, offsets, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws,
                           (hipStream_t)stream);
 }
 
@@ -768,10 +810,21 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, rec, rect, offsets, info,
                             ws_count, st);
   if (rc) return rc;
-  // the one device -> host read of the render: totals and error bits, then wait for it
-  if (hipMemcpyAsync(info_host, info, sizeof(long long) * (2 + L.n), hipMemcpyDeviceToHost, st) != hipSuccess ||
-      hipStreamSynchronize(st) != hipSuccess)
-    return set_error(kHipError, "splat_bin: reading the pair totals failed");
+  // the one device -> host read of the render: totals and error bits
+  hipEvent_t ev = readback_event();
+  if (!ev || hipMemcpyAsync(info_host, info, sizeof(long long) * (2 + L.n), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipEventRecord(ev, st) != hipSuccess)
+    return set_error(kHipError, "splat_bin: queueing the read of the pair totals failed");
+  // With buffers for pair_cap > 0 pairs the pair phase is queued before the host waits for the count: the GPU
+  // goes on with it while the host reads the count (kernels past the count, or past pair_cap, do nothing).
+  const bool spec = pair_cap > 0 && pair_cap <= 0x7fffffffLL - 64 && gid_sorted && tile_starts &&
+                    ws_pairs_bytes >= plan_pairs(L.tbase[L.n], pair_cap).total;
+  if (spec) {
+    rc = bin_pairs_launch(rect, offsets, N, L, (int)pair_cap, info, gid_sorted, tile_starts, pair_splat, pair_q,
+                          ws_pairs, st);
+    if (rc) return rc;
+  }
+  if (hipEventSynchronize(ev) != hipSuccess) return set_error(kHipError, "splat_bin: reading the pair totals failed");
   const long long tot = info_host[0];
   if (info_host[1] & 1) return set_error(kInvalid, "splat_bin: a splat has an empty tile rect (negative cutoff or scale)");
   if (info_host[1] & 2) return set_error(kOverflow, "splat_bin: %lld pairs exceed the int32 pair index range", tot);
@@ -781,9 +834,11 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
         return set_error(kBudget, "splat_bin: %lld pairs on level %d exceed the budget of %lld", info_host[2 + l], l,
                          max_pairs);
   if (tot > pair_cap) return set_error(kCapacity, "splat_bin: %lld pairs exceed the capacity %lld", tot, pair_cap);
+  if (spec) return kOk;
   if (!gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin: null pair buffers");
   if (ws_pairs_bytes < plan_pairs(L.tbase[L.n], tot).total) return set_error(kWorkspace, "splat_bin: pair workspace too small");
-  return bin_pairs_launch(rect, offsets, N, L, (int)tot, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs, st);
+  return bin_pairs_launch(rect, offsets, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs,
+                          st);
 }
 
 }  // extern "C"

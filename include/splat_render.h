@@ -2,7 +2,7 @@
  *
  * Every entry point takes raw device pointers (fp32 / int32, contiguous), sizes and a hipStream_t passed
  * as `void *stream`; all work is enqueued on that stream. No entry point allocates; only splat_bin
- * waits (for the one read-back of the pair totals that sizes the pair buffers).
+ * waits (for the one read-back of the pair totals that sizes the pair buffers and applies the budget).
  * Buffers are owned by the caller; scratch memory comes in as (ws, ws_bytes), sized by the matching
  * *_workspace_bytes query. Every call returns 0 on success or a status code, with a message available
  * from splat_last_error() (thread-local):
@@ -89,12 +89,17 @@ int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, in
                     int *pair_splat, int *pair_q, void *ws, size_t ws_bytes, void *stream);
 
 /* Binning in one call: phase 1 (splat_bin_count), one read of info into pinned host memory info_host
- * (2 + L int64) with a wait on `stream`, then phase 2 (splat_bin_pairs) when the pairs fit. Statuses:
- *   0 the pair phase ran into gid_sorted / tile_starts / pair_splat / pair_q (capacity pair_cap pairs;
- *     ws_pairs sized by splat_bin_pairs_workspace_bytes(N, nt, pair_cap));
- *   6 tot > pair_cap: nothing pair-sized was touched; the caller sizes buffers from info_host[0] and calls
- *     splat_bin_pairs;
- *   7 some level holds more than max_pairs pairs (max_pairs < 0: no budget), before any pair work;
+ * (2 + L int64), then phase 2 (splat_bin_pairs). With pair_cap > 0 (buffers for pair_cap pairs, ws_pairs
+ * sized by splat_bin_pairs_workspace_bytes(N, nt, pair_cap)) phase 2 is queued BEFORE the host waits for
+ * the read: its kernels take the pair count from info on the device, so the GPU runs the pair phase while
+ * the host checks the count; a count above pair_cap (or an error bit) makes that launch write an empty
+ * list (starts 0, gid_sorted[0] = 0) and nothing else. With pair_cap = 0 the host waits first. The call
+ * returns after the read has completed; the pair phase may still be running on `stream`. Statuses:
+ *   0 the pair phase ran into gid_sorted / tile_starts / pair_splat / pair_q;
+ *   6 tot > pair_cap: the caller sizes buffers from info_host[0] and calls splat_bin_pairs (any speculative
+ *     launch wrote only its empty list into the given buffers);
+ *   7 some level holds more than max_pairs pairs (max_pairs < 0: no budget); no buffer beyond pair_cap
+ *     was needed;
  *   1 / 4 the error bits of info (empty rect, int32 overflow).
  * Replaces render_triton.py:351-409 with its one sync (:391) and budget check (:378-385). */
 int splat_bin(const float *mu, const float *scale, const float *theta, const float *opacity,

@@ -72,3 +72,39 @@ def test_pair_budget_raises_before_allocation(dev):
     sc = activate_scale(s.log_scale.to(dev))
     with pytest.raises(RH.PairBudgetExceeded):
         RH._build_tiles(mu, sc, s.H, s.W, 8, 3.0, max_pairs=100)
+
+
+# Once a binning configuration has been seen, the pair phase is queued with the remembered capacity before
+# the host reads the pair count (kernels take the count from device memory). These cases run that path.
+def test_speculative_pair_phase_bit_exact(dev):
+    """The second and later binnings of a configuration (the speculative path) equal the oracle, over a
+    batch whose images have different pair counts."""
+    mu, ls, *_ = random_scene(3000, 200, 160, seed=11, dev=dev, B=3)
+    sc = activate_scale(ls)
+    for _ in range(3):
+        check_equal(mu, sc, 200, 160, 8, 3.0)
+
+
+def test_speculative_capacity_exceeded(dev):
+    """A scene with many more pairs than the remembered capacity: the speculative launch leaves an empty
+    list, the host sees the count and redoes the pair phase with buffers of the right size."""
+    H, W, n = 256, 256, 4000
+    mu, ls, *_ = random_scene(n, H, W, seed=12, dev=dev, ls_mean_px=1.0, ls_std=0.2)
+    check_equal(mu, activate_scale(ls), H, W, 8, 3.0)            # few pairs: sets the capacity
+    mu2, ls2, *_ = random_scene(n, H, W, seed=13, dev=dev, ls_mean_px=12.0, ls_std=0.2)
+    check_equal(mu2, activate_scale(ls2), H, W, 8, 3.0)          # many more pairs than the capacity
+    check_equal(mu, activate_scale(ls), H, W, 8, 3.0)            # and back
+
+
+def test_speculative_budget_and_errors(dev):
+    """After a binning has set a capacity, the pair budget still raises PairBudgetExceeded, and an empty
+    rect (negative scale) still raises, with the speculative launch already queued."""
+    s = synth.config("c0")
+    mu = s.mu.to(dev)
+    sc = activate_scale(s.log_scale.to(dev))
+    check_equal(mu, sc, s.H, s.W, 8, 3.0)
+    with pytest.raises(RH.PairBudgetExceeded):
+        RH._build_tiles(mu, sc, s.H, s.W, 8, 3.0, max_pairs=100)
+    with pytest.raises(ValueError, match="empty tile rect"):
+        RH._build_tiles(mu, -sc, s.H, s.W, 8, 3.0)
+    check_equal(mu, sc, s.H, s.W, 8, 3.0)
