@@ -56,25 +56,98 @@ __device__ __forceinline__ float fwd_pair(const float* __restrict__ r, float py,
   return oma;
 }
 
-// Forward sums of one pixel over pairs [i0, i1) of the tile's list. S_log is accumulated in log2 units as
-// log2 of the product of four (1 - a) factors at a time (each factor >= 1e-4, so the product stays a
-// normal float); the four splats' ids and records are loaded together ahead of their use.
-template <int C, bool ODDS>
-__device__ __forceinline__ void fwd_pixel(const float* __restrict__ rec, const int* __restrict__ gid, int i0, int i1,
-                                          float py, float px, float& sl, float& s_a, float* sc) {
-  int i = i0;
-  for (; i + 4 <= i1; i += 4) {
+// Opacity bound (as float bits; opacities are non-negative, and any other bit pattern compares above it) at or
+// below which op * falloff = exp2(log2(op) - m), m >= 0, stays below 0.99988 plus a few ulps, under the alpha
+// clamp 1 - 1e-4: a group of pairs whose opacities are all at or below it needs no min().
+constexpr unsigned kNoClampOpBits = 0x3f7ff823u;   // 0.99988f
+
+// Orders the LDS writes of a wave before its later reads (and reads before later writes) without a
+// workgroup barrier: the waves of a workgroup run loops of different trip counts.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// One pixel-pair of the per-tile forward: (u0, v0) are the pair's whitened offsets at the tile's first pixel
+// centre, (ly, lx) the lane's pixel centre relative to it, so u = A ly + B lx + u0 and v = Cc ly + D lx + v0.
+// t carries the running product of the group's (1 - a) factors.
+template <int C, bool ODDS, bool CLAMP>
+__device__ __forceinline__ void fwd_tile_pair(const float* __restrict__ r, float2 uv0, float ly, float lx, float& t,
+                                              float& s_a, float* sc) {
+  const float u = fmaf(r[R_A], ly, fmaf(r[R_B], lx, uv0.x));
+  const float v = fmaf(r[R_CC], ly, fmaf(r[R_D], lx, uv0.y));
+  const float fo = hw_exp2(-fmaf(u, u, fmaf(v, v, -r[R_LOP])));
+  const float a = CLAMP ? fminf(fo, kClamp) : fo;
+  float w;
+  if (ODDS) {
+    const float oma = one_minus_alpha(1.f - a, fo, fmaf(u, u, v * v), r[R_OP], 1.f - r[R_OP]);
+    w = a * hw_rcp(oma);
+    t *= oma;
+  } else {
+    w = a;
+    t = fmaf(-a, t, t);   // t (1 - a), one rounding
+  }
+  s_a += w;
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = fmaf(w, r[R_COL + c], sc[c]);
+}
+
+// Pairs [b0, b1) of one batch (their offsets at the tile origin in s_uv[0, b1 - b0)), four at a time: ids and
+// records through scalar loads, offsets by LDS broadcast, one log2 per group.
+template <int C, bool ODDS, bool CLAMP>
+__device__ __forceinline__ void fwd_batch(const float* __restrict__ rec, const int* __restrict__ gid, int b0, int b1,
+                                          const float2* s_uv, float ly, float lx, float& sl, float& s_a, float* sc) {
+  int i = b0;
+  for (; i + 4 <= b1; i += 4) {
     const float* r0 = rec + (size_t)gid[i] * kRec;
     const float* r1 = rec + (size_t)gid[i + 1] * kRec;
     const float* r2 = rec + (size_t)gid[i + 2] * kRec;
     const float* r3 = rec + (size_t)gid[i + 3] * kRec;
-    const float t0 = fwd_pair<C, ODDS>(r0, py, px, s_a, sc);
-    const float t1 = fwd_pair<C, ODDS>(r1, py, px, s_a, sc);
-    const float t2 = fwd_pair<C, ODDS>(r2, py, px, s_a, sc);
-    const float t3 = fwd_pair<C, ODDS>(r3, py, px, s_a, sc);
-    sl += hw_log2((t0 * t1) * (t2 * t3));
+    const int j = i - b0;
+    float t = 1.f;
+    fwd_tile_pair<C, ODDS, CLAMP>(r0, s_uv[j], ly, lx, t, s_a, sc);
+    fwd_tile_pair<C, ODDS, CLAMP>(r1, s_uv[j + 1], ly, lx, t, s_a, sc);
+    fwd_tile_pair<C, ODDS, CLAMP>(r2, s_uv[j + 2], ly, lx, t, s_a, sc);
+    fwd_tile_pair<C, ODDS, CLAMP>(r3, s_uv[j + 3], ly, lx, t, s_a, sc);
+    sl += hw_log2(t);
   }
-  for (; i < i1; ++i) sl += hw_log2(fwd_pair<C, ODDS>(rec + (size_t)gid[i] * kRec, py, px, s_a, sc));
+  for (; i < b1; ++i) {
+    float t = 1.f;
+    fwd_tile_pair<C, ODDS, CLAMP>(rec + (size_t)gid[i] * kRec, s_uv[i - b0], ly, lx, t, s_a, sc);
+    sl += hw_log2(t);
+  }
+}
+
+// Forward sums of one pixel over pairs [i0, i1) of the tile's list, in batches of 64 pairs. At the start of a
+// batch lane j computes the offsets (u0, v0) of pair j at the tile origin (py0, px0) into the wave's LDS row
+// s_uv, and a ballot tells whether any pair of the batch can reach the alpha clamp; the pixel loop then reads
+// the offsets by broadcast while the pairs' ids and records come through scalar loads (SGPR operands).
+// S_log is accumulated in log2 units, one log2 per group of four pairs (each (1 - a) factor is >= 1e-4, so
+// the group's product stays a normal float).
+template <int C, bool ODDS>
+__device__ __forceinline__ void fwd_tile_pixel(const float* __restrict__ rec, const int* __restrict__ gid, int i0,
+                                               int i1, float py0, float px0, float ly, float lx, float2* s_uv,
+                                               int lane, float& sl, float& s_a, float* sc) {
+  for (int b0 = i0; b0 < i1; b0 += 64) {
+    const int b1 = min(i1, b0 + 64);
+    bool clamp = false;
+    if (b0 + lane < b1) {
+      const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)gid[b0 + lane] * 4;
+      const float4 r0 = r4[0];   // gy, gx, A, B
+      const float4 r1 = r4[1];   // Cc, D, op, log2(op)
+      const float dy = py0 - r0.x, dx = px0 - r0.y;
+      s_uv[lane] = make_float2(fmaf(r0.z, dy, r0.w * dx), fmaf(r1.x, dy, r1.y * dx));
+      clamp = __float_as_uint(r1.z) > kNoClampOpBits;
+    }
+    const bool any_clamp = __ballot(clamp) != 0;
+    wave_lds_sync();
+    if (any_clamp)
+      fwd_batch<C, ODDS, true>(rec, gid, b0, b1, s_uv, ly, lx, sl, s_a, sc);
+    else
+      fwd_batch<C, ODDS, false>(rec, gid, b0, b1, s_uv, ly, lx, sl, s_a, sc);
+    wave_lds_sync();
+  }
 }
 
 template <int C>
@@ -155,14 +228,20 @@ __global__ __launch_bounds__(fwd_threads<TILE>()) void k_fwd_cull(
     float* __restrict__ asum_out, float* __restrict__ fg_out, float* __restrict__ slog, float* __restrict__ sa,
     float* __restrict__ sac) {
   constexpr int S = fwd_split<TILE>();
+  constexpr int NW = fwd_threads<TILE>() / 64;   // waves per workgroup
+  __shared__ float2 s_uv[NW][64];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
-  const int l = S > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
-  const int wv = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;   // wave-uniform
+  const int lane = (int)(threadIdx.x & 63);
+  const int l = S > 1 ? lane : (int)threadIdx.x;
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave-uniform
+  const int wv = S > 1 ? wid : 0;
   const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
   const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
   const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
   const float px = ((float)xp + 0.5f) / (float)ta.W;
+  const float py0 = ((float)(ta.ty * TILE) + 0.5f) / (float)ta.H;   // the tile's first pixel centre
+  const float px0 = ((float)(ta.tx * TILE) + 0.5f) / (float)ta.W;
   int g0 = starts[ta.t], g1 = starts[ta.t + 1];
   if (S > 1) {
     const int chunk = ((g1 - g0 + S - 1) / S + 3) & ~3;
@@ -172,7 +251,7 @@ __global__ __launch_bounds__(fwd_threads<TILE>()) void k_fwd_cull(
   float sl = 0.f, s_a = 0.f, sc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) sc[c] = 0.f;
-  fwd_pixel<C, ODDS>(rec, gid, g0, g1, py, px, sl, s_a, sc);
+  fwd_tile_pixel<C, ODDS>(rec, gid, g0, g1, py0, px0, py - py0, px - px0, s_uv[wid], lane, sl, s_a, sc);
   if (S > 1) {
     __shared__ float s_part[S > 1 ? S - 1 : 1][2 + C][64];
     if (wv > 0) {
