@@ -5,10 +5,11 @@
 //                    k_scan_sums + k_offsets beyond kFusedScanBlocks blocks
 //   k_scatter_pairs  load-balanced expansion of every splat's rect into (tile, splat) pairs, splat-major
 //                    as the reference generates them (:396-404), fused with the first radix histogram
-//   k_radix_*        stable LSD radix sort on the tile id, splat id as the value: within a tile the
-//                    splats keep ascending order, the order of the reference's stable argsort (:405-407)
-//   k_tile_starts_q  CSR starts: starts[t] = number of pairs with tile < t (:408), and the map from
-//                    sorted position to splat-major pair index the backward stores by
+//   k_radix_*        stable LSD radix sort on the tile id; the values carried are the splat id and (for
+//                    the backward) the pair's splat-major index, which the first pass takes from the pair's
+//                    position: within a tile the splats keep ascending order, the order of the reference's
+//                    stable argsort (:405-407)
+//   k_tile_starts    CSR starts: starts[t] = number of pairs with tile < t (:408)
 //
 // This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
 // operation separately (a fused mu*W - r*W changes floor() near tile edges).
@@ -332,13 +333,13 @@ __device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
 // id; an inclusive max-scan over the block then gives every pair its owner (splat ids grow with p).
 // The block's first splat comes from a cooperative search; when the block holds at most kBlock splats
 // (always at a few pairs per splat or more) their offsets and rects are loaded once, one per thread, into
-// LDS, and the pair loop reads only LDS. Writes keys[p] = tile, vals[p] = splat, pair_splat[p] = splat
-// (optional) and, with `hist` set, the block's histogram of the first radix digit.
+// LDS, and the pair loop reads only LDS. Writes keys[p] = tile, pair_splat[p] = splat and the block's
+// histogram of the first radix digit.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
                                                           int N, LevelTable L, const long long* __restrict__ info,
                                                           int cap, int dmask, int* __restrict__ keys,
-                                                          int* __restrict__ vals, int* __restrict__ pair_splat,
-                                                          int* __restrict__ hist, int nblocks) {
+                                                          int* __restrict__ pair_splat, int* __restrict__ hist,
+                                                          int nblocks) {
   __shared__ int4 s_own4[kSortKeys / 4];
   __shared__ int4 s_rect[kBlock];
   __shared__ int s_o0[kBlock];
@@ -349,8 +350,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
   const int tot = pair_count(info, cap);
   const int p_base = blockIdx.x * kSortKeys;
   if (p_base >= tot) {   // a block past the pairs of this launch: an empty histogram column
-    if (hist)
-      for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = 0;
+    for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = 0;
     return;
   }
   const int n_here = min(kSortKeys, tot - p_base);
@@ -430,11 +430,9 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
     const int kx = k - ky * rc.z;
     const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;
     keys[p] = tile;
-    vals[p] = g;
-    if (pair_splat) pair_splat[p] = g;
-    if (hist) atomicAdd(&s_hist[tile & dmask], 1);
+    pair_splat[p] = g;
+    atomicAdd(&s_hist[tile & dmask], 1);
   }
-  if (!hist) return;
   __syncthreads();
   for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
 }
@@ -478,22 +476,27 @@ __global__ __launch_bounds__(kBlock) void k_hist_row_scan(int* __restrict__ hist
   if (threadIdx.x == 0) rowtot[blockIdx.x] = carry;
 }
 
-// Stable scatter of one radix pass. Wave w of the block owns keys [base + w*1024, base + (w+1)*1024) and
+// Stable scatter of one radix pass. Wave w of the block owns keys [base + w*512, base + (w+1)*512) and
 // walks them 64 at a time in index order; lanes holding the same digit are ranked among themselves with
 // ballots (lane order = index order), on top of the wave's running count for that digit. The block's keys
 // are then placed in LDS in (digit, index) order and written out by consecutive threads, so each digit's
 // run of the block lands in consecutive global positions: the digit's global start (prefix of the row
 // totals) plus the block's offset within the digit (the row-scanned histogram).
+// Values moved with each key: the splat id (vals) and, with q_out set, the pair's splat-major index (q_in, or
+// the key's input position when q_in is null: the first pass reads the splat-major list).
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
+                                                          const int* __restrict__ q_in,
                                                           const long long* __restrict__ info, int cap, int shift,
                                                           int dbits, const int* __restrict__ hist_scan,
                                                           const int* __restrict__ rowtot, int nblocks,
-                                                          int* __restrict__ keys_out, int* __restrict__ vals_out) {
+                                                          int* __restrict__ keys_out, int* __restrict__ vals_out,
+                                                          int* __restrict__ q_out) {
   __shared__ int s_cnt[kWaves][256];
   __shared__ int s_gbase[256];    // global position of the block's first key with digit d
   __shared__ int s_lbase[256];    // LDS position of the block's first key with digit d
   __shared__ int s_key[kSortKeys];
   __shared__ int s_val[kSortKeys];
+  __shared__ int s_q[kSortKeys];
   __shared__ int s_w[kWaves];
   const int dmask = (1 << dbits) - 1;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -512,13 +515,14 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
   const int p_base = blockIdx.x * kSortKeys;
   const int n_here = min(kSortKeys, tot - p_base);
   const int p0 = p_base + wv * kWaveKeys + lane;
-  int key[kItems], val[kItems], rank[kItems];
+  int key[kItems], val[kItems], qv[kItems], rank[kItems];
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const int p = p0 + j * 64;
     const bool act = p < tot;
     key[j] = act ? keys_in[p] : 0;
     val[j] = act ? vals_in[p] : 0;
+    qv[j] = q_out ? (q_in ? (act ? q_in[p] : 0) : p) : 0;
   }
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
@@ -554,6 +558,7 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     const int lpos = s_lbase[d] + s_cnt[wv][d] + rank[j];
     s_key[lpos] = key[j];
     s_val[lpos] = val[j];
+    if (q_out) s_q[lpos] = qv[j];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < n_here; i += kBlock) {
@@ -562,18 +567,14 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     const int pos = s_gbase[d] + (i - s_lbase[d]);
     keys_out[pos] = k;
     vals_out[pos] = s_val[i];
+    if (q_out) q_out[pos] = s_q[i];
   }
 }
 
-// From the sorted (tile, splat) list: CSR starts (starts[t] = number of pairs with tile < t,
-// render_triton.py:408) and, optionally, pair_q[i] = the splat-major index of sorted pair i:
-// q = offsets[g] + (ty - ty0) * w + (tx - tx0), the pair's index in its splat's rect walk (tile coordinates
-// local to the splat's level).
-__global__ __launch_bounds__(kBlock) void k_tile_starts_q(const int* __restrict__ keys, int* __restrict__ gids,
-                                                          const long long* __restrict__ info, int cap, int nt,
-                                                          LevelTable L, const int4* __restrict__ rect,
-                                                          const int* __restrict__ offsets, int* __restrict__ starts,
-                                                          int* __restrict__ pair_q) {
+// From the sorted tile ids: CSR starts, starts[t] = number of pairs with tile < t (render_triton.py:408).
+__global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ keys, int* __restrict__ gids,
+                                                        const long long* __restrict__ info, int cap, int nt,
+                                                        int* __restrict__ starts) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
   const int tot = pair_count(info, cap);
   if (tot == 0) {   // empty list: all starts 0 and gid_sorted = {0} (render_triton.py:392-394)
@@ -587,13 +588,6 @@ __global__ __launch_bounds__(kBlock) void k_tile_starts_q(const int* __restrict_
   for (int t = prev + 1; t <= k; ++t) starts[t] = i;
   if (i == tot - 1)
     for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
-  if (pair_q) {
-    const int g = gids[i];
-    const int4 rc = rect[g];
-    const int lt = k - L.tbase[rc.w], ntx = L.ntx[rc.w];
-    const int ty = lt / ntx, tx = lt - ty * ntx;
-    pair_q[i] = offsets[g] + (ty - rc.y) * rc.z + (tx - rc.x);
-  }
 }
 
 __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
@@ -604,9 +598,11 @@ __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
 // ----------------------------------------------------------------------------------------------------
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Pair-phase workspace: two sets of (keys, splat ids, splat-major indices) that the radix passes ping-pong
+// between, the per-block digit histograms and the digit totals.
 struct PairsPlan {
   int nblk, passes, dbits, radix;
-  size_t off_keys_a, off_keys_b, off_vals_b, off_hist, off_rowtot, total;
+  size_t off_set[2][3], off_hist, off_rowtot, total;
 };
 
 static PairsPlan plan_pairs(int nt, long long tot) {
@@ -614,14 +610,13 @@ static PairsPlan plan_pairs(int nt, long long tot) {
   p.nblk = tot > 0 ? div_up(tot, kSortKeys) : 0;
   int nbits = 0;
   while (nt > 1 && (1LL << nbits) < nt) ++nbits;   // bits of the largest tile id nt - 1
-  p.passes = (nbits + 7) / 8;
-  p.dbits = p.passes ? (nbits + p.passes - 1) / p.passes : 0;
+  p.passes = nbits > 8 ? (nbits + 7) / 8 : 1;      // at least one pass: it also moves the values into place
+  p.dbits = nbits > 0 ? (nbits + p.passes - 1) / p.passes : 1;
   p.radix = 1 << p.dbits;
   const long long nh = (long long)p.radix * p.nblk;
   size_t o = 0;
-  p.off_keys_a = o; o += align256(sizeof(int) * (size_t)tot);
-  p.off_keys_b = o; o += align256(sizeof(int) * (size_t)tot);
-  p.off_vals_b = o; o += align256(sizeof(int) * (size_t)tot);
+  for (int s = 0; s < 2; ++s)
+    for (int k = 0; k < 3; ++k) { p.off_set[s][k] = o; o += align256(sizeof(int) * (size_t)tot); }
   p.off_hist = o;   o += align256(sizeof(int) * (size_t)(nh > 0 ? nh : 1));
   p.off_rowtot = o; o += align256(sizeof(int) * 256);
   p.total = o;
@@ -712,38 +707,46 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
     return check_launch("splat_bin_pairs(empty)");
   }
   char* base = (char*)ws;
-  int* keys_a = (int*)(base + pl.off_keys_a);
-  int* keys_b = (int*)(base + pl.off_keys_b);
-  int* vals_b = (int*)(base + pl.off_vals_b);
+  int* S[2][3];   // workspace sets: keys, splat ids, splat-major indices
+  for (int s = 0; s < 2; ++s)
+    for (int k = 0; k < 3; ++k) S[s][k] = (int*)(base + pl.off_set[s][k]);
   int* hist = (int*)(base + pl.off_hist);
   int* rowtot = (int*)(base + pl.off_rowtot);
-  // Pass k reads buffer k % 2 and writes (k + 1) % 2, so the final pass lands in buffer `fin`; with no
-  // pass the scatter's own output (buffer 0 = fin) is final.
-  const int fin = pl.passes & 1;
-  int* K[2];
-  int* V[2];
-  K[fin] = keys_a; K[1 - fin] = keys_b;
-  V[fin] = gid_sorted; V[1 - fin] = vals_b;
+  // The scatter writes the splat-major keys and splat ids into set 1 (the splat ids into the caller's
+  // pair_splat when given). Pass k < passes - 1 writes set k % 2 and the next pass reads it; the last pass
+  // writes its keys into the set it does not read and the values into gid_sorted / pair_q.
+  const bool maps = pair_q != nullptr;
+  int* psplat = pair_splat ? pair_splat : S[1][1];
   const int dmask = pl.radix - 1;
-  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, dmask, K[0],
-                                              V[0], pair_splat, pl.passes ? hist : nullptr, pl.nblk);
+  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, dmask,
+                                              S[1][0], psplat, hist, pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
+  const int* kin = S[1][0];
+  const int* vin = psplat;
+  const int* qin = nullptr;
+  int* kfin = nullptr;
   for (int pass = 0; pass < pl.passes; ++pass) {
     const int shift = pass * pl.dbits;
-    const int src = pass & 1, dst = 1 - src;
-    if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(K[src], dinfo, t, shift, dmask, hist, pl.nblk);
+    const bool last = pass == pl.passes - 1;
+    int* const* D = S[pass & 1];
+    int* kout = D[0];
+    int* vout = last ? gid_sorted : D[1];
+    int* qout = maps ? (last ? pair_q : D[2]) : nullptr;
+    if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(kin, dinfo, t, shift, dmask, hist, pl.nblk);
     k_hist_row_scan<<<pl.radix, kBlock, 0, st>>>(hist, pl.nblk, rowtot);
-    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(K[src], V[src], dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk,
-                                                K[dst], V[dst]);
+    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(kin, vin, qin, dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk, kout,
+                                                vout, qout);
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
+    kin = kout;
+    vin = vout;
+    qin = qout;
+    kfin = kout;
   }
   const int nthr = t > nt + 1 ? t : nt + 1;
-  k_tile_starts_q<<<div_up(nthr, kBlock), kBlock, 0, st>>>(K[fin], gid_sorted, dinfo, t, nt, L,
-                                                           reinterpret_cast<const int4*>(rect), offsets, tile_starts,
-                                                           pair_q);
-  return check_launch("k_tile_starts_q");
+  k_tile_starts<<<div_up(nthr, kBlock), kBlock, 0, st>>>(kfin, gid_sorted, dinfo, t, nt, tile_starts);
+  return check_launch("k_tile_starts");
 }
 
 // One event per thread and device, recorded after the read-back of the pair count (splat_bin).
