@@ -736,149 +736,87 @@ __device__ __forceinline__ void zero_grads(int g, float* __restrict__ g_mu, floa
   for (int c = 0; c < C; ++c) g_col[(size_t)g * C + c] = 0.f;
 }
 
-// DPP moves (VALU, no LDS): lane i reads lane i - n of its row of 16 (row_shr:n), or lane 15 / 31 of the
-// wave for rows 1, 3 / 2, 3 (row_bcast:15 / :31). Lanes without a source get `old`.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ int dpp_i(int old, int x) {
-  return __builtin_amdgcn_update_dpp(old, x, CTRL, ROWS, 0xf, false);
-}
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xf, false));
-}
+// Per-splat reduction of the per-pair records (contiguous, splat-major: splat g owns q in
+// [offsets[g], offsets[g+1])) into parameter gradients, in one launch. kSumLanes consecutive lanes share a
+// splat: lane r of the group sums records r, r + kSumLanes, ... in order (kSumUnroll loads in flight), and
+// the group's partial sums are combined by a fixed xor tree. A splat with more than kLightPairs pairs is
+// left out of that loop and summed afterwards by its whole wave (lane-strided partial sums, then a fixed
+// xor tree), so one heavy splat does not serialise its wave. The order of every addition is fixed:
+// deterministic. Splats with no pair (none for valid rects) get zeros. With g_bg set, the grid's first
+// workgroup sums the per-tile background partials instead.
+constexpr int kSumLanes = 4;
+constexpr int kLightPairs = 64;
+constexpr int kSumUnroll = 8;
 
-// One step of a segmented inclusive prefix scan over the wave: add the source lane's sums when it holds
-// the same (sorted) key.
-template <int CTRL, int ROWS, int R>
-__device__ __forceinline__ void seg_scan_step(int key, float* v) {
-  const bool take = dpp_i<CTRL, ROWS>(-2, key) == key;
+// s += records q, q + step, ... below qe, in that order. The records of kSumUnroll steps are loaded before
+// any is added (clamped to the last valid one), so each lane keeps kSumUnroll loads in flight.
+template <int R>
+__device__ __forceinline__ void sum_pair_recs(float* s, const float* __restrict__ psum, int q, int qe, int step) {
+  for (; q < qe; q += kSumUnroll * step) {
+    float a[kSumUnroll][R];
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const float o = dpp_f<CTRL, ROWS>(v[k]);
-    v[k] += take ? o : 0.f;
+    for (int u = 0; u < kSumUnroll; ++u) {
+      const float* r = psum + (size_t)min(q + u * step, qe - 1) * R;
+#pragma unroll
+      for (int k = 0; k < R; ++k) a[u][k] = r[k];
+    }
+#pragma unroll
+    for (int u = 0; u < kSumUnroll; ++u)
+      if (q + u * step < qe) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) s[k] += a[u][k];
+      }
   }
 }
 
-// Segmented inclusive prefix scan (keys non-decreasing along the lanes): each lane ends with the sum of its
-// segment's values up to itself; a segment's total is in its last lane.
-template <int R>
-__device__ __forceinline__ void seg_prefix_scan(int key, float* v) {
-  seg_scan_step<0x111, 0xf, R>(key, v);   // row_shr:1
-  seg_scan_step<0x112, 0xf, R>(key, v);   // row_shr:2
-  seg_scan_step<0x114, 0xf, R>(key, v);   // row_shr:4
-  seg_scan_step<0x118, 0xf, R>(key, v);   // row_shr:8
-  seg_scan_step<0x142, 0xa, R>(key, v);   // row_bcast:15
-  seg_scan_step<0x143, 0xc, R>(key, v);   // row_bcast:31
-}
-
-// Per-splat reduction of the per-pair records (contiguous, splat-major: splat g owns q in
-// [offsets[g], offsets[g+1])) into parameter gradients, in one launch. A wave covers kRedSub sub-chunks of 64
-// consecutive pairs (lane = pair), all loaded up front. In each sub-chunk a segmented prefix scan (DPP, no
-// LDS) leaves every segment's in-chunk total in its last lane; a segment still open at a sub-chunk's end
-// carries its sum (wave-uniform) into the next. The wave that holds a splat's first pair owns the splat: the
-// one owned segment that runs past the wave's end is completed by the whole wave reading the rest of its
-// records (load-balanced for splats of thousands of pairs); pairs of a splat that started in an earlier wave
-// are left to that wave. Splats with no pair (none for valid rects) get zeros.
-// With g_bg set, the grid's first workgroup sums the per-tile background partials instead.
-constexpr int kRedSub = 4;
-constexpr int kRedPairs = 64 * kRedSub;
-
 template <int C>
-__global__ __launch_bounds__(256) void k_splat_reduce(const float* __restrict__ rec, const float* __restrict__ psum,
-                                                      const int* __restrict__ pair_splat,
-                                                      const int* __restrict__ offsets, int tot, int N, int nwaves,
-                                                      float* __restrict__ g_mu, float* __restrict__ g_scale,
-                                                      float* __restrict__ g_theta, float* __restrict__ g_op,
-                                                      float* __restrict__ g_col, const float* __restrict__ bg_part,
-                                                      int nparts, float* __restrict__ g_bg) {
+__global__ __launch_bounds__(256) void k_splat_sum(const float* __restrict__ rec, const float* __restrict__ psum,
+                                                   const int* __restrict__ offsets, int N, float* __restrict__ g_mu,
+                                                   float* __restrict__ g_scale, float* __restrict__ g_theta,
+                                                   float* __restrict__ g_op, float* __restrict__ g_col,
+                                                   const float* __restrict__ bg_part, int nparts,
+                                                   float* __restrict__ g_bg) {
   constexpr int R = pair_rec<C>();
-  if (g_bg && blockIdx.x == 0) {   // first, so it overlaps the pair waves
+  constexpr int kPerBlock = 256 / kSumLanes;
+  if (g_bg && blockIdx.x == 0) {   // first, so it overlaps the splat waves
     block_bg_sum<C>(bg_part, nparts, g_bg);
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int w = (blockIdx.x - (g_bg ? 1 : 0)) * 4 + (threadIdx.x >> 6);
-  if (w >= nwaves) return;
-  const int q0 = w * kRedPairs;
-  const int qend = min(q0 + kRedPairs, tot);
-  int g[kRedSub];
-  float v[kRedSub][kSums];
-#pragma unroll
-  for (int s = 0; s < kRedSub; ++s) {
-    const int q = q0 + 64 * s + lane;
-    const bool act = q < qend;
-    g[s] = act ? pair_splat[q] : -1;
-    const float* src = psum + (size_t)(act ? q : 0) * R;
-#pragma unroll
-    for (int k = 0; k < kSums; ++k) v[s][k] = (act && k < R) ? src[k] : 0.f;
+  const int r = lane % kSumLanes;
+  const int g = (blockIdx.x - (g_bg ? 1 : 0)) * kPerBlock + (int)threadIdx.x / kSumLanes;
+  int q0 = 0, q1 = 0;
+  if (g < N) {
+    q0 = offsets[g];
+    q1 = offsets[g + 1];
   }
-  const int gbefore = q0 > 0 ? pair_splat[q0 - 1] : -1;
-  const int glast = pair_splat[qend - 1];
-  const int qe_last = offsets[glast + 1];
-  // splats with no pairs between the previous wave's last pair and this wave's first
-  if (lane == 0)
-    for (int gz = gbefore + 1; gz < g[0]; ++gz) zero_grads<C>(gz, g_mu, g_scale, g_theta, g_op, g_col);
-  bool fin[kRedSub], ends[kRedSub];
-  int gnx[kRedSub];
-  float carry[kSums];
+  const bool heavy = q1 - q0 > kLightPairs;
+  float s[R];
 #pragma unroll
-  for (int k = 0; k < kSums; ++k) carry[k] = 0.f;
-  bool c_own = false;   // the segment entering the current sub-chunk started in this wave
-  int gin = gbefore;    // splat of the pair just before the current sub-chunk
+  for (int k = 0; k < R; ++k) s[k] = 0.f;
+  if (!heavy) sum_pair_recs<R>(s, psum, q0 + r, q1, kSumLanes);
 #pragma unroll
-  for (int s = 0; s < kRedSub; ++s) {
-    const int key = g[s];
-    seg_prefix_scan<R>(key, v[s]);
-    const bool entering = key >= 0 && key == gin;   // a prefix of the lanes
-    if (entering && c_own) {
+  for (int d = 1; d < kSumLanes; d <<= 1)
 #pragma unroll
-      for (int k = 0; k < R; ++k) v[s][k] += carry[k];
-    }
-    const bool own = key >= 0 && (!entering || c_own);
-    const int after = s + 1 < kRedSub ? __shfl(g[s + 1], 0, 64) : (qe_last > qend ? glast : -1);
-    int knext = __shfl_down(key, 1, 64);
-    if (lane == 63) knext = after;
-    gnx[s] = knext;
-    ends[s] = key >= 0 && knext != key;   // the segment's last pair in the wave
-    fin[s] = own && ends[s];
-    const int k63 = __shfl(key, 63, 64);
-    const bool open = k63 >= 0 && after == k63;
-    if (open) {
+    for (int k = 0; k < R; ++k) s[k] += __shfl_xor(s[k], d, 64);
+  for (unsigned long long hm = __ballot(heavy && r == 0); hm; hm &= hm - 1) {
+    const int j = __builtin_ctzll(hm);
+    const int h0 = __builtin_amdgcn_readlane(q0, j), h1 = __builtin_amdgcn_readlane(q1, j);
+    float t[R];
 #pragma unroll
-      for (int k = 0; k < R; ++k) carry[k] = __shfl(v[s][k], 63, 64);
-      c_own = __shfl(own ? 1 : 0, 63, 64) != 0;
-    } else {
-      c_own = false;
-    }
-    gin = k63 >= 0 ? k63 : gin;
-  }
-  // the owned segment running past the wave: the whole wave sums its remaining records
-  if (c_own && qe_last > qend) {
-    float t[kSums];
-#pragma unroll
-    for (int k = 0; k < kSums; ++k) t[k] = 0.f;
-    for (int j = qend + lane; j < qe_last; j += 64) {
-      const float* r = psum + (size_t)j * R;
-#pragma unroll
-      for (int k = 0; k < R; ++k) t[k] += r[k];
-    }
+    for (int k = 0; k < R; ++k) t[k] = 0.f;
+    sum_pair_recs<R>(t, psum, h0 + lane, h1, 64);
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-      float x = t[k];
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-      carry[k] += x;
+      const float x = wave_sum(t[k]);
+      if (lane == j) s[k] = x;
     }
-    if (lane == 0) splat_grads<C>(glast, rec, carry, g_mu, g_scale, g_theta, g_op, g_col);
   }
-#pragma unroll
-  for (int s = 0; s < kRedSub; ++s) {
-    if (fin[s]) splat_grads<C>(g[s], rec, v[s], g_mu, g_scale, g_theta, g_op, g_col);
-    if (ends[s])
-      for (int gz = g[s] + 1; gz < gnx[s]; ++gz) zero_grads<C>(gz, g_mu, g_scale, g_theta, g_op, g_col);
-  }
-  if (qend == tot && lane == 0)
-    for (int gz = glast + 1; gz < N; ++gz) zero_grads<C>(gz, g_mu, g_scale, g_theta, g_op, g_col);
+  if (g >= N || r != 0) return;
+  if (q1 > q0)
+    splat_grads<C>(g, rec, s, g_mu, g_scale, g_theta, g_op, g_col);
+  else
+    zero_grads<C>(g, g_mu, g_scale, g_theta, g_op, g_col);
 }
 
 // Zero gradients for every splat (a render with no pairs), plus g_bg from the partials in the first block.
@@ -1265,18 +1203,15 @@ int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_spl
   if (N < 0 || tot < 0 || tot > 0x7fffffffLL - 64 || (N == 0 && tot > 0))
     return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
   if ((N > 0 && (!rec || !offsets || !g_mu || !g_scale || !g_op || !g_color)) ||
-      (tot > 0 && (!pair_splat || !pair_sums)) || (g_bg && (!bg_part || nparts < 1)))
+      (tot > 0 && !pair_sums) || (g_bg && (!bg_part || nparts < 1)))
     return set_error(kInvalid, "splat_reduce_pairs: null pointer");
   hipStream_t st = (hipStream_t)stream;
-  const int nwaves = (int)((tot + kRedPairs - 1) / kRedPairs);
-  const int t = (int)tot;
   const unsigned extra = g_bg ? 1u : 0u;
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
-    if (t > 0)
-      k_splat_reduce<CC><<<(unsigned)((nwaves + 3) / 4) + extra, 256, 0, st>>>(
-          rec, pair_sums, pair_splat, offsets, t, N, nwaves, g_mu, g_scale, g_theta, g_op, g_color, bg_part, nparts,
-          g_bg);
+    if (tot > 0)
+      k_splat_sum<CC><<<(unsigned)((N + 256 / kSumLanes - 1) / (256 / kSumLanes)) + extra, 256, 0, st>>>(
+          rec, pair_sums, offsets, N, g_mu, g_scale, g_theta, g_op, g_color, bg_part, nparts, g_bg);
     else if (N > 0 || g_bg)
       k_zero_grads<CC><<<(unsigned)((N + 255) / 256) + extra, 256, 0, st>>>(N, g_mu, g_scale, g_theta, g_op,
                                                                             g_color, bg_part, nparts, g_bg);
