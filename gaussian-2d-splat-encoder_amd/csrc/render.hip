@@ -69,6 +69,16 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Whitened offsets (u, v) of the pixel centre (py0, px0) from a splat with centre (gy, gx) and rotation rows
+// (A, B), (Cc, D), evaluated in float64 and rounded once. A tile's pixels add their own offsets from the tile's
+// first pixel centre to these, so their rounding error is shared by the whole tile; with one rounding it stays
+// at half an ulp of the result, below the rounding the per-pixel form makes at every pixel.
+__device__ __forceinline__ float2 offsets_at(float py0, float px0, float gy, float gx, float A, float B, float Cc,
+                                             float D) {
+  const double dy = (double)py0 - (double)gy, dx = (double)px0 - (double)gx;
+  return make_float2((float)fma((double)A, dy, (double)B * dx), (float)fma((double)Cc, dy, (double)D * dx));
+}
+
 // One pixel-pair of the per-tile forward: (u0, v0) are the pair's whitened offsets at the tile's first pixel
 // centre, (ly, lx) the lane's pixel centre relative to it, so u = A ly + B lx + u0 and v = Cc ly + D lx + v0.
 // t carries the running product of the group's (1 - a) factors.
@@ -136,8 +146,7 @@ __device__ __forceinline__ void fwd_tile_pixel(const float* __restrict__ rec, co
       const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)gid[b0 + lane] * 4;
       const float4 r0 = r4[0];   // gy, gx, A, B
       const float4 r1 = r4[1];   // Cc, D, op, log2(op)
-      const float dy = py0 - r0.x, dx = px0 - r0.y;
-      s_uv[lane] = make_float2(fmaf(r0.z, dy, r0.w * dx), fmaf(r1.x, dy, r1.y * dx));
+      s_uv[lane] = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
       clamp = __float_as_uint(r1.z) > kNoClampOpBits;
     }
     const bool any_clamp = __ballot(clamp) != 0;
@@ -515,42 +524,79 @@ __device__ __forceinline__ bool near_possible(float op, float lop, float gy, flo
   return op > kNearOpaqueBwd && d2 < smax * smax * (lop - kLog2NearOpaqueBwd + kNearMargin);
 }
 
-// Per-pair sums over the TILE x TILE pixels of a tile (lane = pair), with 1 - a = 1 - op f by one fma:
+__device__ __forceinline__ float uniform_f(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
+// Geometry of one pair in the backward's lane-per-pair loops: the whitened offsets (u0, v0) of the tile's first
+// pixel centre and the rotation rows (A, B) and (Cc, D), so that at the pixel (yy, xx) of the tile
+// u = A ly[yy] + B lx[xx] + u0 and v = Cc ly[yy] + D lx[xx] + v0, where ly[yy] and lx[xx] are the pixel centre's
+// offsets from the tile's first pixel centre (differences of the float centres, exact).
+struct PairGeo {
+  float u0, v0, A, B, Cc, D;
+};
+
+__device__ __forceinline__ PairGeo pair_geo(const float4& r0, const float4& r1, float py0, float px0) {
+  const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
+  return {uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
+}
+
+// A lane whose pair was taken out: u = 1e30 at every pixel, so u^2 overflows, the falloff is 0, 1 - a = 1 and
+// every sum of the lane stays 0.
+__device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
+  if (mute) {
+    g.u0 = 1e30f;
+    g.A = g.B = g.Cc = g.D = 0.f;
+  }
+}
+
+// Row stride (float4) of the per-pixel upstream terms in LDS: one padding slot per row, so the rows that
+// different lanes read at once (row-split remainder chunks) start on different banks.
+template <int TILE>
+__host__ __device__ constexpr int up_stride() { return TILE + 1; }
+
+// Per-pair sums over rows [row0, row0 + nrows) of the tile (lane = pair), with 1 - a = 1 - op f by one fma:
 // the caller has taken every pair that may be near-opaque in the tile (near_possible) out of the wave's
-// lanes. Straight-line, every pixel of a row unrolled; the row's first pixel index is copied into a VGPR
-// once per row, so the row's LDS reads take constant offsets from it.
+// lanes. The row terms A ly and Cc ly are taken once per row; per pixel, u and v are one fma each with the
+// column offsets lxs[] (wave-uniform, SGPR operands); the row's upstream terms come from LDS.
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ void pair_tile(float gy, float gx, float A, float B, float Cc, float D, float op,
-                                          const float4& col, const float* s_py, const float* s_px, const float4* s_pa,
-                                          const float4* s_pb, PairSums<C>& s) {
-  constexpr int kUnrollX = TILE < 8 ? TILE : 8;
+__device__ __forceinline__ void pair_rows(const PairGeo& g, float op, const float4& col, int row0, int nrows,
+                                          const float* s_ly, const float* lxs, const float4* s_pa, const float4* s_pb,
+                                          PairSums<C>& s) {
 #pragma nounroll
-  for (int yy = 0; yy < TILE; ++yy) {
-    const float dy = s_py[yy] - gy;
-    const float uy = A * dy, vy = Cc * dy;
-    int row;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(row) : "s"(yy * TILE));
-    const float4* pa_row = s_pa + row;
-    const float4* pb_row = s_pb + row;
-#pragma unroll kUnrollX
+  for (int yy = row0; yy < row0 + nrows; ++yy) {
+    const float ly = s_ly[yy];
+    const float uy = fmaf(g.A, ly, g.u0), vy = fmaf(g.Cc, ly, g.v0);
+    const float4* pa_row = s_pa + yy * up_stride<TILE>();
+    const float4* pb_row = s_pb + yy * up_stride<TILE>();
+#pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
       const float4 pa = pa_row[xx];
       const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float dx = s_px[xx] - gx;
-      const float u = fmaf(B, dx, uy), v = fmaf(D, dx, vy);
+      const float u = fmaf(g.B, lxs[xx], uy), v = fmaf(g.D, lxs[xx], vy);
       const float f = hw_exp2(-fmaf(u, u, v * v));
       bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, pa, pb, s);
     }
   }
 }
 
-// A lane whose pair was taken out: geometry for which u = 1e30 * (py + 16) is finite and u^2 overflows, so
-// the falloff is 0 at every pixel, 1 - a = 1 and every sum of the lane stays 0.
-__device__ __forceinline__ void mute_pair(bool mute, float& gy, float& A, float& B, float& Cc, float& D) {
-  if (mute) {
-    gy = -16.f;
-    A = 1e30f;
-    B = Cc = D = 0.f;
+// Per-pair sums over the pixels [j0, j0 + npx) of one row of the tile (lane = pair, lane-varying j0): the
+// remainder chunks that give a pair fewer pixels than a row.
+template <int C, bool ODDS, int TILE>
+__device__ __forceinline__ void pair_row_part(const PairGeo& g, float op, const float4& col, int j0, int npx,
+                                              const float* s_ly, const float* s_lx, const float4* s_pa,
+                                              const float4* s_pb, PairSums<C>& s) {
+  const int yy = j0 / TILE;
+  const float ly = s_ly[yy];
+  const float uy = fmaf(g.A, ly, g.u0), vy = fmaf(g.Cc, ly, g.v0);
+  for (int l = j0; l < j0 + npx; ++l) {
+    const int xx = l - yy * TILE;
+    const float lx = s_lx[xx];
+    const int k = yy * up_stride<TILE>() + xx;
+    const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float u = fmaf(g.B, lx, uy), v = fmaf(g.D, lx, vy);
+    const float f = hw_exp2(-fmaf(u, u, v * v));
+    bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, s_pa[k], pb, s);
   }
 }
 
@@ -558,20 +604,23 @@ __device__ __forceinline__ void mute_pair(bool mute, float& gy, float& A, float&
 // every pixel (bwd_px_near), reduced over the wave: every lane returns the totals. For the pairs taken out
 // of the lane-per-pair loops (a few near-opaque splats around their centre tile).
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, const float* s_py,
-                                                    const float* s_px, const float4* s_pa, const float4* s_pb,
-                                                    int lane, float& op) {
+__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, float py0, float px0,
+                                                    const float* s_ly, const float* s_lx, const float4* s_pa,
+                                                    const float4* s_pb, int lane, float& op) {
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
   const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
+  const PairGeo pg = pair_geo(r0, r1, py0, px0);
   const PairOp po = pair_op(r1.z);
   op = r1.z;
   PairSums<C> s;
   for (int l = lane; l < TILE * TILE; l += 64) {
-    const float dy = s_py[l / TILE] - r0.x, dx = s_px[l % TILE] - r0.y;
-    const float u = fmaf(r0.z, dy, r0.w * dx), v = fmaf(r1.x, dy, r1.y * dx);
+    const int yy = l / TILE, xx = l % TILE;
+    const float ly = s_ly[yy], lx = s_lx[xx];
+    const float u = fmaf(pg.A, ly, fmaf(pg.B, lx, pg.u0)), v = fmaf(pg.Cc, ly, fmaf(pg.D, lx, pg.v0));
     const float m = fmaf(u, u, v * v);
-    const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-    bwd_px_near<C, ODDS>(u, v, m, hw_exp2(-m), po, col, s_pa[l], pb, s);
+    const int k = yy * up_stride<TILE>() + xx;
+    const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    bwd_px_near<C, ODDS>(u, v, m, hw_exp2(-m), po, col, s_pa[k], pb, s);
   }
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) xor_reduce<C>(s, d);
@@ -582,8 +631,10 @@ __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ re
 // Composite (level 0): upstream from T/asum/fg/gout (see pixel_upstream for UPS); per-tile partials of
 // sum_p gout * T go to bg_part[c * ntiles + (t - tb0)]. FIELDS: upstream from the packed fields.
 // One wave per tile: the per-pixel upstream terms are staged in LDS, then the wave takes the tile's pairs
-// 64 at a time (lane = pair). At 6 waves per SIMD (at most 80 VGPRs) there are enough waves to cover the
-// latency of the VALU, LDS and transcendental pipes.
+// 64 at a time (lane = pair). The last r < 64 pairs get L lanes each (the largest power of two with
+// r L <= 64), each lane covering a 1/L share of the tile's pixels (whole rows when that share is at least a
+// row) and the L partial sums are combined with xor shuffles. At 6 waves per SIMD (at most 80 VGPRs) there
+// are enough waves to cover the latency of the VALU, LDS and transcendental pipes.
 template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
@@ -592,9 +643,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
     float* __restrict__ dsa, float* __restrict__ dsac, const int* __restrict__ pair_q, float* __restrict__ psum,
     float* __restrict__ bg_part) {
   constexpr int NP = TILE * TILE;
-  __shared__ float4 s_pa[NP];
-  __shared__ float4 s_pb[NP];
-  __shared__ float s_py[TILE], s_px[TILE];
+  constexpr int RS = up_stride<TILE>();
+  __shared__ float4 s_pa[TILE * RS];
+  __shared__ float4 s_pb[TILE * RS];
+  __shared__ float s_ly[TILE], s_lx[TILE];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
   const int t = ta.t;
@@ -608,12 +660,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
       pixel_upstream<C, FIELDS, UPS>(p, (size_t)L.pbase[ta.l] + p, bg, Tin, asum_in, fg_in, gout, dslog, dsa, dsac,
                                      pa, pb, bgp);
     }
-    s_pa[l] = pa;
-    s_pb[l] = pb;
-  }
-  if (lane < TILE) {
-    s_py[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / (float)ta.H;
-    s_px[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / (float)ta.W;
+    const int k = (l / TILE) * RS + l % TILE;
+    s_pa[k] = pa;
+    s_pb[k] = pb;
   }
   if (!FIELDS && bg_part) {
 #pragma unroll
@@ -622,72 +671,77 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
       if (lane == 0) bg_part[(size_t)c * ntiles + (t - tb0)] = v;
     }
   }
+  // the tile's first and last pixel centres (render_triton.py:455-456) and the per-row / per-column offsets
+  const float fH = (float)ta.H, fW = (float)ta.W;
+  const float py0 = uniform_f(((float)(ta.ty * TILE) + 0.5f) / fH);
+  const float px0 = uniform_f(((float)(ta.tx * TILE) + 0.5f) / fW);
+  const float py1 = uniform_f(((float)(ta.ty * TILE + TILE - 1) + 0.5f) / fH);
+  const float px1 = uniform_f(((float)(ta.tx * TILE + TILE - 1) + 0.5f) / fW);
+  if (lane < TILE) {
+    s_ly[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / fH - py0;
+    s_lx[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW - px0;
+  }
   __syncthreads();
+  float lxs[TILE];
+#pragma unroll
+  for (int xx = 0; xx < TILE; ++xx) lxs[xx] = uniform_f(s_lx[xx]);
   const int g0 = starts[t], g1 = starts[t + 1];
   const int n = g1 - g0;
   const int nfull = n >> 6;
-  // full chunks: lane = pair, every pixel of the tile, row / column terms factored out of u and v
+  // full chunks: lane = pair, every pixel of the tile
   for (int k = 0; k < nfull; ++k) {
     const int i = g0 + 64 * k + lane;
     const int g = gid[i];
     const int q = pair_q[i];
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y;
     const float op = r1.z;
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    const bool near = near_possible(op, r1.w, gy, gx, fmaxf(sc.x, sc.y), s_py[0], s_py[TILE - 1], s_px[0],
-                                    s_px[TILE - 1]);
-    float mgy = gy, mA = A, mB = B, mCc = Cc, mD = D;
-    mute_pair(near, mgy, mA, mB, mCc, mD);
+    const bool near = near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
+    PairGeo pg = pair_geo(r0, r1, py0, px0);
+    mute_pair(near, pg);
     PairSums<C> s;
-    pair_tile<C, ODDS, TILE>(mgy, gx, mA, mB, mCc, mD, op, col, s_py, s_px, s_pa, s_pb, s);
+    pair_rows<C, ODDS, TILE>(pg, op, col, 0, TILE, s_ly, lxs, s_pa, s_pb, s);
     if (!near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
     for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
       const int j = __builtin_ctzll(nm);
       float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_py, s_px, s_pa,
-                                                          s_pb, lane, opj);
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
+                                                          s_pa, s_pb, lane, opj);
       if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
     }
   }
-  // remainder of r < 64 pairs: L lanes per pair (largest power of two with r * L <= 64, L <= pixels),
-  // each lane covering NP / L consecutive pixels; the L partial sums are combined with xor shuffles.
+  // remainder of r < 64 pairs: L lanes per pair, each lane covering NP / L consecutive pixels; the L partial
+  // sums are combined with xor shuffles.
   const int r = n & 63;
   if (r) {
-    int L = 1;
-    while (r * L * 2 <= 64 && L * 2 <= NP) L <<= 1;
-    const int pr = lane / L, sub = lane % L;
+    int Lp = 1;
+    while (r * Lp * 2 <= 64 && Lp * 2 <= NP) Lp <<= 1;
+    const int pr = lane / Lp, sub = lane % Lp;
     const bool act = pr < r;
     const int i = g1 - r + pr;
     const int g = act ? gid[i] : 0;
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float gy = r0.x, gx = r0.y, A = r0.z, B = r0.w, Cc = r1.x, D = r1.y;
     const float op = r1.z;
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    const int npx = NP / L, j0 = sub * npx;
-    const bool near = act && near_possible(op, r1.w, gy, gx, fmaxf(sc.x, sc.y), s_py[0], s_py[TILE - 1], s_px[0],
-                                           s_px[TILE - 1]);
-    float mgy = gy, mA = A, mB = B, mCc = Cc, mD = D;
-    mute_pair(near, mgy, mA, mB, mCc, mD);
+    const bool near = act && near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
+    PairGeo pg = pair_geo(r0, r1, py0, px0);
+    mute_pair(near || !act, pg);
     PairSums<C> s;
-    for (int jj = 0; jj < npx; ++jj) {
-      const int l = j0 + jj;
-      const float dy = s_py[l / TILE] - mgy, dx = s_px[l % TILE] - gx;
-      const float4 pb = C > 2 ? s_pb[l] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float u = fmaf(mA, dy, mB * dx), v = fmaf(mCc, dy, mD * dx);
-      const float f = hw_exp2(-fmaf(u, u, v * v));
-      bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, s_pa[l], pb, s);
-    }
-    for (int d = 1; d < L; d <<= 1) xor_reduce<C>(s, d);
+    const int npx = NP / Lp;
+    if (npx >= TILE)   // whole rows (uniform branch)
+      pair_rows<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_ly, lxs, s_pa, s_pb, s);
+    else
+      pair_row_part<C, ODDS, TILE>(pg, op, col, sub * npx, npx, s_ly, s_lx, s_pa, s_pb, s);
+    for (int d = 1; d < Lp; d <<= 1) xor_reduce<C>(s, d);
     const int q = act ? pair_q[i] : 0;
     if (act && sub == 0 && !near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
     for (unsigned long long nm = __ballot(near && sub == 0); nm; nm &= nm - 1) {
       const int j = __builtin_ctzll(nm);
       float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_py, s_px, s_pa,
-                                                          s_pb, lane, opj);
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
+                                                          s_pa, s_pb, lane, opj);
       if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
     }
   }
