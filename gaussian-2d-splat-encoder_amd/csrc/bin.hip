@@ -260,6 +260,15 @@ __device__ __forceinline__ int pair_count(const long long* __restrict__ info, in
   return (t > cap || (info[1] & 3)) ? 0 : (int)t;
 }
 
+// Quotient of k >= 0 by w >= 1: a float estimate (within one of the quotient while k < 2^24), corrected to
+// the exact integer quotient.
+__device__ __forceinline__ int div_rect(int k, int w) {
+  int q = (int)((float)k * __builtin_amdgcn_rcpf((float)w));
+  while (q > 0 && q * w > k) --q;
+  while ((q + 1) * w <= k) ++q;
+  return q;
+}
+
 // ----------------------------------------------------------------------------------------------------
 // pair expansion (render_triton.py:396-404): pair p belongs to the last splat g with offsets[g] <= p, and
 // k = p - offsets[g] walks that splat's rect row by row.
@@ -426,7 +435,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
       k = p - offsets[g];
       rc = rect[g];
     }
-    const int ky = k / rc.z;
+    const int ky = div_rect(k, rc.z);
     const int kx = k - ky * rc.z;
     const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;
     keys[p] = tile;
@@ -445,10 +454,15 @@ __global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ k
   for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
   __syncthreads();
   const int p_base = blockIdx.x * kSortKeys;
+  int kv[kItems];
+#pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const int p = p_base + j * kBlock + threadIdx.x;
-    if (p < tot) atomicAdd(&s_hist[(keys[p] >> shift) & dmask], 1);
+    kv[j] = p < tot ? keys[p] : -1;
   }
+#pragma unroll
+  for (int j = 0; j < kItems; ++j)
+    if (kv[j] >= 0) atomicAdd(&s_hist[(kv[j] >> shift) & dmask], 1);
   __syncthreads();
   for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
 }
@@ -572,22 +586,25 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
 }
 
 // From the sorted tile ids: CSR starts, starts[t] = number of pairs with tile < t (render_triton.py:408).
+// Thread = tile: a lower-bound binary search over the sorted keys, so runs of empty tiles cost nothing extra
+// (threads of neighbouring tiles walk the same first probes, which stay in cache).
 __global__ __launch_bounds__(kBlock) void k_tile_starts(const int* __restrict__ keys, int* __restrict__ gids,
                                                         const long long* __restrict__ info, int cap, int nt,
                                                         int* __restrict__ starts) {
-  const int i = blockIdx.x * kBlock + threadIdx.x;
+  const int t = blockIdx.x * kBlock + threadIdx.x;
+  if (t > nt) return;
   const int tot = pair_count(info, cap);
   if (tot == 0) {   // empty list: all starts 0 and gid_sorted = {0} (render_triton.py:392-394)
-    if (i <= nt) starts[i] = 0;
-    if (i == 0) gids[0] = 0;
+    starts[t] = 0;
+    if (t == 0) gids[0] = 0;
     return;
   }
-  if (i >= tot) return;
-  const int k = keys[i];
-  const int prev = i ? keys[i - 1] : -1;
-  for (int t = prev + 1; t <= k; ++t) starts[t] = i;
-  if (i == tot - 1)
-    for (int t = k + 1; t <= nt; ++t) starts[t] = tot;
+  int lo = 0, hi = tot;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (keys[mid] < t) lo = mid + 1; else hi = mid;
+  }
+  starts[t] = lo;
 }
 
 __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
@@ -744,8 +761,7 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
     qin = qout;
     kfin = kout;
   }
-  const int nthr = t > nt + 1 ? t : nt + 1;
-  k_tile_starts<<<div_up(nthr, kBlock), kBlock, 0, st>>>(kfin, gid_sorted, dinfo, t, nt, tile_starts);
+  k_tile_starts<<<div_up(nt + 1, kBlock), kBlock, 0, st>>>(kfin, gid_sorted, dinfo, t, nt, tile_starts);
   return check_launch("k_tile_starts");
 }
 

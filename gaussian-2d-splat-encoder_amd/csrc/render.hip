@@ -222,22 +222,20 @@ __device__ __forceinline__ TileAt tile_at(const LevelTable& L, int tb0, int ntil
 // Waves sharing one 8x8 tile in the forward: each composites a contiguous share of the tile's pair list for
 // the tile's 64 pixels, and the partial sums are added in wave order through LDS. More waves per tile hide
 // the scalar-load latency of the record stream and even out tiles of different lengths.
-#ifndef SPLAT_FWD_SPLIT
-#define SPLAT_FWD_SPLIT 4
-#endif
-template <int TILE>
-__host__ __device__ constexpr int fwd_split() { return TILE == 8 ? SPLAT_FWD_SPLIT : 1; }
-template <int TILE>
-__host__ __device__ constexpr int fwd_threads() { return tile_threads(TILE) * fwd_split<TILE>(); }
+// 8x8 tiles: 4 waves per tile, or 16 with kFlagWide (few tiles with long pair lists: the coarse levels of an
+// octave render, where a launch may hold a few hundred tiles of thousands of pairs each).
+template <int TILE, bool WIDE>
+__host__ __device__ constexpr int fwd_split() { return TILE == 8 ? (WIDE ? 16 : 4) : 1; }
+template <int TILE, int S>
+__host__ __device__ constexpr int fwd_threads() { return tile_threads(TILE) * S; }
 
-template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
-__global__ __launch_bounds__(fwd_threads<TILE>()) void k_fwd_cull(
+template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE, int S>
+__global__ __launch_bounds__((fwd_threads<TILE, S>())) void k_fwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, float* __restrict__ out, float* __restrict__ Tout,
     float* __restrict__ asum_out, float* __restrict__ fg_out, float* __restrict__ slog, float* __restrict__ sa,
     float* __restrict__ sac) {
-  constexpr int S = fwd_split<TILE>();
-  constexpr int NW = fwd_threads<TILE>() / 64;   // waves per workgroup
+  constexpr int NW = fwd_threads<TILE, S>() / 64;   // waves per workgroup
   __shared__ float2 s_uv[NW][64];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
@@ -1173,9 +1171,16 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
     return with_tile(TILE, [&](auto tt) {
       return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
-        k_fwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
-            <<<ntiles, fwd_threads<TT>(), 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum,
-                                                   fg, slog, sa, sac);
+        constexpr bool FL = decltype(fl)::value != 0, OD = decltype(od)::value != 0, UP = decltype(up)::value != 0;
+        if (TT == 8 && (flags & kFlagWide)) {
+          constexpr int S = fwd_split<TT, true>();
+          k_fwd_cull<CC, FL, OD, UP, TT, S><<<ntiles, fwd_threads<TT, S>(), 0, st>>>(
+              rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
+        } else {
+          constexpr int S = fwd_split<TT, false>();
+          k_fwd_cull<CC, FL, OD, UP, TT, S><<<ntiles, fwd_threads<TT, S>(), 0, st>>>(
+              rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
+        }
         return check_launch("k_fwd_cull");
       });
     });

@@ -63,6 +63,7 @@ EXPORTED = tuple(_SIGS)
 FLAG_FIELDS = 1
 FLAG_ODDS = 2
 FLAG_UPS = 4
+FLAG_WIDE = 8
 MAX_LEVELS = 12   # kMaxLevels of the library
 
 STATUS_CAPACITY = 6

@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from ._lib import FLAG_FIELDS, FLAG_ODDS, FLAG_UPS, SplatLevels, check, ptr
+from ._lib import FLAG_FIELDS, FLAG_ODDS, FLAG_UPS, FLAG_WIDE, SplatLevels, check, ptr
 from .params import activate_scale
 from .render import _pixels
 
@@ -330,6 +330,26 @@ def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
 
 
 # ----------------------------------------------------------------------------------------------- cull path
+def _wide(TILE, ntiles, pairs):
+    """FLAG_WIDE (16 waves per 8x8 tile instead of 4) for a forward launch over few tiles with long pair lists,
+    where 4 waves per tile would leave most of the GPU idle."""
+    return FLAG_WIDE if TILE == 8 and 0 < ntiles < 2048 and pairs >= 128 * ntiles else 0
+
+
+def _dense_levels(bins, lt, mask):
+    """Coarse levels (>= 1, present in `mask`) whose tiles hold long pair lists: each gets a forward launch of
+    its own with FLAG_WIDE; the other coarse levels share one launch."""
+    if bins.TILE != 8:
+        return []
+    geom, L = bins.geom, bins.n_levels
+    dense = []
+    for l in range(1, L):
+        tiles = (geom[l + 1][3] if l + 1 < L else bins.nt) - geom[l][3]
+        if (mask >> l) & 1 and _wide(8, tiles, lt[l]):
+            dense.append(l)
+    return dense
+
+
 def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
     """splat_render_fwd for batch b over levels lev = (begin, end); comp = (bg, out, T, asum, fg) or Nones,
     fields = (slog, sa, sac) or Nones."""
@@ -360,8 +380,8 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     for b in range(B):
         ev = kernel_timer.record("fwd")
-        _render_fwd(lib, bins, b, C, flags, (0, 1), 1, (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None),
-                    stream)
+        _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, bins.tot_b[b]), (0, 1), 1,
+                    (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
         kernel_timer.close("fwd", ev)
     return out, (T, asum, fg), bins
 
@@ -377,7 +397,8 @@ def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=
     flags = FLAG_FIELDS | (FLAG_ODDS if odds else 0)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     for b in range(B):
-        _render_fwd(lib, bins, b, C, flags, (0, 1), 1, (None,) * 5, (slog[b], sa[b], sac[b]), stream)
+        _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, bins.tot_b[b]), (0, 1), 1, (None,) * 5,
+                    (slog[b], sa[b], sac[b]), stream)
     return slog, sa, sac, bins
 
 
@@ -397,13 +418,21 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     bgf = _f32(bg)
     odd = FLAG_ODDS if odds else 0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
+    nt0 = bins.ntiles0
     for b in range(B):
         mask = bins.level_mask(b)
+        lt = bins.level_tot_b[b]
         ev = kernel_timer.record("fwd")
         if mask & ~1:
-            _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5, fl, stream)
-        _render_fwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], out[b], T[b], asum[b], fg[b]), fl,
-                    stream)
+            dense = _dense_levels(bins, lt, mask)
+            light = mask & ~1 & ~sum(1 << l for l in dense)
+            if light:
+                _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5, fl, stream)
+            for l in dense:
+                _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5, fl,
+                            stream)
+        _render_fwd(lib, bins, b, C, FLAG_UPS | odd | _wide(TILE, nt0, lt[0]), (0, 1), mask,
+                    (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
         kernel_timer.close("fwd", ev)
     return out, (T, asum, fg), bins
 

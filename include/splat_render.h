@@ -29,6 +29,9 @@ extern "C" {
 #define SPLAT_FLAG_FIELDS 1 /* forward writes raw sums (S_log, S_a, S_ac); backward takes dS_* upstream */
 #define SPLAT_FLAG_ODDS 2   /* colour weight a/(1-a) instead of a */
 #define SPLAT_FLAG_UPS 4    /* composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a */
+#define SPLAT_FLAG_WIDE 8   /* forward, TILE 8: 16 waves share each tile's pair list instead of 4 (a performance
+                               hint for launches of few tiles with long lists; results are identical up to the
+                               order the partial sums are added in) */
 
 /* Levels of a render. A NULL splat_levels* (or mode 0) is the single canvas (H, W). Otherwise splats are
  * routed to canvases ("levels"): level 0 is (H, W); coarser levels are rendered into packed fields and

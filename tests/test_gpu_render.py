@@ -111,3 +111,15 @@ def test_heavy_tail_splats(dev):
     ls = torch.where(heavy[..., None].to(dev), big.to(dev), ls)
     run_case(mu, ls, col, op, bg, th, H, W, 8, odds=False, fields=False, seed=9)
     run_case(mu, ls, col, op, bg, th, H, W, 8, odds=True, fields=True, seed=10)
+
+
+@pytest.mark.parametrize("odds,fields", [(False, False), (True, True), (True, False)])
+def test_long_pair_lists_wide_split(dev, odds, fields):
+    """Few tiles with long pair lists (64 tiles of ~1,500 pairs): the forward takes 16 waves per tile
+    (FLAG_WIDE); images and gradients against the oracle."""
+    H = W = 64
+    scene = random_scene(2000, H, W, seed=23, dev=dev, ls_mean_px=8.0, ls_std=0.3, op_max=0.95)
+    sc = activate_scale(scene[1])
+    gid, st = oracle_pairs(scene[0], sc, H, W, 8)
+    assert RH._wide(8, len(st) - 1, int(st[-1])), "the scene must take the 16-wave forward"
+    run_case(*scene, H, W, 8, odds, fields, seed=24)
