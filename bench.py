@@ -102,6 +102,54 @@ def time_loop(fn, steps, warmup):
     return start.elapsed_time(end) / steps, wall
 
 
+def kernel_times(leaves, H, W, odds, reps):
+    """Average device time (ms) of each stage of the fwd+bwd step, from HIP events on the stream the kernels
+    run on. The forward tile kernel, the backward tile kernel and the per-splat reduction are each launched
+    `reps` times back to back between two events (same inputs, outputs overwritten), so the GPU never waits
+    on the host inside the bracket; the binning (which reads its pair count back to the host once per call)
+    is bracketed call by call. Also returns the binning of the frame (pair count, pixel-pairs)."""
+    dev = leaves[0].device
+    mu, ls, col, op, bg, th = [t.detach() for t in leaves]
+    sc = torch.nn.functional.softplus(ls) + 1e-4
+    out, (T, asum, fg), bins = RH._forward_cull(mu, sc, col, op, bg, th, H, W, 8, 3.0, odds=odds)
+    C = col.shape[-1]
+    gout = torch.randn(out.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+    lib, stream = RH._lib.load(), RH._lib.stream_ptr(dev)
+    flags = RH.FLAG_ODDS if odds else 0
+    bgf = bg.contiguous()
+    comp = (bgf[0], out[0], T[0], asum[0], fg[0])
+    sums, bg_part = RH._bwd_buffers(lib, bins, 0, C, True, dev)
+    up = (bgf[0], T[0], asum[0], fg[0], gout[0], None, None, None)
+    grads = RH._grads_out(1, mu.shape[1], C, dev, th is not None)
+    g_bg = torch.empty(1, C, device=dev)
+    fwd_flags = flags | RH._wide(8, bins.nt, bins.tot_b[0])
+
+    def span(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    ms = {
+        "fwd": span(lambda: RH._render_fwd(lib, bins, 0, C, fwd_flags, (0, 1), 1, comp, (None,) * 3, stream)),
+        "bwd": span(lambda: RH._render_bwd(lib, bins, 0, C, flags, (0, 1), 1, up, sums, bg_part, stream)),
+        "reduce": span(lambda: RH._reduce(lib, bins, 0, C, sums, bg_part, grads, g_bg[0], stream)),
+    }
+    RH.kernel_timer.enable(True)
+    for _ in range(reps):
+        RH._bin(mu, sc, col, op, th, H, W, 8, 3.0)
+    ev = RH.kernel_timer.elapsed_ms()
+    RH.kernel_timer.enable(False)
+    ms["bin"] = sum(ev["bin"]) / len(ev["bin"])
+    return ms, bins
+
+
 def cpu_baseline(s, rows=(368, 400), threads=None):
     """The reference's CPU renderer (render.py:90-110 math, fp32 torch, materialised falloff), restated in
     oracle/render_ref.py, over a band of rows of the same frame; scaled to a full frame."""
@@ -258,16 +306,8 @@ def main():
     ms_oct_fwd, _ = time_loop(oct_fwd, args.steps, args.warmup)
     ms_oct, _ = time_loop(oct_fwd_bwd, args.steps, args.warmup)
 
-    # live kernel timing: HIP events bracketing the per-tile forward / backward launches over K steps
-    RH.kernel_timer.enable(True)
-    for _ in range(args.steps):
-        fwd_bwd()
-    ev = RH.kernel_timer.elapsed_ms()
-    RH.kernel_timer.enable(False)
-    avg = {k: sum(v) / len(v) for k, v in ev.items()}
-    _, _, bins = RH._forward_cull(leaves[0].detach(), torch.nn.functional.softplus(leaves[1].detach()) + 1e-4,
-                                  leaves[2].detach(), leaves[3].detach(), leaves[4].detach(), leaves[5].detach(),
-                                  H, W, 8, 3.0, odds=odds)
+    # live kernel timing: HIP events around K back-to-back launches of each stage on the stream it runs on
+    avg, bins = kernel_times(leaves, H, W, odds, args.steps)
     tot = bins.tot_b[0]
     ppe = ppe_of(bins, H, W)
     fl_f, fl_b = FLOPS_FWD[odds] * ppe, FLOPS_BWD[odds] * ppe

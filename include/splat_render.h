@@ -150,7 +150,8 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels *lv
                            float *dslog, float *dsa, float *dsac, void *ws, size_t ws_bytes, void *stream);
 
 /* Backward, step 2: per-splat reduction of the pair sums into parameter gradients, written (not
- * accumulated), deterministic, no global atomics, one launch. Takes the binning's offsets and pair_splat.
+ * accumulated), deterministic, no global atomics, one launch. Takes the binning's offsets (splat g owns the
+ * sums records [offsets[g], offsets[g+1])); pair_splat is not read and may be NULL.
  * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
  * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = ntiles0 per-tile partials of step 1.
  * One call covers the pairs of every level.
