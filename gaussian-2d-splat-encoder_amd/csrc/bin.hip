@@ -36,7 +36,7 @@ template <int C>
 __global__ __launch_bounds__(kBlock) void k_decode_count(
     const float* __restrict__ mu, const float* __restrict__ scale, const float* __restrict__ theta,
     const float* __restrict__ opacity, const float* __restrict__ color, int N, LevelTable L, Routing R, float fT,
-    float cutoff, int do_bin, float4* __restrict__ rec, int4* __restrict__ rect, int* __restrict__ counts,
+    float cutoff, int do_bin, int act, float4* __restrict__ rec, int4* __restrict__ rect, int* __restrict__ counts,
     long long* __restrict__ block_sums) {
   __shared__ long long s_part[kWaves];
   __shared__ int s_lev[kMaxLevels];
@@ -49,7 +49,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   bool bad = false;
   if (g < N) {
     const float2 m = reinterpret_cast<const float2*>(mu)[g];      // (y, x)
-    const float2 s = reinterpret_cast<const float2*>(scale)[g];   // (sy, sx)
+    float2 s = reinterpret_cast<const float2*>(scale)[g];   // (sy, sx), or raw log-scales with act
+    if (act) s = make_float2(activate_scale(s.x), activate_scale(s.y));
     float sn = 0.f, cs = 1.f;
     if (theta) sincosf(theta[g], &sn, &cs);
     const float ky = kWhiten / s.x, kx = kWhiten / s.y;
@@ -676,7 +677,7 @@ int splat_decode(const float* mu, const float* scale, const float* theta, const 
   LevelTable L{};
   Routing R{};
 #define SPLAT_DECODE(CC)                                                                                      \
-  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, 1.f, 0.f, 0,        \
+  k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, 1.f, 0.f, 0, 0,     \
                                             reinterpret_cast<float4*>(rec), nullptr, nullptr, nullptr)
   switch (C) { case 1: SPLAT_DECODE(1); break; case 2: SPLAT_DECODE(2); break;
                case 3: SPLAT_DECODE(3); break; default: SPLAT_DECODE(4); break; }
@@ -691,11 +692,12 @@ namespace {
 // Launches of the count phase (decode + route + count + offsets + info). Arguments already validated.
 int bin_count_launch(const float* mu, const float* scale, const float* theta, const float* opacity,
                      const float* color, int C, int N, const LevelTable& L, const Routing& R, int TILE, float cutoff,
-                     float* rec, int* rect, int* offsets, long long* info, void* ws, hipStream_t st) {
+                     int flags, float* rec, int* rect, int* offsets, long long* info, void* ws, hipStream_t st) {
   const int nb = div_up(N, kBlock);
   long long* sums = (long long*)ws;
 #define SPLAT_DC(CC)                                                                                         \
   k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, (float)TILE, cutoff, 1, \
+                                            (flags & kFlagLogScale) ? 1 : 0,                                \
                                             reinterpret_cast<float4*>(rec), reinterpret_cast<int4*>(rect), \
                                             offsets, sums)
   switch (C) { case 1: SPLAT_DC(1); break; case 2: SPLAT_DC(2); break;
@@ -779,18 +781,19 @@ hipEvent_t readback_event() {
 extern "C" {
 
 int splat_bin_count(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
-                    int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, float* rec, int* rect,
-                    int* offsets, long long* info, void* ws, size_t ws_bytes, void* stream) {
+                    int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, int flags, float* rec,
+                    int* rect, int* offsets, long long* info, void* ws, size_t ws_bytes, void* stream) {
   if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
     return set_error(kInvalid, "splat_bin_count: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
+  if (flags & ~kFlagLogScale) return set_error(kInvalid, "splat_bin_count: unknown flags 0x%x", flags);
   LevelTable L;
   Routing R;
   if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin_count: bad levels");
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
     return set_error(kInvalid, "splat_bin_count: null pointer");
   if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
-  return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, rec, rect, offsets, info, ws,
-                          (hipStream_t)stream);
+  return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets, info,
+                          ws, (hipStream_t)stream);
 }
 
 size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
@@ -813,12 +816,13 @@ int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, in
 }
 
 int splat_bin(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color, int C,
-              int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, long long max_pairs, float* rec,
-              int* rect, int* offsets, long long* info, long long* info_host, void* ws_count, size_t ws_count_bytes,
+              int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, int flags, long long max_pairs,
+              float* rec, int* rect, int* offsets, long long* info, long long* info_host, void* ws_count, size_t ws_count_bytes,
               long long pair_cap, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws_pairs,
               size_t ws_pairs_bytes, void* stream) {
   if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1 || pair_cap < 0)
     return set_error(kInvalid, "splat_bin: N=%d C=%d H=%d W=%d TILE=%d cap=%lld", N, C, H, W, TILE, pair_cap);
+  if (flags & ~kFlagLogScale) return set_error(kInvalid, "splat_bin: unknown flags 0x%x", flags);
   LevelTable L;
   Routing R;
   if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin: bad levels");
@@ -826,8 +830,8 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
     return set_error(kInvalid, "splat_bin: null pointer");
   if (ws_count_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin: count workspace too small");
   hipStream_t st = (hipStream_t)stream;
-  int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, rec, rect, offsets, info,
-                            ws_count, st);
+  int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets,
+                            info, ws_count, st);
   if (rc) return rc;
   // the one device -> host read of the render: totals and error bits
   hipEvent_t ev = readback_event();

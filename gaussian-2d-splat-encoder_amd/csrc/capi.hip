@@ -28,6 +28,6 @@ extern "C" {
 
 const char* splat_last_error(void) { return splat::g_last_error; }
 
-int splat_abi_version(void) { return 1; }
+int splat_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -488,7 +488,7 @@ template <int C>
 __device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec, const float* sums,
                                             float* __restrict__ g_mu, float* __restrict__ g_scale,
                                             float* __restrict__ g_theta, float* __restrict__ g_op,
-                                            float* __restrict__ g_col) {
+                                            float* __restrict__ g_col, const float* __restrict__ lsc) {
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
   const float op = r4[1].z;
   const float4 r3 = r4[3];
@@ -497,8 +497,15 @@ __device__ __forceinline__ void splat_grads(int g, const float* __restrict__ rec
   const float grx = -op * sums[2] / (kWhiten * sx);
   g_mu[2 * g + 0] = -(cs * gry - sn * grx);
   g_mu[2 * g + 1] = -(sn * gry + cs * grx);
-  g_scale[2 * g + 0] = 2.f * kLn2 * op * sums[3] / sy;
-  g_scale[2 * g + 1] = 2.f * kLn2 * op * sums[4] / sx;
+  float gsy = 2.f * kLn2 * op * sums[3] / sy;
+  float gsx = 2.f * kLn2 * op * sums[4] / sx;
+  if (lsc) {   // w.r.t. the raw log-scales: chain through the activation
+    const float2 x = reinterpret_cast<const float2*>(lsc)[g];
+    gsy = activate_scale_grad(gsy, x.x);
+    gsx = activate_scale_grad(gsx, x.y);
+  }
+  g_scale[2 * g + 0] = gsy;
+  g_scale[2 * g + 1] = gsx;
   if (g_theta) g_theta[g] = -2.f * kLn2 * op * sums[5] * ((sx - sy) * (sx + sy) / (sx * sy));
   g_op[g] = sums[0];
 #pragma unroll
@@ -827,7 +834,7 @@ __global__ __launch_bounds__(256) void k_splat_sum(const float* __restrict__ rec
                                                    float* __restrict__ g_scale, float* __restrict__ g_theta,
                                                    float* __restrict__ g_op, float* __restrict__ g_col,
                                                    const float* __restrict__ bg_part, int nparts,
-                                                   float* __restrict__ g_bg) {
+                                                   float* __restrict__ g_bg, const float* __restrict__ lsc) {
   constexpr int R = pair_rec<C>();
   constexpr int kPerBlock = 256 / kSumLanes;
   if (g_bg && blockIdx.x == 0) {   // first, so it overlaps the splat waves
@@ -866,7 +873,7 @@ __global__ __launch_bounds__(256) void k_splat_sum(const float* __restrict__ rec
   }
   if (g >= N || r != 0) return;
   if (q1 > q0)
-    splat_grads<C>(g, rec, s, g_mu, g_scale, g_theta, g_op, g_col);
+    splat_grads<C>(g, rec, s, g_mu, g_scale, g_theta, g_op, g_col, lsc);
   else
     zero_grads<C>(g, g_mu, g_scale, g_theta, g_op, g_col);
 }
@@ -985,7 +992,7 @@ __global__ __launch_bounds__(256) void k_acc_finalize(const float* __restrict__ 
   if (g >= N) return;
   float v[kSums];
   for (int k = 0; k < kSums; ++k) v[k] = acc[(size_t)g * kAcc + k];
-  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col);
+  splat_grads<C>(g, rec, v, g_mu, g_scale, g_theta, g_op, g_col, nullptr);
 }
 
 // ------------------------------------------------------------------------------------ upsample adjoint
@@ -1257,8 +1264,8 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels* lv
 }
 
 int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_splat, long long tot,
-                       int N, int C, const float* pair_sums, const float* bg_part, int nparts, float* g_mu,
-                       float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* stream) {
+                       int N, int C, const float* pair_sums, const float* bg_part, int nparts, const float* log_scale,
+                       float* g_mu, float* g_scale, float* g_theta, float* g_op, float* g_color, float* g_bg, void* stream) {
   if (N < 0 || tot < 0 || tot > 0x7fffffffLL - 64 || (N == 0 && tot > 0))
     return set_error(kInvalid, "splat_reduce_pairs: N=%d tot=%lld", N, tot);
   if ((N > 0 && (!rec || !offsets || !g_mu || !g_scale || !g_op || !g_color)) ||
@@ -1270,7 +1277,7 @@ int splat_reduce_pairs(const float* rec, const int* offsets, const int* pair_spl
     constexpr int CC = decltype(cc)::value;
     if (tot > 0)
       k_splat_sum<CC><<<(unsigned)((N + 256 / kSumLanes - 1) / (256 / kSumLanes)) + extra, 256, 0, st>>>(
-          rec, pair_sums, offsets, N, g_mu, g_scale, g_theta, g_op, g_color, bg_part, nparts, g_bg);
+          rec, pair_sums, offsets, N, g_mu, g_scale, g_theta, g_op, g_color, bg_part, nparts, g_bg, log_scale);
     else if (N > 0 || g_bg)
       k_zero_grads<CC><<<(unsigned)((N + 255) / 256) + extra, 256, 0, st>>>(N, g_mu, g_scale, g_theta, g_op,
                                                                             g_color, bg_part, nparts, g_bg);

@@ -42,6 +42,7 @@ constexpr int kFlagFields = 1;   // write raw partial sums (S_log, S_a, S_ac) in
 constexpr int kFlagOdds = 2;     // weight colour by the odds a / (1 - a) instead of a
 constexpr int kFlagUps = 4;      // composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a
 constexpr int kFlagWide = 8;     // forward of 8x8 tiles: 16 waves per tile instead of 4 (long pair lists)
+constexpr int kFlagLogScale = 16; // binning: `scale` holds raw log-scales, activated by the decode pass
 
 // Status codes of the C-ABI.
 enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2, kUnsupported = 3, kOverflow = 4, kWorkspace = 5,
@@ -59,6 +60,20 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int n) {
   const int q = n / kXcd, r = n % kXcd;
   const int x = bid % kXcd, l = bid / kXcd;
   return x * q + (x < r ? x : r) + l;
+}
+
+// Scale activation of params.py:18-28, softplus(x) + 1e-4, evaluated as torch evaluates F.softplus(x) + 1e-4
+// in fp32 (beta 1, threshold 20: x above the threshold passes through; the constant is added as float 1e-4).
+__device__ __forceinline__ float activate_scale(float x) {
+  const float sp = x > 20.f ? x : log1pf(expf(x));
+  return sp + 1e-4f;
+}
+
+// Upstream gradient g of activate_scale(x) -> gradient w.r.t. x, as torch's softplus backward evaluates it:
+// x > 20 ? g : g * z / (z + 1) with z = e^x (the + 1e-4 passes g through unchanged).
+__device__ __forceinline__ float activate_scale_grad(float g, float x) {
+  const float z = expf(x);
+  return x > 20.f ? g : g * z / (z + 1.f);
 }
 
 __device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

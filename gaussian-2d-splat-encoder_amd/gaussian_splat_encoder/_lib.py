@@ -38,10 +38,10 @@ _SIGS = {
     "splat_decode": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "splat_bin_count_workspace_bytes": (_SZ, [_I]),
     "splat_levels_geometry": (_I, [_I, _I, _I, _LV, _VP, _I]),
-    "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _VP, _VP, _VP, _VP, _VP, _SZ,
+    "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _VP, _VP, _VP, _VP, _VP, _SZ,
                              _VP]),
     "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _LL]),
-    "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
+    "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                        _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP, _VP,
@@ -51,7 +51,7 @@ _SIGS = {
                               _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_upsample_adjoint_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV]),
     "splat_upsample_adjoint": (_I, [_I, _I, _I, _I, _LV, _U, _VP, _VP, _VP, _VP, _SZ, _VP]),
-    "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_exact_fwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "splat_exact_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
     "splat_exact_bwd": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
@@ -64,6 +64,7 @@ FLAG_FIELDS = 1
 FLAG_ODDS = 2
 FLAG_UPS = 4
 FLAG_WIDE = 8
+FLAG_LOG_SCALE = 16
 MAX_LEVELS = 12   # kMaxLevels of the library
 
 STATUS_CAPACITY = 6

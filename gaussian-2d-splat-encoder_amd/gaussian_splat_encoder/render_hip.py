@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from ._lib import FLAG_FIELDS, FLAG_ODDS, FLAG_UPS, FLAG_WIDE, SplatLevels, check, ptr
+from ._lib import FLAG_FIELDS, FLAG_LOG_SCALE, FLAG_ODDS, FLAG_UPS, FLAG_WIDE, SplatLevels, check, ptr
 from .params import activate_scale
 from .render import _pixels
 
@@ -236,13 +236,16 @@ class _Carve:
         return t if shape is None else t.view(shape)
 
 
-def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True, lv=None) -> TileBins:
+def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True, lv=None,
+         scale_is_log=False) -> TileBins:
     """Decode + bin every batch (render_triton.py:351-409). One host read of the pair totals per image.
     with_maps=False skips the pair maps only the backward needs (forward-only renders). `lv` (a
-    _lib.SplatLevels) routes splats to levels (octave / coarse-fine renders, render_triton.py:879-980)."""
+    _lib.SplatLevels) routes splats to levels (octave / coarse-fine renders, render_triton.py:879-980).
+    scale_is_log: `scale` holds fp32 raw log-scales, activated in the decode pass (params.py:18-28)."""
     _dev_check(mu, scale, color, opacity, theta)
     ev = kernel_timer.record("bin")
-    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv)
+    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv,
+                     FLAG_LOG_SCALE if scale_is_log else 0)
     kernel_timer.close("bin", ev)
     return bins
 
@@ -261,7 +264,7 @@ def _pair_buffers(lib, N, nt, cap, with_maps, dev):
     return _Carve([4 * c, 4 * (nt + 1), 4 * m, 4 * m, lib.splat_bin_pairs_workspace_bytes(N, nt, cap)], dev)
 
 
-def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv):
+def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv, sflags):
     B, N, C = color.shape
     dev = mu.device
     lib = _lib.load()
@@ -291,7 +294,7 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         pp = (lambda i: None) if pb is None else pb.ptr
         info_np[0] = info_np[1] = 0
         rc = lib.splat_bin(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]), ptr(col_[b]),
-                           C, N, H, W, TILE, float(cutoff), lvr, budget, blk.ptr(0), blk.ptr(1), blk.ptr(2),
+                           C, N, H, W, TILE, float(cutoff), lvr, sflags, budget, blk.ptr(0), blk.ptr(1), blk.ptr(2),
                            blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0), pp(1),
                            pp(2) if with_maps else None, pp(3) if with_maps else None, pp(4),
                            0 if pb is None else pb.nbytes(4), stream)
@@ -368,12 +371,12 @@ def _composite_buffers(B, P, C, dev):
 
 
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
-                  with_maps=True):
+                  with_maps=True, scale_is_log=False):
     """Composite forward (render_triton.py:538-567): out [B,P,C], (T, asum, fg), bins."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, scale_is_log=scale_is_log)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     bgf = _f32(bg)
     flags = FLAG_ODDS if odds else 0
@@ -402,14 +405,16 @@ def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=
     return slog, sa, sac, bins
 
 
-def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, with_maps=True):
+def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, with_maps=True,
+                    scale_is_log=False):
     """Fused multi-level forward (render_triton.py:879-980 without the per-group torch glue): one binning
     over every level, FIELDS renders of the coarse levels into packed fields, then the level-0 composite
     adds their bilinear upsamples. Returns out [B,P,C], (T, asum unclamped, fg), bins."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv=lv)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv=lv,
+                scale_is_log=scale_is_log)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     L = bins.n_levels
     # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
@@ -452,8 +457,9 @@ def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stre
                                *[ptr(u) for u in upstream], ptr(sums), ptr(bg_part), stream), "splat_render_bwd")
 
 
-def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream):
-    """Per-splat reduction of batch b's pair sums into `grads` (and g_bg from the level-0 tile partials)."""
+def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
+    """Per-splat reduction of batch b's pair sums into `grads` (and g_bg from the level-0 tile partials).
+    lsc: the fp32 raw log-scales [B,N,2] of a scale_is_log binning; g_scale is then w.r.t. them."""
     tot = bins.tot_b[b]
     N = bins.N
     ev = kernel_timer.record("reduce")
@@ -461,7 +467,7 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream):
     sl = lambda t: None if (t is None or N == 0) else ptr(t[b])
     check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
                                  bins.p(b, "psplat") if tot else None, tot, N, C, ptr(sums), ptr(bg_part),
-                                 bins.ntiles0, sl(g_mu),
+                                 bins.ntiles0, sl(lsc), sl(g_mu),
                                  sl(g_scale), sl(g_th), sl(g_op), sl(g_col), ptr(g_bg), stream), "splat_reduce_pairs")
     kernel_timer.close("reduce", ev)
 
@@ -474,7 +480,7 @@ def _bwd_buffers(lib, bins, b, C, with_bg, dev):
     return buf[:ns], (buf[ns:] if with_bg else None)
 
 
-def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream):
+def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream, lsc=None):
     """Both backward steps for batch b of a single-level render: per-tile pair sums, then the per-splat
     reduction into `grads`."""
     dev = bins.blocks[b].buf.device
@@ -482,11 +488,13 @@ def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream):
     ev = kernel_timer.record("bwd")
     _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
     kernel_timer.close("bwd", ev)
-    _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream)
+    _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc)
 
 
-def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, bins, H, W, TILE=8, odds=False):
-    """render_triton.py:723-765: grads for mu, scale, color, opacity, bg, theta (None without theta)."""
+def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, bins, H, W, TILE=8, odds=False,
+                   scale_is_log=False):
+    """render_triton.py:723-765: grads for mu, scale, color, opacity, bg, theta (None without theta).
+    scale_is_log: `scale` holds the raw log-scales the binning activated; g_scale is w.r.t. them."""
     B, N, C = color.shape
     dev = mu.device
     grads = _grads_out(B, N, C, dev, theta is not None)
@@ -496,7 +504,7 @@ def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, 
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
         up = (bgf[b], T[b], asum[b], fg[b], go[b], None, None, None)
-        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream)
+        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream, _f32(scale) if scale_is_log else None)
     g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
@@ -517,10 +525,11 @@ def _backward_cull_fields(dS_log, dS_a, dS_ac, mu, scale, color, opacity, theta,
     return grads
 
 
-def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds):
+def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, log_scale=None):
     """Backward of _forward_levels: level-0 composite backward (clamp_min gradient of S_a, render_triton.py
     :918 / :976) writing the pixel upstream, its exact adjoint through the upsample onto the coarse levels,
-    their FIELDS backward, then one per-splat reduction over the pairs of every level."""
+    their FIELDS backward, then one per-splat reduction over the pairs of every level. log_scale: the raw
+    log-scales of a scale_is_log binning (g_scale is then w.r.t. them)."""
     B, N, C = color.shape
     dev = color.device
     grads = _grads_out(B, N, C, dev, has_theta)
@@ -534,6 +543,7 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds):
     lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
     adj_ws = _ws(lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr), dev) if L > 1 \
         else None
+    lsc = None if log_scale is None else _f32(log_scale)
     for b in range(B):
         mask = bins.level_mask(b)
         sums, bg_part = _bwd_buffers(lib, bins, b, C, True, dev)
@@ -545,21 +555,24 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds):
                                              ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
             _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5 + dS, sums, None, stream)
         kernel_timer.close("bwd", ev)
-        _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream)
+        _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream, lsc)
     g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
 class _AlphaRenderCull(torch.autograd.Function):
-    """render_triton.py:813-833. Inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds)."""
+    """render_triton.py:813-833. Inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds).
+    scale_is_log=True: `scale` is the fp32 raw log-scale, activated inside the binning's decode pass, and its
+    gradient is w.r.t. the log-scale (what activate_scale + this Function would give, in one node)."""
 
     @staticmethod
-    def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=False):
+    def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=False, scale_is_log=False):
         out, (T, asum, fg), bins = _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=odds,
-                                                 with_maps=any(ctx.needs_input_grad[:6]))
+                                                 with_maps=any(ctx.needs_input_grad[:6]), scale_is_log=scale_is_log)
         ctx.has_theta = theta is not None
         ctx.HW = (H, W, TILE)
         ctx.odds = odds
+        ctx.scale_is_log = scale_is_log
         ctx.tiles = bins
         ctx.save_for_backward(mu, scale, color, opacity, bg, theta if theta is not None else mu.new_zeros(1),
                               T, asum, fg)
@@ -571,8 +584,9 @@ class _AlphaRenderCull(torch.autograd.Function):
         H, W, TILE = ctx.HW
         th = theta if ctx.has_theta else None
         g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_cull(grad_out, mu, scale, color, opacity, bg, th, T, asum,
-                                                                fg, ctx.tiles, H, W, TILE, odds=ctx.odds)
-        return g_mu, g_scale, g_col, g_op, g_bg, g_th, None, None, None, None, None
+                                                                fg, ctx.tiles, H, W, TILE, odds=ctx.odds,
+                                                                scale_is_log=ctx.scale_is_log)
+        return g_mu, g_scale, g_col, g_op, g_bg, g_th, None, None, None, None, None, None
 
 
 class _AlphaRenderCullFields(torch.autograd.Function):
@@ -607,24 +621,28 @@ class _AlphaRenderCullFields(torch.autograd.Function):
 
 class _AlphaRenderLevels(torch.autograd.Function):
     """Fused octave / coarse-fine render (render_triton.py:879-980) with the levels described by `lv`:
-    inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv) -> out [B,P,C]."""
+    inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, scale_is_log)
+    -> out [B,P,C]. scale_is_log as in _AlphaRenderCull."""
 
     @staticmethod
-    def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+    def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
+                scale_is_log=False):
         out, (T, asum, fg), bins = _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff,
-                                                   max_pairs, odds, lv, any(ctx.needs_input_grad[:6]))
+                                                   max_pairs, odds, lv, any(ctx.needs_input_grad[:6]),
+                                                   scale_is_log=scale_is_log)
         ctx.has_theta = theta is not None
         ctx.odds = odds
         ctx.tiles = bins
-        ctx.save_for_backward(color, bg, T, asum, fg)
+        ctx.scale_is_log = scale_is_log
+        ctx.save_for_backward(color, bg, T, asum, fg, scale if scale_is_log else None)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        color, bg, T, asum, fg = ctx.saved_tensors
+        color, bg, T, asum, fg, log_scale = ctx.saved_tensors
         g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(grad_out, color, bg, ctx.has_theta, T, asum, fg,
-                                                                  ctx.tiles, ctx.odds)
-        return (g_mu, g_scale, g_col, g_op, g_bg, g_th) + (None,) * 7
+                                                                  ctx.tiles, ctx.odds, log_scale)
+        return (g_mu, g_scale, g_col, g_op, g_bg, g_th) + (None,) * 8
 
 
 # ----------------------------------------------------------------------------------------------- exact path
@@ -693,15 +711,31 @@ class _AlphaRender(torch.autograd.Function):
 
 
 # ----------------------------------------------------------------------------------------------- public API
+def _scale_arg(log_scale):
+    """(scale, scale_is_log) for the binned autograd Functions: fp32 raw log-scales go in as they are and are
+    activated in the decode pass (the bits of activate_scale in fp32); other dtypes are activated by torch
+    first, in their own dtype, as the reference does."""
+    if log_scale.dtype == torch.float32:
+        return log_scale, True
+    return activate_scale(log_scale), False
+
+
+def _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+    scale, is_log = _scale_arg(log_scale)
+    return _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
+                                    is_log)
+
+
 def render_alpha_full_triton(mu, log_scale, color, opacity, bg, H, W, theta=None, cull=False, TILE=8, cutoff=3.0,
                              odds=False):
     """render_triton.py:326-347. cull=False: exact (every pixel sums every splat); cull=True: tile-binned
     at `cutoff` sigma. Returns [B,C,H,W]. The name is kept for drop-in compatibility; no Triton is used."""
     B, N, C = color.shape
-    scale = activate_scale(log_scale)
     if cull:
-        out = _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds)
+        scale, is_log = _scale_arg(log_scale)
+        out = _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds, is_log)
     else:
+        scale = activate_scale(log_scale)
         if odds:
             raise NotImplementedError("odds compositing is only wired through the cull/octave path; "
                                       "use cull=True or render_alpha_octave")
@@ -747,9 +781,8 @@ def render_alpha_multires(mu, log_scale, color, opacity, bg, H, W, theta=None, n
     fields are summed (bilinear upsample of the coarse ones) and composited once. Fused: one binning over
     both canvases and one composite kernel that upsamples the coarse fields in its epilogue."""
     B, N, C = color.shape
-    scale = activate_scale(log_scale)
     lv = _multires_levels(H, W, N, n_coarse, coarse_factor)
-    out = _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
+    out = _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
     return out.reshape(B, H, W, C).permute(0, 3, 1, 2)
 
 
@@ -776,7 +809,6 @@ def render_alpha_octave(mu, log_scale, color, opacity, bg, H, W, theta=None, cut
     upsamples the coarse octaves' fields in its epilogue (octaves whose canvas is clamped to 8x8 share one
     level, which sums the same fields)."""
     B, N, C = color.shape
-    scale = activate_scale(log_scale)
     lv = _octave_levels(H, W, base_texels, max_octaves)
-    out = _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
+    out = _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
     return out.reshape(B, H, W, C).permute(0, 3, 1, 2)

@@ -32,6 +32,10 @@ extern "C" {
 #define SPLAT_FLAG_WIDE 8   /* forward, TILE 8: 16 waves share each tile's pair list instead of 4 (a performance
                                hint for launches of few tiles with long lists; results are identical up to the
                                order the partial sums are added in) */
+#define SPLAT_FLAG_LOG_SCALE 16 /* binning (splat_bin, splat_bin_count): `scale` holds the raw log-scales [N,2]; the
+                                   decode pass activates them, softplus(x) + 1e-4 with the bits torch's fp32
+                                   F.softplus(x) + 1e-4 gives (params.py:18-28), so callers need no activation
+                                   pass of their own; rec holds the activated scale either way */
 
 /* Levels of a render. A NULL splat_levels* (or mode 0) is the single canvas (H, W). Otherwise splats are
  * routed to canvases ("levels"): level 0 is (H, W); coarser levels are rendered into packed fields and
@@ -75,7 +79,7 @@ int splat_decode(const float *mu, const float *scale, const float *theta, const 
 size_t splat_bin_count_workspace_bytes(int N);
 int splat_bin_count(const float *mu, const float *scale, const float *theta, const float *opacity,
                     const float *color, int C, int N, int H, int W, int TILE, float cutoff,
-                    const splat_levels *lv, float *rec, int *rect, int *offsets, long long *info, void *ws,
+                    const splat_levels *lv, int flags, float *rec, int *rect, int *offsets, long long *info, void *ws,
                     size_t ws_bytes, void *stream);
 
 /* Binning phase 2: expand rects into pairs, stable radix sort on the global tile id, CSR tile starts.
@@ -107,7 +111,7 @@ int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, in
  * Replaces render_triton.py:351-409 with its one sync (:391) and budget check (:378-385). */
 int splat_bin(const float *mu, const float *scale, const float *theta, const float *opacity,
               const float *color, int C, int N, int H, int W, int TILE, float cutoff, const splat_levels *lv,
-              long long max_pairs, float *rec, int *rect, int *offsets, long long *info, long long *info_host,
+              int flags, long long max_pairs, float *rec, int *rect, int *offsets, long long *info, long long *info_host,
               void *ws_count, size_t ws_count_bytes, long long pair_cap, int *gid_sorted, int *tile_starts,
               int *pair_splat, int *pair_q, void *ws_pairs, size_t ws_pairs_bytes, void *stream);
 
@@ -152,13 +156,15 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels *lv
 /* Backward, step 2: per-splat reduction of the pair sums into parameter gradients, written (not
  * accumulated), deterministic, no global atomics, one launch. Takes the binning's offsets (splat g owns the
  * sums records [offsets[g], offsets[g+1])); pair_splat is not read and may be NULL.
- * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale), g_theta[N] (NULL when there is no theta),
+ * g_mu[N,2], g_scale[N,2] (w.r.t. the activated scale; with log_scale[N,2] given, the raw log-scales of a
+ * SPLAT_FLAG_LOG_SCALE binning, w.r.t. those, chained as torch's softplus backward evaluates it),
+ * g_theta[N] (NULL when there is no theta),
  * g_op[N], g_color[N,C]; g_bg[C] (NULL skips) from the nparts = ntiles0 per-tile partials of step 1.
  * One call covers the pairs of every level.
  * Replaces the index_add_ scatter and the g_bg reduction, render_triton.py:723-810. */
 int splat_reduce_pairs(const float *rec, const int *offsets, const int *pair_splat, long long tot, int N,
-                       int C, const float *pair_sums, const float *bg_part, int nparts, float *g_mu,
-                       float *g_scale, float *g_theta, float *g_op, float *g_color, float *g_bg, void *stream);
+                       int C, const float *pair_sums, const float *bg_part, int nparts, const float *log_scale,
+                       float *g_mu, float *g_scale, float *g_theta, float *g_op, float *g_color, float *g_bg, void *stream);
 
 /* Exact (unculled) path: every pixel sums every splat; pixel centres py[P], px[P] supplied by the caller.
  * Replaces _render_fwd_kernel / _render_bwd_kernel and their wrappers, render_triton.py:58-303. */

@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.splat_abi_version() == 1
+    assert lib.splat_abi_version() == 2
 
 
 def test_workspace_queries_without_gpu():
@@ -43,7 +43,7 @@ def test_invalid_arguments_are_reported_not_launched():
     assert b"null" in lib.splat_last_error()
     with pytest.raises(_lib.SplatError, match="invalid argument"):
         _lib.check(rc, "splat_render_fwd")
-    assert lib.splat_bin_count(None, None, None, None, None, 9, 10, 8, 8, 8, 3.0, None, None, None, None, None,
+    assert lib.splat_bin_count(None, None, None, None, None, 9, 10, 8, 8, 8, 3.0, None, 0, None, None, None, None,
                                None, 0, None) == 1
     oct6 = ctypes.byref(_lib.SplatLevels(1, 6, 8.0, 0, 0, 0))
     # the composite renders level 0 only; FIELDS and UPS exclude each other; level range inside the table
@@ -107,3 +107,15 @@ def test_host_rejects_cpu_tensors():
     z = torch.zeros
     with pytest.raises(RuntimeError, match="device tensors"):
         render_alpha_octave(z(1, 4, 2), z(1, 4, 2), z(1, 4, 3), z(1, 4), z(1, 3), 16, 16)
+
+
+def test_bin_rejects_unknown_flags():
+    """splat_bin / splat_bin_count accept only SPLAT_FLAG_LOG_SCALE; the check precedes any device work."""
+    lib = _lib.load()
+    for bad in (1, 8, 32, 16 | 2):
+        assert lib.splat_bin_count(None, None, None, None, None, 3, 4, 16, 16, 8, 3.0, None, bad, None, None, None,
+                                   None, None, 0, None) == 1
+        assert b"unknown flags" in lib.splat_last_error()
+        assert lib.splat_bin(None, None, None, None, None, 3, 4, 16, 16, 8, 3.0, None, bad, -1, None, None, None,
+                             None, None, None, 0, 0, None, None, None, None, None, 0, None) == 1
+        assert b"unknown flags" in lib.splat_last_error()

@@ -170,3 +170,35 @@ def test_batch_of_three(dev):
         assert (o1[0] - out[b]).abs().max().item() <= 1e-6
         for n in ["mu", "ls", "col", "op", "th"]:
             assert rel_err(np_(g1[n][0]), np_(gd[n][b])) <= 1e-5, n
+
+
+@pytest.mark.parametrize("kind", ["cull", "octave", "multires"])
+def test_scale_activation_in_decode_matches_torch_bits(dev, monkeypatch, kind):
+    """fp32 log-scales are activated inside the binning's decode pass and the log-scale gradient is chained in
+    the per-splat reduction. Both must give exactly the bits of activate_scale (torch's softplus + 1e-4) and
+    its autograd: same decoded records, pair lists, image and gradients."""
+    H = W = 64
+    scene = list(random_scene(800, H, W, seed=41, dev=dev))
+    ls = scene[1].clone()
+    # every regime of softplus: exp underflow, small, around 0, the threshold 20 and past it
+    ls[0, :9, :] = torch.tensor([-100., -30., -8., -2., 0., 1.5, 19.9, 20., 20.5], device=dev)[:, None]
+    ls[0, 9:12, 0] = torch.tensor([-4., 2., 21.], device=dev)
+    scene[1] = ls
+    fn = {"cull": RH.render_alpha_full_triton, "octave": RH.render_alpha_octave,
+          "multires": RH.render_alpha_multires}[kind]
+    kw = {"cull": {"cull": True}, "octave": {}, "multires": {"n_coarse": 100}}[kind]
+    gout = gout_for(H, W, dev, 9)
+    mu, _, col, op, _, th = scene
+    b_fused = RH._bin(mu, ls, col, op, th, H, W, 8, 3.0, scale_is_log=True)
+    b_torch = RH._bin(mu, activate_scale(ls), col, op, th, H, W, 8, 3.0)
+    rec = lambda b: b.blocks[0].view(0, 16 * 800, torch.float32)
+    assert torch.equal(rec(b_fused), rec(b_torch))
+    g_f, s_f = b_fused.as_tuple()[:2]
+    g_t, s_t = b_torch.as_tuple()[:2]
+    assert torch.equal(g_f[0], g_t[0]) and torch.equal(s_f[0], s_t[0])
+    out_f, gd_f = device_run(fn, scene, gout, H=H, W=W, **kw)
+    monkeypatch.setattr(RH, "_scale_arg", lambda t: (activate_scale(t), False))
+    out_t, gd_t = device_run(fn, scene, gout, H=H, W=W, **kw)
+    assert torch.equal(out_f, out_t)
+    for n in NAMES:
+        assert torch.equal(gd_f[n], gd_t[n]), (n, (gd_f[n] - gd_t[n]).abs().max().item())
