@@ -9,11 +9,9 @@
 //
 // Backward: one wave per tile, lane = pair. The tile's per-pixel upstream terms (dS_log, dS_a, dS_ac)
 // are derived once (lane = pixel) into LDS; each lane then walks the tile's pixels for its own pair and
-// accumulates the per-pair sums in registers (the per-tile reduction) and stores them in pair order.
-// No global atomics: a reduce pass walks the pairs in splat-major order (wave = 64 consecutive pairs,
-// gathered through the binning's inverse permutation), sums each splat's pairs with a segmented scan, and
-// a fix-up pass completes splats whose pairs span several waves. Deterministic. The sums become
-// parameter gradients by:
+// accumulates the per-pair sums in registers (the per-tile reduction) and stores them at the pair's
+// splat-major index. No global atomics: a reduce pass sums each splat's records (contiguous, in a fixed
+// order) into its gradients. Deterministic. The sums become parameter gradients by:
 //   q    = da * falloff where op * falloff < 1 - 1e-4 (0 on the clamp)      da: render_triton.py:688-697
 //   g_op = sum q,   Qu = sum q u,  Qv = sum q v,  Quu = sum q u^2,  Qvv = sum q v^2,  Quv = sum q u v
 //   g_sy = 2 ln2 op Quu / sy,  g_sx = 2 ln2 op Qvv / sx
@@ -389,12 +387,12 @@ __device__ __forceinline__ PairOp pair_op(float op) {
   return {op, kNearOpaqueBwd * rop, rop};
 }
 
-// Accumulation of one pixel-pair of the backward from its falloff f (0 for a lane on the clamp) and 1 - a.
-// The colour sums are accumulated as sum w' * dS_ac with w' = w / op (the caller multiplies by op once per
-// pair).
+// One pixel-pair of the backward from its falloff f (0 for a lane on the clamp) and 1 - a: adds the colour
+// terms to gc (as sum w' * dS_ac with w' = w / op; the caller multiplies by op once per pair) and returns
+// q = da * falloff, the pixel's weight in the pair's moment sums.
 template <int C, bool ODDS>
-__device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, const float4& col, const float4& pa,
-                                        const float4& pb, PairSums<C>& s) {
+__device__ __forceinline__ float bwd_q(float f, float oma, const float4& col, const float4& pa, const float4& pb,
+                                       float* gc) {
   const float rr = hw_rcp(oma);
   float ct = fmaf(pa.z, col.x, pa.y);   // dS_a + sum_c dS_ac[c] col[c]
   if (C > 1) ct = fmaf(pa.w, col.y, ct);
@@ -408,11 +406,18 @@ __device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, co
     da = fmaf(-pa.x, rr, ct);
     cw = f;
   }
-  s.gc[0] = fmaf(cw, pa.z, s.gc[0]);
-  if (C > 1) s.gc[1] = fmaf(cw, pa.w, s.gc[1]);
-  if (C > 2) s.gc[2] = fmaf(cw, pb.x, s.gc[2]);
-  if (C > 3) s.gc[3] = fmaf(cw, pb.y, s.gc[3]);
-  const float q = da * f;
+  gc[0] = fmaf(cw, pa.z, gc[0]);
+  if (C > 1) gc[1] = fmaf(cw, pa.w, gc[1]);
+  if (C > 2) gc[2] = fmaf(cw, pb.x, gc[2]);
+  if (C > 3) gc[3] = fmaf(cw, pb.y, gc[3]);
+  return da * f;
+}
+
+// Accumulation of one pixel-pair of the backward with its whitened offsets u, v.
+template <int C, bool ODDS>
+__device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, const float4& col, const float4& pa,
+                                        const float4& pb, PairSums<C>& s) {
+  const float q = bwd_q<C, ODDS>(f, oma, col, pa, pb, s.gc);
   const float qu = q * u, qv = q * v;
   s.q += q;
   s.qu += qu;
@@ -560,29 +565,118 @@ __device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
 template <int TILE>
 __host__ __device__ constexpr int up_stride() { return TILE + 1; }
 
-// Per-pair sums over rows [row0, row0 + nrows) of the tile (lane = pair), with 1 - a = 1 - op f by one fma:
-// the caller has taken every pair that may be near-opaque in the tile (near_possible) out of the wave's
-// lanes. The row terms A ly and Cc ly are taken once per row; per pixel, u and v are one fma each with the
-// column offsets lxs[] (wave-uniform, SGPR operands); the row's upstream terms come from LDS.
+// Offsets of the tile's pixel centres from the tile centre (cy, cx from the first pixel centre: half the
+// offsets of the last row / column), which lies at (ty, tx): rows in LDS, columns as wave-uniform values.
+template <int TILE>
+struct CentredOffsets {
+  float cy, cx, ty, tx;
+  float lx[TILE];
+};
+
+// Two forms of the per-pair sums over whole rows of the tile (lane = pair). Offsets are taken from the tile
+// centre: u = uc + A ly + B lx and v = vc + Cc ly + D lx with (ly, lx) the centred offsets.
+//  * direct: per pixel u and v (one fma each from the row terms) and the five moments of q in (u, v),
+//    eight operations;
+//  * moments: offsets (ly', lx') from the pair's own centre (the splat centre clamped to the tile); per pixel
+//    m = u^2 + v^2 as a quadratic in lx' with per-row coefficients (no u or v) and three row sums
+//    (q, q lx', q lx'^2); each row folds its sums into the six moments of q in (ly', lx'), which map onto
+//    sum q u, ..., sum q u v once per pair since u, v are linear in (ly', lx'). Four fewer operations per
+//    pixel.
+// The moment form evaluates sum q u^2 as up^2 sum q + 2 up sum q du + sum q du^2 (up = u at the pair's
+// centre, du = u - up): the terms cancel where q sits away from that centre, and the rounding error grows
+// with the pair's whitened span over the tile, max |du|. Centred on the splat, the error relative to the
+// splat's own sums stays below 1e-5 up to a span of 8 in float32 experiments (4x4 to 16x16 tiles), and
+// reaches 1e-4 and more for splats far smaller than a pixel (spans of 20 to 60). Pairs with a span above
+// kMomentSpan take the direct form.
+constexpr float kMomentSpan = 8.f;
+
+template <int TILE>
+__device__ __forceinline__ bool moment_span_ok(const PairGeo& g, const CentredOffsets<TILE>& co) {
+  return fmaxf(fmaf(fabsf(g.A), co.cy, fabsf(g.B) * co.cx), fmaf(fabsf(g.Cc), co.cy, fabsf(g.D) * co.cx)) <=
+         kMomentSpan;
+}
+
+// Direct form over rows [row0, row0 + nrows), with 1 - a = 1 - op f by one fma: the caller has taken every
+// pair that may be near-opaque in the tile (near_possible) out of the wave's lanes.
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ void pair_rows(const PairGeo& g, float op, const float4& col, int row0, int nrows,
-                                          const float* s_ly, const float* lxs, const float4* s_pa, const float4* s_pb,
-                                          PairSums<C>& s) {
+__device__ __forceinline__ void pair_rows_direct(const PairGeo& g, float op, const float4& col, int row0, int nrows,
+                                                 const float* s_lyc, const CentredOffsets<TILE>& co,
+                                                 const float4* s_pa, const float4* s_pb, PairSums<C>& s) {
+  const float uc = fmaf(g.B, co.cx, fmaf(g.A, co.cy, g.u0));
+  const float vc = fmaf(g.D, co.cx, fmaf(g.Cc, co.cy, g.v0));
 #pragma nounroll
   for (int yy = row0; yy < row0 + nrows; ++yy) {
-    const float ly = s_ly[yy];
-    const float uy = fmaf(g.A, ly, g.u0), vy = fmaf(g.Cc, ly, g.v0);
+    const float ly = s_lyc[yy];
+    const float uy = fmaf(g.A, ly, uc), vy = fmaf(g.Cc, ly, vc);
     const float4* pa_row = s_pa + yy * up_stride<TILE>();
     const float4* pb_row = s_pb + yy * up_stride<TILE>();
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
       const float4 pa = pa_row[xx];
       const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float u = fmaf(g.B, lxs[xx], uy), v = fmaf(g.D, lxs[xx], vy);
+      const float u = fmaf(g.B, co.lx[xx], uy), v = fmaf(g.D, co.lx[xx], vy);
       const float f = hw_exp2(-fmaf(u, u, v * v));
       bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, pa, pb, s);
     }
   }
+}
+
+// Moment form over rows [row0, row0 + nrows) for pairs with moment_span_ok (and not near-opaque); (gy, gx) is
+// the splat centre.
+template <int C, bool ODDS, int TILE>
+__device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, float gx, float op, const float4& col,
+                                                  int row0, int nrows, const float* s_lyc,
+                                                  const CentredOffsets<TILE>& co, const float4* s_pa,
+                                                  const float4* s_pb, PairSums<C>& s) {
+  // the pair's centre (ey, ex), in centred offsets, and u, v there
+  const float ey = fminf(fmaxf(gy - co.ty, -co.cy), co.cy), ex = fminf(fmaxf(gx - co.tx, -co.cx), co.cx);
+  const float up = fmaf(g.B, co.cx + ex, fmaf(g.A, co.cy + ey, g.u0));
+  const float vp = fmaf(g.D, co.cx + ex, fmaf(g.Cc, co.cy + ey, g.v0));
+  // along a row, u = uy + B lx' and v = vy + D lx', so m = (uy^2 + vy^2) + 2 (uy B + vy D) lx' + (B^2 + D^2) lx'^2
+  const float a2 = fmaf(g.B, g.B, g.D * g.D), b2 = 2.f * g.B, d2 = 2.f * g.D;
+  float lxp[TILE];   // the column offsets lx', once per pair
+#pragma unroll
+  for (int xx = 0; xx < TILE; ++xx) lxp[xx] = co.lx[xx] - ex;
+  float m0 = 0.f, my = 0.f, myy = 0.f, mx = 0.f, mxy = 0.f, mxx = 0.f;   // sum q {1, ly', ly'^2, lx', lx' ly', lx'^2}
+#pragma nounroll
+  for (int yy = row0; yy < row0 + nrows; ++yy) {
+    const float ly = s_lyc[yy] - ey;
+    const float uy = fmaf(g.A, ly, up), vy = fmaf(g.Cc, ly, vp);
+    const float a0 = fmaf(uy, uy, vy * vy), a1 = fmaf(uy, b2, vy * d2);
+    const float4* pa_row = s_pa + yy * up_stride<TILE>();
+    const float4* pb_row = s_pb + yy * up_stride<TILE>();
+    float r0 = 0.f, r1 = 0.f, r2 = 0.f;
+#pragma unroll
+    for (int xx = 0; xx < TILE; ++xx) {
+      const float4 pa = pa_row[xx];
+      const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float lx = lxp[xx];
+      const float f = hw_exp2(-fmaf(fmaf(a2, lx, a1), lx, a0));
+      const float q = bwd_q<C, ODDS>(f, fmaf(-op, f, 1.f), col, pa, pb, s.gc);
+      const float ql = q * lx;
+      r0 += q;
+      r1 += ql;
+      r2 = fmaf(ql, lx, r2);
+    }
+    m0 += r0;
+    my = fmaf(ly, r0, my);
+    myy = fmaf(ly * ly, r0, myy);
+    mx += r1;
+    mxy = fmaf(ly, r1, mxy);
+    mxx += r2;
+  }
+  // with du = u - up = A ly' + B lx' and dv = v - vp = Cc ly' + D lx':
+  const float su = fmaf(g.A, my, g.B * mx);                                   // sum q du
+  const float sv = fmaf(g.Cc, my, g.D * mx);                                  // sum q dv
+  const float suu = fmaf(g.A * g.A, myy, fmaf(2.f * g.A * g.B, mxy, g.B * g.B * mxx));
+  const float svv = fmaf(g.Cc * g.Cc, myy, fmaf(2.f * g.Cc * g.D, mxy, g.D * g.D * mxx));
+  const float suv = fmaf(g.A * g.Cc, myy, fmaf(fmaf(g.A, g.D, g.B * g.Cc), mxy, g.B * g.D * mxx));
+  s.q += m0;
+  s.qu += fmaf(up, m0, su);
+  s.qv += fmaf(vp, m0, sv);
+  s.quu += fmaf(up, fmaf(up, m0, 2.f * su), suu);
+  s.qvv += fmaf(vp, fmaf(vp, m0, 2.f * sv), svv);
+  s.quv += fmaf(up, fmaf(vp, m0, sv), fmaf(vp, su, suv));
 }
 
 // Per-pair sums over the pixels [j0, j0 + npx) of one row of the tile (lane = pair, lane-varying j0): the
@@ -607,7 +701,8 @@ __device__ __forceinline__ void pair_row_part(const PairGeo& g, float op, const 
 
 // Sums of pair g (wave-uniform) over the tile's pixels with lane = pixel and 1 - a evaluated carefully at
 // every pixel (bwd_px_near), reduced over the wave: every lane returns the totals. For the pairs taken out
-// of the lane-per-pair loops (a few near-opaque splats around their centre tile).
+// of the lane-per-pair loops (a few near-opaque splats around their centre tile, and splats far smaller than
+// the tile).
 template <int C, bool ODDS, int TILE>
 __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, float py0, float px0,
                                                     const float* s_ly, const float* s_lx, const float4* s_pa,
@@ -636,12 +731,13 @@ __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ re
 // Composite (level 0): upstream from T/asum/fg/gout (see pixel_upstream for UPS); per-tile partials of
 // sum_p gout * T go to bg_part[c * ntiles + (t - tb0)]. FIELDS: upstream from the packed fields.
 // One wave per tile: the per-pixel upstream terms are staged in LDS, then the wave takes the tile's pairs
-// 64 at a time (lane = pair). The last r < 64 pairs get L lanes each (the largest power of two with
-// r L <= 64), each lane covering a 1/L share of the tile's pixels (whole rows when that share is at least a
-// row) and the L partial sums are combined with xor shuffles. At 6 waves per SIMD (at most 80 VGPRs) there
-// are enough waves to cover the latency of the VALU, LDS and transcendental pipes.
+// 64 at a time (lane = pair) in the moment form, the pairs that need the direct form in passes of their own.
+// The last r < 64 pairs of a pass get L lanes each (the largest power of two with r L <= 64), each lane
+// covering a 1/L share of the tile's pixels (whole rows when that share is at least a row) and the L partial
+// sums are combined with xor shuffles. At 5 waves per SIMD (at most 96 VGPRs, no spills) there are enough waves
+// to cover the latency of the VALU, LDS and transcendental pipes.
 template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_bwd_cull(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
@@ -652,6 +748,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
   __shared__ float4 s_pa[TILE * RS];
   __shared__ float4 s_pb[TILE * RS];
   __shared__ float s_ly[TILE], s_lx[TILE];
+  __shared__ float s_lyc[TILE];
+  __shared__ int s_defer[128];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
   const int t = ta.t;
@@ -687,67 +785,93 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6))) void k_
     s_lx[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW - px0;
   }
   __syncthreads();
-  float lxs[TILE];
+  CentredOffsets<TILE> co;
+  co.cy = 0.5f * (py1 - py0);
+  co.cx = 0.5f * (px1 - px0);
+  co.ty = py0 + co.cy;
+  co.tx = px0 + co.cx;
 #pragma unroll
-  for (int xx = 0; xx < TILE; ++xx) lxs[xx] = uniform_f(s_lx[xx]);
+  for (int xx = 0; xx < TILE; ++xx) co.lx[xx] = uniform_f(s_lx[xx] - co.cx);
+  if (lane < TILE) {
+    const float ly = s_ly[lane] - co.cy;
+    s_lyc[lane] = ly;
+  }
+  __syncthreads();
   const int g0 = starts[t], g1 = starts[t + 1];
   const int n = g1 - g0;
-  const int nfull = n >> 6;
-  // full chunks: lane = pair, every pixel of the tile
-  for (int k = 0; k < nfull; ++k) {
-    const int i = g0 + 64 * k + lane;
-    const int g = gid[i];
-    const int q = pair_q[i];
-    const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
-    const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-    const float op = r1.z;
-    const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    const bool near = near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
-    PairGeo pg = pair_geo(r0, r1, py0, px0);
-    mute_pair(near, pg);
-    PairSums<C> s;
-    pair_rows<C, ODDS, TILE>(pg, op, col, 0, TILE, s_ly, lxs, s_pa, s_pb, s);
-    if (!near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
-    for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
-      const int j = __builtin_ctzll(nm);
-      float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
-                                                          s_pa, s_pb, lane, opj);
-      if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
-    }
-  }
-  // remainder of r < 64 pairs: L lanes per pair, each lane covering NP / L consecutive pixels; the L partial
-  // sums are combined with xor shuffles.
-  const int r = n & 63;
-  if (r) {
+  // One pass over np <= 64 pairs: Lp lanes per pair (the largest power of two with np Lp <= 64, at most NP),
+  // lane = (pair pr = lane / Lp, share sub = lane % Lp of the tile's pixels: whole rows when that share is at
+  // least a row). The Lp partial sums are combined with xor shuffles; near-opaque pairs are taken out and
+  // summed by careful_pair. MOM: the moment form; whole-row pairs it cannot take (moment_span_ok) are appended
+  // to s_defer for a direct pass.
+  int ndefer = 0;
+  auto pass = [&](int np, auto pair_index, auto mom) {
+    constexpr bool MOM = decltype(mom)::value != 0;
     int Lp = 1;
-    while (r * Lp * 2 <= 64 && Lp * 2 <= NP) Lp <<= 1;
+    while (np * Lp * 2 <= 64 && Lp * 2 <= NP) Lp <<= 1;
     const int pr = lane / Lp, sub = lane % Lp;
-    const bool act = pr < r;
-    const int i = g1 - r + pr;
+    const int npx = NP / Lp;
+    const bool act = pr < np;
+    const int i = act ? pair_index(pr) : 0;
     const int g = act ? gid[i] : 0;
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
     const float op = r1.z;
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    const bool near = act && near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
     PairGeo pg = pair_geo(r0, r1, py0, px0);
-    mute_pair(near || !act, pg);
+    const bool near = act && near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
+    const bool defer = MOM && act && !near && npx >= TILE && !moment_span_ok<TILE>(pg, co);
+    mute_pair(near || defer || !act, pg);
     PairSums<C> s;
-    const int npx = NP / Lp;
-    if (npx >= TILE)   // whole rows (uniform branch)
-      pair_rows<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_ly, lxs, s_pa, s_pb, s);
-    else
+    if (Lp == 1) {   // every row (uniform branch; the loops' bounds are wave-uniform)
+      if (MOM)
+        pair_rows_moments<C, ODDS, TILE>(pg, r0.x, r0.y, op, col, 0, TILE, s_lyc, co, s_pa, s_pb, s);
+      else
+        pair_rows_direct<C, ODDS, TILE>(pg, op, col, 0, TILE, s_lyc, co, s_pa, s_pb, s);
+    } else if (npx >= TILE) {   // whole rows
+      if (MOM)
+        pair_rows_moments<C, ODDS, TILE>(pg, r0.x, r0.y, op, col, sub * (npx / TILE), npx / TILE, s_lyc, co, s_pa,
+                                         s_pb, s);
+      else
+        pair_rows_direct<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_lyc, co, s_pa, s_pb, s);
+    } else {
       pair_row_part<C, ODDS, TILE>(pg, op, col, sub * npx, npx, s_ly, s_lx, s_pa, s_pb, s);
+    }
     for (int d = 1; d < Lp; d <<= 1) xor_reduce<C>(s, d);
     const int q = act ? pair_q[i] : 0;
-    if (act && sub == 0 && !near) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
+    if (act && sub == 0 && !near && !defer) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
     for (unsigned long long nm = __ballot(near && sub == 0); nm; nm &= nm - 1) {
       const int j = __builtin_ctzll(nm);
       float opj;
       const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
                                                           s_pa, s_pb, lane, opj);
       if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
+    }
+    if (MOM) {
+      const unsigned long long dm = __ballot(defer && sub == 0);
+      if (defer && sub == 0) s_defer[ndefer + __popcll(dm & ((1ull << lane) - 1ull))] = i;
+      ndefer += __popcll(dm);
+    }
+  };
+  // The tile's pairs in moment passes of 64; the deferred ones in direct passes of 64 as soon as 64 are
+  // waiting (so at most 127 wait: s_defer[128]), the rest at the end.
+  int done = 0;
+  for (;;) {
+    if (ndefer >= 64 || (done == n && ndefer > 0)) {
+      wave_lds_sync();
+      const int np = min(ndefer, 64);
+      pass(np, [&](int pr) { return s_defer[pr]; }, IC<0>{});
+      const int rest = ndefer - np;
+      const int moved = lane < rest ? s_defer[np + lane] : 0;
+      wave_lds_sync();
+      if (lane < rest) s_defer[lane] = moved;
+      ndefer = rest;
+    } else if (done < n) {
+      const int np = min(n - done, 64);
+      pass(np, [&](int pr) { return g0 + done + pr; }, IC<1>{});
+      done += np;
+    } else {
+      break;
     }
   }
 }
