@@ -573,6 +573,25 @@ struct CentredOffsets {
   float lx[TILE];
 };
 
+// Pairs whose op * falloff stays below 2^-kCullLog2 (about 1e-9) at every pixel centre of the tile add nothing
+// the backward keeps: their sums would change a splat's gradients by about 1e-9 of their size (the splat's
+// own tiles near its centre carry falloffs near 1). They get a zero record and no lanes of the row loops. At
+// the 768 x 768 benchmark about a tenth of the pairs qualify, mostly elongated splats' tiles across their
+// narrow axis. The test is a lower bound of m = u^2 + v^2 over the box of the tile's pixel centres: u and v are
+// linear in the pixel offsets, so over the box each lies in an interval given by the corners, and
+// m >= dist(0, u-interval)^2 + dist(0, v-interval)^2.
+constexpr float kCullLog2 = 30.f;
+
+// Lower bound of u^2 + v^2 over ly in [0, Ly], lx in [0, Lx] with u = u0 + A ly + B lx, v = v0 + Cc ly + D lx.
+__device__ __forceinline__ float box_min_m(float u0, float v0, float A, float B, float Cc, float D, float Ly,
+                                           float Lx) {
+  const float ua = A * Ly, ub = B * Lx, va = Cc * Ly, vb = D * Lx;
+  const float ulo = u0 + fminf(ua, 0.f) + fminf(ub, 0.f), uhi = u0 + fmaxf(ua, 0.f) + fmaxf(ub, 0.f);
+  const float vlo = v0 + fminf(va, 0.f) + fminf(vb, 0.f), vhi = v0 + fmaxf(va, 0.f) + fmaxf(vb, 0.f);
+  const float du = fmaxf(fmaxf(ulo, -uhi), 0.f), dv = fmaxf(fmaxf(vlo, -vhi), 0.f);
+  return fmaf(du, du, dv * dv);
+}
+
 // Two forms of the per-pair sums over whole rows of the tile (lane = pair). Offsets are taken from the tile
 // centre: u = uc + A ly + B lx and v = vc + Cc ly + D lx with (ly, lx) the centred offsets.
 //  * direct: per pixel u and v (one fma each from the row terms) and the five moments of q in (u, v),
@@ -749,7 +768,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   __shared__ float4 s_pb[TILE * RS];
   __shared__ float s_ly[TILE], s_lx[TILE];
   __shared__ float s_lyc[TILE];
-  __shared__ int s_defer[128];
+  __shared__ int s_defer[128], s_mi[128];
+  __shared__ float2 s_muv[128];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
   const int t = ta.t;
@@ -798,30 +818,68 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   }
   __syncthreads();
   const int g0 = starts[t], g1 = starts[t + 1];
-  const int n = g1 - g0;
-  // One pass over np <= 64 pairs: Lp lanes per pair (the largest power of two with np Lp <= 64, at most NP),
-  // lane = (pair pr = lane / Lp, share sub = lane % Lp of the tile's pixels: whole rows when that share is at
-  // least a row). The Lp partial sums are combined with xor shuffles; near-opaque pairs are taken out and
-  // summed by careful_pair. MOM: the moment form; whole-row pairs it cannot take (moment_span_ok) are appended
-  // to s_defer for a direct pass.
-  int ndefer = 0;
-  auto pass = [&](int np, auto pair_index, auto mom) {
+  const unsigned long long below = (1ull << lane) - 1ull;
+  // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (op * falloff below
+  // 2^-kCullLog2 at every pixel centre: a zero record), near-opaque (summed by careful_pair at once), small
+  // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi / s_muv with
+  // their offsets at the tile origin, for a moment pass). Only queued pairs occupy lanes of the row loops.
+  int nmain = 0, ndefer = 0;
+  auto classify = [&](int c0) {
+    const int i = c0 + lane;
+    const bool act = i < g1;
+    const int g = act ? gid[i] : 0;
+    const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
+    const float4 r0 = r4[0], r1 = r4[1];
+    const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
+    const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
+    const PairGeo pg{uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
+    const bool negl = act && r1.w - box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) < -kCullLog2;
+    const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
+    const bool defer = act && !negl && !near && !moment_span_ok<TILE>(pg, co);
+    const bool mom = act && !negl && !near && !defer;
+    const int q = (negl || near) ? pair_q[i] : 0;
+    if (negl) store_pair<C>(psum + (size_t)q * pair_rec<C>(), PairSums<C>(), 1.f);
+    for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
+      const int j = __builtin_ctzll(nm);
+      float opj;
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
+                                                          s_pa, s_pb, lane, opj);
+      if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
+    }
+    const unsigned long long dm = __ballot(defer), mm = __ballot(mom);
+    if (defer) s_defer[ndefer + __popcll(dm & below)] = i;
+    if (mom) {
+      const int k = nmain + __popcll(mm & below);
+      s_mi[k] = i;
+      s_muv[k] = uv;
+    }
+    ndefer += __popcll(dm);
+    nmain += __popcll(mm);
+  };
+  // One pass over np <= 64 queued pairs: Lp lanes per pair (the largest power of two with np Lp <= 64, at most
+  // NP), lane = (pair pr = lane / Lp, share sub = lane % Lp of the tile's pixels: whole rows when that share is
+  // at least a row); the Lp partial sums are combined with xor shuffles. MOM: the moment form over s_mi / s_muv,
+  // else the direct form over s_defer.
+  auto pass = [&](int np, auto mom) {
     constexpr bool MOM = decltype(mom)::value != 0;
     int Lp = 1;
     while (np * Lp * 2 <= 64 && Lp * 2 <= NP) Lp <<= 1;
     const int pr = lane / Lp, sub = lane % Lp;
     const int npx = NP / Lp;
     const bool act = pr < np;
-    const int i = act ? pair_index(pr) : 0;
+    const int i = act ? (MOM ? s_mi[pr] : s_defer[pr]) : 0;
     const int g = act ? gid[i] : 0;
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
     const float op = r1.z;
-    const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    PairGeo pg = pair_geo(r0, r1, py0, px0);
-    const bool near = act && near_possible(op, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
-    const bool defer = MOM && act && !near && npx >= TILE && !moment_span_ok<TILE>(pg, co);
-    mute_pair(near || defer || !act, pg);
+    PairGeo pg;
+    if (MOM) {
+      const float2 uv = s_muv[act ? pr : 0];
+      pg = {uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
+    } else {
+      pg = pair_geo(r0, r1, py0, px0);
+    }
+    mute_pair(!act, pg);
     PairSums<C> s;
     if (Lp == 1) {   // every row (uniform branch; the loops' bounds are wave-uniform)
       if (MOM)
@@ -838,38 +896,37 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
       pair_row_part<C, ODDS, TILE>(pg, op, col, sub * npx, npx, s_ly, s_lx, s_pa, s_pb, s);
     }
     for (int d = 1; d < Lp; d <<= 1) xor_reduce<C>(s, d);
-    const int q = act ? pair_q[i] : 0;
-    if (act && sub == 0 && !near && !defer) store_pair<C>(psum + (size_t)q * pair_rec<C>(), s, op);
-    for (unsigned long long nm = __ballot(near && sub == 0); nm; nm &= nm - 1) {
-      const int j = __builtin_ctzll(nm);
-      float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
-                                                          s_pa, s_pb, lane, opj);
-      if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
-    }
-    if (MOM) {
-      const unsigned long long dm = __ballot(defer && sub == 0);
-      if (defer && sub == 0) s_defer[ndefer + __popcll(dm & ((1ull << lane) - 1ull))] = i;
-      ndefer += __popcll(dm);
-    }
+    if (act && sub == 0) store_pair<C>(psum + (size_t)pair_q[i] * pair_rec<C>(), s, op);
   };
-  // The tile's pairs in moment passes of 64; the deferred ones in direct passes of 64 as soon as 64 are
-  // waiting (so at most 127 wait: s_defer[128]), the rest at the end.
-  int done = 0;
+  // Queued pairs run in passes of 64 as soon as 64 wait (so at most 127 wait in either queue), the rest once
+  // the tile's pairs are classified; a pass's entries leave the queue and the rest move to its front.
+  int done = g0;
   for (;;) {
-    if (ndefer >= 64 || (done == n && ndefer > 0)) {
+    if (ndefer >= 64 || (done >= g1 && ndefer > 0)) {
       wave_lds_sync();
       const int np = min(ndefer, 64);
-      pass(np, [&](int pr) { return s_defer[pr]; }, IC<0>{});
+      pass(np, IC<0>{});
       const int rest = ndefer - np;
       const int moved = lane < rest ? s_defer[np + lane] : 0;
       wave_lds_sync();
       if (lane < rest) s_defer[lane] = moved;
       ndefer = rest;
-    } else if (done < n) {
-      const int np = min(n - done, 64);
-      pass(np, [&](int pr) { return g0 + done + pr; }, IC<1>{});
-      done += np;
+    } else if (nmain >= 64 || (done >= g1 && nmain > 0)) {
+      wave_lds_sync();
+      const int np = min(nmain, 64);
+      pass(np, IC<1>{});
+      const int rest = nmain - np;
+      const int mi = lane < rest ? s_mi[np + lane] : 0;
+      const float2 muv = lane < rest ? s_muv[np + lane] : make_float2(0.f, 0.f);
+      wave_lds_sync();
+      if (lane < rest) {
+        s_mi[lane] = mi;
+        s_muv[lane] = muv;
+      }
+      nmain = rest;
+    } else if (done < g1) {
+      classify(done);
+      done += 64;
     } else {
       break;
     }
