@@ -5,11 +5,15 @@
 //                    k_scan_sums + k_offsets beyond kFusedScanBlocks blocks
 //   k_scatter_pairs  load-balanced expansion of every splat's rect into (tile, splat) pairs, splat-major
 //                    as the reference generates them (:396-404), fused with the first radix histogram
-//   k_radix_*        stable LSD radix sort on the tile id; the values carried are the splat id and (for
+//   k_radix_*        stable radix passes on the tile id; the values carried are the splat id and (for
 //                    the backward) the pair's splat-major index, which the first pass takes from the pair's
 //                    position: within a tile the splats keep ascending order, the order of the reference's
 //                    stable argsort (:405-407)
-//   k_tile_starts    CSR starts: starts[t] = number of pairs with tile < t (:408)
+//   k_local_sort     tile ids of 10 to 14 bits: one radix pass orders the pairs by super-tile (tile >> lb),
+//                    then a workgroup per super-tile sorts its pairs on the low lb bits and writes the
+//                    super-tile's CSR starts
+//   k_tile_starts    otherwise (LSD passes over the whole id): CSR starts, starts[t] = number of pairs with
+//                    tile < t (:408)
 //
 // This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
 // operation separately (a fused mu*W - r*W changes floor() near tile edges).
@@ -26,6 +30,8 @@ constexpr int kItems = 8;                       // keys per thread in the pair/s
 constexpr int kSortKeys = kBlock * kItems;      // 2048 keys per block
 constexpr int kWaveKeys = kSortKeys / kWaves;   // 512 consecutive keys per wave
 constexpr long long kBadBit = 1LL << 62;        // marks a block holding an empty or inverted rect
+constexpr int kMaxRadixBits = 9;                // radix passes sort on digits of at most 9 bits
+constexpr int kMaxRadix = 1 << kMaxRadixBits;
 
 // ----------------------------------------------------------------------------------------------------
 // decode + level + rect + count. block_sums[blk * kSumCols + 0] = the block's pair count (| kBadBit),
@@ -344,16 +350,16 @@ __device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
 // The block's first splat comes from a cooperative search; when the block holds at most kBlock splats
 // (always at a few pairs per splat or more) their offsets and rects are loaded once, one per thread, into
 // LDS, and the pair loop reads only LDS. Writes keys[p] = tile, pair_splat[p] = splat and the block's
-// histogram of the first radix digit.
+// histogram of the first radix digit, (tile >> shift) & dmask.
 __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict__ rect, const int* __restrict__ offsets,
                                                           int N, LevelTable L, const long long* __restrict__ info,
-                                                          int cap, int dmask, int* __restrict__ keys,
+                                                          int cap, int shift, int dmask, int* __restrict__ keys,
                                                           int* __restrict__ pair_splat, int* __restrict__ hist,
                                                           int nblocks) {
   __shared__ int4 s_own4[kSortKeys / 4];
   __shared__ int4 s_rect[kBlock];
   __shared__ int s_o0[kBlock];
-  __shared__ int s_hist[256];
+  __shared__ int s_hist[kMaxRadix];
   __shared__ int s_w[kWaves];
   int* s_own = reinterpret_cast<int*>(s_own4);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -365,7 +371,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
   }
   const int n_here = min(kSortKeys, tot - p_base);
   const int p_last = p_base + n_here - 1;
-  for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
+  for (int i = threadIdx.x; i <= dmask; i += kBlock) s_hist[i] = 0;
   for (int i = threadIdx.x; i < kSortKeys / 4; i += kBlock) s_own4[i] = make_int4(-1, -1, -1, -1);
   const int glo = block_last_le(offsets, N, p_base, s_w);
   // window of the next kBlock splats: offsets and rect, one per thread
@@ -421,27 +427,39 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
                                                max(loc[4 * k4 + 2], ex), max(loc[4 * k4 + 3], ex));
   }
   __syncthreads();
+  // The histogram adds runs: consecutive lanes with equal digits (a splat's tiles along a rect row) count in
+  // one LDS atomic by the run's first lane.
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const int i = wv * kWaveKeys + j * 64 + lane;
-    if (i >= n_here) continue;
-    const int p = p_base + i;
-    const int g = s_own[i];
-    int k;
-    int4 rc;
-    if (fast) {
-      k = p - s_o0[g - glo];
-      rc = s_rect[g - glo];
-    } else {
-      k = p - offsets[g];
-      rc = rect[g];
+    const bool act = i < n_here;
+    int d = -1;
+    if (act) {
+      const int p = p_base + i;
+      const int g = s_own[i];
+      int k;
+      int4 rc;
+      if (fast) {
+        k = p - s_o0[g - glo];
+        rc = s_rect[g - glo];
+      } else {
+        k = p - offsets[g];
+        rc = rect[g];
+      }
+      const int ky = div_rect(k, rc.z);
+      const int kx = k - ky * rc.z;
+      const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;
+      keys[p] = tile;
+      pair_splat[p] = g;
+      d = (tile >> shift) & dmask;
     }
-    const int ky = div_rect(k, rc.z);
-    const int kx = k - ky * rc.z;
-    const int tile = L.tbase[rc.w] + (rc.y + ky) * L.ntx[rc.w] + rc.x + kx;
-    keys[p] = tile;
-    pair_splat[p] = g;
-    atomicAdd(&s_hist[tile & dmask], 1);
+    const int dprev = __shfl_up(d, 1, 64);
+    const bool brk = !act || lane == 0 || dprev != d;   // a run starts here (inactive lanes: the tail)
+    const unsigned long long bound = __ballot(brk);
+    if (act && brk) {
+      const unsigned long long after = bound & ~((2ull << lane) - 1ull);
+      atomicAdd(&s_hist[d], (after ? __builtin_ctzll(after) : 64) - lane);
+    }
   }
   __syncthreads();
   for (int d = threadIdx.x; d <= dmask; d += kBlock) hist[d * nblocks + blockIdx.x] = s_hist[d];
@@ -450,9 +468,9 @@ __global__ __launch_bounds__(kBlock) void k_scatter_pairs(const int4* __restrict
 __global__ __launch_bounds__(kBlock) void k_radix_hist(const int* __restrict__ keys, const long long* __restrict__ info,
                                                        int cap, int shift, int dmask, int* __restrict__ hist,
                                                        int nblocks) {
-  __shared__ int s_hist[256];
+  __shared__ int s_hist[kMaxRadix];
   const int tot = pair_count(info, cap);
-  for (int i = threadIdx.x; i < 256; i += kBlock) s_hist[i] = 0;
+  for (int i = threadIdx.x; i <= dmask; i += kBlock) s_hist[i] = 0;
   __syncthreads();
   const int p_base = blockIdx.x * kSortKeys;
   int kv[kItems];
@@ -499,6 +517,9 @@ __global__ __launch_bounds__(kBlock) void k_hist_row_scan(int* __restrict__ hist
 // totals) plus the block's offset within the digit (the row-scanned histogram).
 // Values moved with each key: the splat id (vals) and, with q_out set, the pair's splat-major index (q_in, or
 // the key's input position when q_in is null: the first pass reads the splat-major list).
+// DPT digits per thread in the per-digit steps: radix up to 256 DPT (DPT = 2 for 9-bit digits). The keys are
+// loaded first, so their memory round trip overlaps the loads of the digit totals and offsets.
+template <int DPT>
 __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict__ keys_in, const int* __restrict__ vals_in,
                                                           const int* __restrict__ q_in,
                                                           const long long* __restrict__ info, int cap, int shift,
@@ -506,9 +527,10 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
                                                           const int* __restrict__ rowtot, int nblocks,
                                                           int* __restrict__ keys_out, int* __restrict__ vals_out,
                                                           int* __restrict__ q_out) {
-  __shared__ int s_cnt[kWaves][256];
-  __shared__ int s_gbase[256];    // global position of the block's first key with digit d
-  __shared__ int s_lbase[256];    // LDS position of the block's first key with digit d
+  constexpr int MAXR = 256 * DPT;
+  __shared__ int s_cnt[kWaves][MAXR];
+  __shared__ int s_gbase[MAXR];    // global position of the block's first key with digit d
+  __shared__ int s_lbase[MAXR];    // LDS position of the block's first key with digit d
   __shared__ int s_key[kSortKeys];
   __shared__ int s_val[kSortKeys];
   __shared__ int s_q[kSortKeys];
@@ -517,16 +539,6 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int tot = pair_count(info, cap);
   if ((int)blockIdx.x * kSortKeys >= tot) return;   // no keys here (uniform: before any barrier)
-  for (int i = threadIdx.x; i < kWaves * 256; i += kBlock) (&s_cnt[0][0])[i] = 0;
-  {
-    const int d = threadIdx.x;   // kBlock == 256 >= radix
-    const int rt = d <= dmask ? rowtot[d] : 0;
-    int total;
-    const int dstart = block256_excl<false>(rt, s_w, total);
-    if (d <= dmask) s_gbase[d] = dstart + hist_scan[d * nblocks + blockIdx.x];
-  }
-  __syncthreads();
-  const unsigned long long lt = (1ull << lane) - 1ull;
   const int p_base = blockIdx.x * kSortKeys;
   const int n_here = min(kSortKeys, tot - p_base);
   const int p0 = p_base + wv * kWaveKeys + lane;
@@ -539,6 +551,28 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     val[j] = act ? vals_in[p] : 0;
     qv[j] = q_out ? (q_in ? (act ? q_in[p] : 0) : p) : 0;
   }
+  for (int i = threadIdx.x; i < kWaves * MAXR; i += kBlock) (&s_cnt[0][0])[i] = 0;
+  {
+    // thread t: digits DPT t ... DPT t + DPT - 1
+    int rt[DPT], hs[DPT], sum = 0;
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = DPT * (int)threadIdx.x + k;
+      rt[k] = d <= dmask ? rowtot[d] : 0;
+      hs[k] = d <= dmask ? hist_scan[d * nblocks + blockIdx.x] : 0;
+      sum += rt[k];
+    }
+    int total;
+    int dstart = block256_excl<false>(sum, s_w, total);
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = DPT * (int)threadIdx.x + k;
+      if (d <= dmask) s_gbase[d] = dstart + hs[k];
+      dstart += rt[k];
+    }
+  }
+  __syncthreads();
+  const unsigned long long lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const bool act = p0 + j * 64 < tot;
@@ -557,13 +591,23 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
   __syncthreads();
   {
     // per digit: wave offsets within the block's run of that digit, and the run's LDS start
-    const int d = threadIdx.x;
-    int run = 0;
-    if (d <= dmask)
-      for (int w = 0; w < kWaves; ++w) { const int c = s_cnt[w][d]; s_cnt[w][d] = run; run += c; }
+    int run[DPT], sum = 0;
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = DPT * (int)threadIdx.x + k;
+      run[k] = 0;
+      if (d <= dmask)
+        for (int w = 0; w < kWaves; ++w) { const int c = s_cnt[w][d]; s_cnt[w][d] = run[k]; run[k] += c; }
+      sum += run[k];
+    }
     int total;
-    const int lstart = block256_excl<false>(d <= dmask ? run : 0, s_w, total);
-    if (d <= dmask) s_lbase[d] = lstart;
+    int lstart = block256_excl<false>(sum, s_w, total);
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = DPT * (int)threadIdx.x + k;
+      if (d <= dmask) s_lbase[d] = lstart;
+      lstart += run[k];
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -583,6 +627,161 @@ __global__ __launch_bounds__(kBlock) void k_radix_scatter(const int* __restrict_
     keys_out[pos] = k;
     vals_out[pos] = s_val[i];
     if (q_out) q_out[pos] = s_q[i];
+  }
+}
+
+// Second phase of the two-phase sort: workgroup s takes super-tile s, the tiles [s R, s R + R) with R = 2^lb,
+// whose pairs [sb, se) a radix pass on tile >> lb has put together in splat-major order (sb = sum of rowtot
+// over the super-tiles before s). A stable counting sort on the low lb bits of the tile puts them in (tile,
+// splat) order: gid_sorted / pair_q (when given) at [sb, se), and tile_starts of its tiles (render_triton.py:
+// 405-408). The pairs go in rounds of kLocalKeys: wave w holds 512 consecutive ones (loaded at once) and ranks
+// them 64 at a time, equal digits by ballots on top of its running counts; the waves' counts are scanned per
+// digit in wave order (16 lanes per digit). The round is staged in LDS in (digit, index) order and written
+// out by consecutive threads, so every digit's run of the round lands in consecutive positions. A super-tile
+// of one round takes its digit histogram from the round's counts (its output is then one contiguous run); a
+// larger one counts its digits first (LDS atomics).
+constexpr int kLocalThreads = 1024;
+constexpr int kLocalWaves = kLocalThreads / 64;
+constexpr int kLocalWaveKeys = 512;
+constexpr int kLocalKeys = kLocalWaves * kLocalWaveKeys;
+constexpr int kLocalMaxBits = 5;
+
+__global__ __launch_bounds__(kLocalThreads) void k_local_sort(const int* __restrict__ keys, const int* __restrict__ vals,
+                                                              const int* __restrict__ q_in,
+                                                              const long long* __restrict__ info, int cap, int lb,
+                                                              int nt, int nsuper, const int* __restrict__ rowtot,
+                                                              int* __restrict__ gid_sorted, int* __restrict__ pair_q,
+                                                              int* __restrict__ tile_starts) {
+  constexpr int RM = 1 << kLocalMaxBits;
+  constexpr int J = kLocalWaveKeys / 64;
+  static_assert(kLocalWaves == 16 && RM * kLocalWaves <= kLocalThreads, "digit scan layout");
+  __shared__ int s_part[kLocalWaves];
+  __shared__ int s_dig[RM];    // start of digit d within the super-tile, plus its pairs in earlier rounds
+  __shared__ int s_rt[RM];     // the round's pairs of digit d
+  __shared__ int s_lst[RM];    // LDS start of digit d's run in the round
+  __shared__ int s_gb[RM];     // start of the round's digit-d run within the super-tile
+  __shared__ int s_cnt[kLocalWaves][RM];
+  __shared__ int s_g[kLocalKeys];
+  __shared__ int s_q[kLocalKeys];
+  __shared__ unsigned char s_d[kLocalKeys];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int s = blockIdx.x;
+  const int R = 1 << lb;
+  const int tot = pair_count(info, cap);
+  // sb = sum of rowtot[0, s) (s < 512 <= kLocalThreads: one load per thread)
+  const int mine = (tot > 0 && (int)threadIdx.x < s) ? rowtot[threadIdx.x] : 0;
+  const int cnt_s = tot > 0 ? rowtot[s] : 0;
+  const int part = wave_sum_i(mine);
+  if (lane == 0) s_part[wv] = part;
+  if (threadIdx.x < RM) s_dig[threadIdx.x] = 0;
+  __syncthreads();
+  int sb = 0;
+#pragma unroll
+  for (int w = 0; w < kLocalWaves; ++w) sb += s_part[w];
+  const int se = sb + cnt_s;
+  const bool one_round = cnt_s <= kLocalKeys;
+  if (s == nsuper - 1 && threadIdx.x == 0) {
+    tile_starts[nt] = tot;
+    if (tot == 0) gid_sorted[0] = 0;   // empty list: gid_sorted = {0} (render_triton.py:392-394)
+  }
+  if (!one_round) {   // the super-tile's digit histogram first, kLocalKeys keys per step
+    for (int rb = sb; rb < se; rb += kLocalKeys) {
+      int kv[J];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int i = rb + j * kLocalThreads + (int)threadIdx.x;
+        kv[j] = i < se ? keys[i] : -1;
+      }
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (kv[j] >= 0) atomicAdd(&s_dig[kv[j] & (R - 1)], 1);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      const int h = lane < RM ? s_dig[lane] : 0;
+      const int ex = wave_incl_scan<int>(h, lane) - h;
+      if (lane < R) {
+        s_dig[lane] = ex;
+        if (s * R + lane < nt) tile_starts[s * R + lane] = sb + ex;
+      }
+    }
+  }
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int rb = sb; rb < se || (one_round && rb == sb); rb += kLocalKeys) {
+    const int i0 = rb + wv * kLocalWaveKeys + lane;
+    const int n_round = min(kLocalKeys, se - rb);
+    int dg[J], rank[J], gv[J], qv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int i = i0 + j * 64;
+      const bool act = i < se;
+      dg[j] = act ? keys[i] & (R - 1) : 0;
+      gv[j] = act ? vals[i] : 0;
+      qv[j] = (act && pair_q) ? q_in[i] : 0;
+    }
+    if (threadIdx.x < kLocalWaves * RM) (&s_cnt[0][0])[threadIdx.x] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const bool act = i0 + j * 64 < se;
+      const int d = dg[j];
+      unsigned long long peers = __ballot(act);
+      for (int b = 0; b < lb; ++b) {
+        const bool bit = (d >> b) & 1;
+        const unsigned long long m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int below = __popcll(peers & lt);
+      const int before = s_cnt[wv][d];
+      if (act && below == 0) s_cnt[wv][d] = before + __popcll(peers);
+      rank[j] = before + below;
+    }
+    __syncthreads();
+    if (threadIdx.x < kLocalWaves * RM) {   // digit d = t / 16, wave w = t % 16: wave offsets in wave order
+      const int d = threadIdx.x >> 4, w = threadIdx.x & 15;
+      const int c = s_cnt[w][d];
+      int inc = c;
+#pragma unroll
+      for (int k = 1; k < 16; k <<= 1) {
+        const int o = __shfl_up(inc, k, 16);
+        if (w >= k) inc += o;
+      }
+      s_cnt[w][d] = inc - c;
+      if (w == 15) s_rt[d] = inc;
+    }
+    __syncthreads();
+    if (wv == 0) {   // lane d: LDS start of the digit's run, its place in the super-tile
+      const int d = lane;
+      const int rt = d < R ? s_rt[d] : 0;
+      const int lst = wave_incl_scan<int>(rt, lane) - rt;
+      if (d < R) {
+        if (one_round) {   // the round is the whole super-tile: its counts are the histogram
+          s_dig[d] = lst;
+          if (s * R + d < nt) tile_starts[s * R + d] = sb + lst;
+        }
+        s_lst[d] = lst;
+        s_gb[d] = s_dig[d];
+        s_dig[d] += rt;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (i0 + j * 64 >= se) continue;
+      const int d = dg[j];
+      const int lpos = s_lst[d] + s_cnt[wv][d] + rank[j];
+      s_g[lpos] = gv[j];
+      s_q[lpos] = qv[j];
+      s_d[lpos] = (unsigned char)d;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_round; i += kLocalThreads) {
+      const int d = s_d[i];
+      const int pos = sb + s_gb[d] + (i - s_lst[d]);
+      gid_sorted[pos] = s_g[i];
+      if (pair_q) pair_q[pos] = s_q[i];
+    }
+    __syncthreads();
   }
 }
 
@@ -618,8 +817,15 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Pair-phase workspace: two sets of (keys, splat ids, splat-major indices) that the radix passes ping-pong
 // between, the per-block digit histograms and the digit totals.
+// Two sort plans, both stable on the tile id (so splats keep ascending order within a tile):
+//  * two-phase (lb > 0): tile ids of 10 to 14 bits; one radix pass on the super-tile tile >> lb (9 bits), then
+//    k_local_sort orders every super-tile's pairs on the low lb bits and writes the tile starts. Taken while
+//    the super-tiles average at most kLocalAvgMax pairs (one workgroup sorts each);
+//  * LSD (lb = 0): ceil(bits / 9) radix passes of equal digits, then k_tile_starts.
+constexpr long long kLocalAvgMax = 16384;
+
 struct PairsPlan {
-  int nblk, passes, dbits, radix;
+  int nblk, passes, dbits, radix, lb, nsuper;
   size_t off_set[2][3], off_hist, off_rowtot, total;
 };
 
@@ -628,15 +834,29 @@ static PairsPlan plan_pairs(int nt, long long tot) {
   p.nblk = tot > 0 ? div_up(tot, kSortKeys) : 0;
   int nbits = 0;
   while (nt > 1 && (1LL << nbits) < nt) ++nbits;   // bits of the largest tile id nt - 1
-  p.passes = nbits > 8 ? (nbits + 7) / 8 : 1;      // at least one pass: it also moves the values into place
-  p.dbits = nbits > 0 ? (nbits + p.passes - 1) / p.passes : 1;
+  const int lb = nbits - kMaxRadixBits;
+  if (lb >= 1 && lb <= kLocalMaxBits) {
+    const long long nsuper = ((long long)(nt - 1) >> lb) + 1;
+    if (tot <= nsuper * kLocalAvgMax) {
+      p.lb = lb;
+      p.nsuper = (int)nsuper;
+    }
+  }
+  if (p.lb > 0) {
+    p.passes = 1;
+    p.dbits = kMaxRadixBits;
+  } else {
+    // at least one pass: it also moves the values into place
+    p.passes = nbits > kMaxRadixBits ? (nbits + kMaxRadixBits - 1) / kMaxRadixBits : 1;
+    p.dbits = nbits > 0 ? (nbits + p.passes - 1) / p.passes : 1;
+  }
   p.radix = 1 << p.dbits;
   const long long nh = (long long)p.radix * p.nblk;
   size_t o = 0;
   for (int s = 0; s < 2; ++s)
     for (int k = 0; k < 3; ++k) { p.off_set[s][k] = o; o += align256(sizeof(int) * (size_t)tot); }
   p.off_hist = o;   o += align256(sizeof(int) * (size_t)(nh > 0 ? nh : 1));
-  p.off_rowtot = o; o += align256(sizeof(int) * 256);
+  p.off_rowtot = o; o += align256(sizeof(int) * kMaxRadix);
   p.total = o;
   return p;
 }
@@ -737,8 +957,9 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
   const bool maps = pair_q != nullptr;
   int* psplat = pair_splat ? pair_splat : S[1][1];
   const int dmask = pl.radix - 1;
-  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, dmask,
-                                              S[1][0], psplat, hist, pl.nblk);
+  const bool two_phase = pl.lb > 0;
+  k_scatter_pairs<<<pl.nblk, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, pl.lb,
+                                              dmask, S[1][0], psplat, hist, pl.nblk);
   int rc = check_launch("k_scatter_pairs");
   if (rc) return rc;
   const int* kin = S[1][0];
@@ -746,22 +967,31 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
   const int* qin = nullptr;
   int* kfin = nullptr;
   for (int pass = 0; pass < pl.passes; ++pass) {
-    const int shift = pass * pl.dbits;
-    const bool last = pass == pl.passes - 1;
+    const int shift = two_phase ? pl.lb : pass * pl.dbits;
+    const bool last = pass == pl.passes - 1 && !two_phase;   // writes the final gid_sorted / pair_q
     int* const* D = S[pass & 1];
     int* kout = D[0];
     int* vout = last ? gid_sorted : D[1];
     int* qout = maps ? (last ? pair_q : D[2]) : nullptr;
     if (pass > 0) k_radix_hist<<<pl.nblk, kBlock, 0, st>>>(kin, dinfo, t, shift, dmask, hist, pl.nblk);
     k_hist_row_scan<<<pl.radix, kBlock, 0, st>>>(hist, pl.nblk, rowtot);
-    k_radix_scatter<<<pl.nblk, kBlock, 0, st>>>(kin, vin, qin, dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk, kout,
-                                                vout, qout);
+    if (pl.dbits > 8)
+      k_radix_scatter<2><<<pl.nblk, kBlock, 0, st>>>(kin, vin, qin, dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk,
+                                                     kout, vout, qout);
+    else
+      k_radix_scatter<1><<<pl.nblk, kBlock, 0, st>>>(kin, vin, qin, dinfo, t, shift, pl.dbits, hist, rowtot, pl.nblk,
+                                                     kout, vout, qout);
     rc = check_launch("k_radix_scatter");
     if (rc) return rc;
     kin = kout;
     vin = vout;
     qin = qout;
     kfin = kout;
+  }
+  if (two_phase) {
+    k_local_sort<<<pl.nsuper, kLocalThreads, 0, st>>>(kin, vin, qin, dinfo, t, pl.lb, nt, pl.nsuper, rowtot, gid_sorted,
+                                                      maps ? pair_q : nullptr, tile_starts);
+    return check_launch("k_local_sort");
   }
   k_tile_starts<<<div_up(nt + 1, kBlock), kBlock, 0, st>>>(kfin, gid_sorted, dinfo, t, nt, tile_starts);
   return check_launch("k_tile_starts");

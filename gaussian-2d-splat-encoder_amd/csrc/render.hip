@@ -933,31 +933,57 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   }
 }
 
-// Sum of per-tile partials part[c * nparts + i] over i for every channel, by one 256-thread workgroup
-// (fixed order: deterministic). Each thread keeps 8 independent loads in flight per step, so the workgroup
-// finishes in a few memory round trips even for tens of thousands of partials.
+// Sum of per-tile partials part[c * nparts + i] over i for every channel, by one 256-thread workgroup (fixed
+// order: deterministic). The C * nparts floats are read as one flat array, by float4 loads when `part` is
+// 16-byte aligned, 16 loads per thread in flight before any is added: at 9,216 tiles (27,648 floats) that is
+// two memory round trips, short enough to stay hidden behind the splat waves of the same launch.
 template <int C>
 __device__ __forceinline__ void block_bg_sum(const float* __restrict__ part, int nparts, float* __restrict__ g_bg) {
+  constexpr int kU = 16;
   __shared__ float s_w[4][kMaxC];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  float acc[kMaxC][8];
+  const int n = C * nparts;
+  float acc[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+  // adds x (flat index i) to its channel's sum
+  auto add = [&](int i, float x) {
 #pragma unroll
-  for (int c = 0; c < C; ++c)
+    for (int c = 0; c < C; ++c) acc[c] += (i >= c * nparts && i < (c + 1) * nparts) ? x : 0.f;
+  };
+  int done = 0;
+  if ((reinterpret_cast<uintptr_t>(part) & 15) == 0) {
+    const float4* p4 = reinterpret_cast<const float4*>(part);
+    const int n4 = n / 4;
+    for (int j0 = threadIdx.x; j0 < n4; j0 += 256 * kU) {
+      float4 v[kU];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[c][u] = 0.f;
-  for (int i0 = threadIdx.x; i0 < nparts; i0 += 256 * 8) {
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + u * 256;
-        if (i < nparts) acc[c][u] += part[(size_t)c * nparts + i];
+      for (int u = 0; u < kU; ++u) {
+        const int j = j0 + u * 256;
+        v[u] = j < n4 ? p4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = 4 * (j0 + u * 256);
+        add(i, v[u].x);
+        add(i + 1, v[u].y);
+        add(i + 2, v[u].z);
+        add(i + 3, v[u].w);
+      }
+    }
+    done = 4 * n4;
+  }
+  for (int i0 = done + (int)threadIdx.x; i0 < n; i0 += 256 * kU) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = i0 + u * 256;
+      v[u] = i < n ? part[i] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) add(i0 + u * 256, v[u]);
   }
 #pragma unroll
   for (int c = 0; c < C; ++c) {
-    const float x = wave_sum(((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) +
-                             ((acc[c][4] + acc[c][5]) + (acc[c][6] + acc[c][7])));
+    const float x = wave_sum(acc[c]);
     if (lane == 0) s_w[wv][c] = x;
   }
   __syncthreads();

@@ -104,6 +104,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
 // Inclusive prefix sum across the 64 lanes of a wave.
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T v, int lane) {

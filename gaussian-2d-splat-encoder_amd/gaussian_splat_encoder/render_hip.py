@@ -474,7 +474,7 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
 
 def _bwd_buffers(lib, bins, b, C, with_bg, dev):
     """Per-pair sums and (optionally) the level-0 per-tile background partials, one allocation."""
-    ns = lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4
+    ns = (lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4 + 3) & ~3   # partials start 16-byte aligned
     nb = C * bins.ntiles0 if with_bg else 0
     buf = torch.empty(ns + nb, device=dev)
     return buf[:ns], (buf[ns:] if with_bg else None)

@@ -33,11 +33,27 @@ def test_configs_bit_exact(dev, name, TILE):
     (37, 51, 4, 5.0, 300, 0.0),
     (100, 60, 16, 3.0, 2000, 0.1),
     (8, 8, 8, 3.0, 50, 0.5),           # a single tile: no radix pass
-    (2100, 2100, 8, 3.0, 20000, 0.0),  # 69,169 tiles: 17-bit keys, three radix passes
+    (2100, 2100, 8, 3.0, 20000, 0.0),  # 69,169 tiles: 17-bit keys, two 9-bit radix passes
+    (1000, 700, 8, 3.0, 20000, 0.05),  # 11,000 tiles: two-phase sort on a ragged super-tile range
 ])
 def test_edge_cases_bit_exact(dev, H, W, TILE, cutoff, n, margin):
     mu, ls, *_ = random_scene(n, H, W, seed=H + W + n, dev=dev, margin=margin, B=2)
     check_equal(mu, activate_scale(ls), H, W, TILE, cutoff)
+
+
+@pytest.mark.parametrize("H,W,TILE,n,spread", [
+    (256, 256, 8, 12000, 0.02),    # 1,024 tiles (super-tiles of 2): ~12k pairs per super-tile, two rounds
+    (1024, 1024, 8, 8000, 0.01),   # 16,384 tiles (super-tiles of 32): a few dense super-tiles
+    (64, 64, 2, 9000, 0.0),        # 1,024 tiles and ~9.2M pairs: past the two-phase limit, LSD passes
+])
+def test_dense_super_tiles_bit_exact(dev, H, W, TILE, n, spread):
+    """Two-phase sort with super-tiles of more than one round (8,192 pairs) of the local sort, and the
+    fallback to LSD passes when super-tiles would average more than 16,384 pairs."""
+    g = torch.Generator().manual_seed(H + n)
+    mu = (0.5 + spread * torch.randn(1, n, 2, generator=g)).clamp(0.0, 1.0)
+    big = TILE == 2   # splats that cover the whole canvas
+    ls = torch.full((1, n, 2), float(np.log(0.4 if big else 3.0 / H))) + 0.1 * torch.randn(1, n, 2, generator=g)
+    check_equal(mu.to(dev), activate_scale(ls.to(dev)), H, W, TILE, 3.0)
 
 
 def test_near_tile_edges_not_fma_contracted(dev):
