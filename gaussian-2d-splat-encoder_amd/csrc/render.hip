@@ -101,28 +101,39 @@ __device__ __forceinline__ void fwd_tile_pair(const float* __restrict__ r, float
   for (int c = 0; c < C; ++c) sc[c] = fmaf(w, r[R_COL + c], sc[c]);
 }
 
-// Pairs [b0, b1) of one batch (their offsets at the tile origin in s_uv[0, b1 - b0)), four at a time: ids and
-// records through scalar loads, offsets by LDS broadcast, one log2 per group.
+// Pairs [b0, b1) of one batch (their offsets at the tile origin in s_uv[0, b1 - b0)), in groups of four:
+// ids and records through scalar loads, offsets by LDS broadcast. The (1 - a) factors of eight pairs (two
+// groups) are multiplied before one log2: each factor is >= 1e-4, so the product stays >= 1e-32, a normal float.
+template <int C, bool ODDS, bool CLAMP>
+__device__ __forceinline__ void fwd_group4(const float* __restrict__ rec, const int* __restrict__ gid, int i, int j,
+                                           const float2* s_uv, float ly, float lx, float& t, float& s_a, float* sc) {
+  const float* r0 = rec + (size_t)gid[i] * kRec;
+  const float* r1 = rec + (size_t)gid[i + 1] * kRec;
+  const float* r2 = rec + (size_t)gid[i + 2] * kRec;
+  const float* r3 = rec + (size_t)gid[i + 3] * kRec;
+  fwd_tile_pair<C, ODDS, CLAMP>(r0, s_uv[j], ly, lx, t, s_a, sc);
+  fwd_tile_pair<C, ODDS, CLAMP>(r1, s_uv[j + 1], ly, lx, t, s_a, sc);
+  fwd_tile_pair<C, ODDS, CLAMP>(r2, s_uv[j + 2], ly, lx, t, s_a, sc);
+  fwd_tile_pair<C, ODDS, CLAMP>(r3, s_uv[j + 3], ly, lx, t, s_a, sc);
+}
+
 template <int C, bool ODDS, bool CLAMP>
 __device__ __forceinline__ void fwd_batch(const float* __restrict__ rec, const int* __restrict__ gid, int b0, int b1,
                                           const float2* s_uv, float ly, float lx, float& sl, float& s_a, float* sc) {
   int i = b0;
-  for (; i + 4 <= b1; i += 4) {
-    const float* r0 = rec + (size_t)gid[i] * kRec;
-    const float* r1 = rec + (size_t)gid[i + 1] * kRec;
-    const float* r2 = rec + (size_t)gid[i + 2] * kRec;
-    const float* r3 = rec + (size_t)gid[i + 3] * kRec;
-    const int j = i - b0;
+  for (; i + 8 <= b1; i += 8) {
     float t = 1.f;
-    fwd_tile_pair<C, ODDS, CLAMP>(r0, s_uv[j], ly, lx, t, s_a, sc);
-    fwd_tile_pair<C, ODDS, CLAMP>(r1, s_uv[j + 1], ly, lx, t, s_a, sc);
-    fwd_tile_pair<C, ODDS, CLAMP>(r2, s_uv[j + 2], ly, lx, t, s_a, sc);
-    fwd_tile_pair<C, ODDS, CLAMP>(r3, s_uv[j + 3], ly, lx, t, s_a, sc);
+    fwd_group4<C, ODDS, CLAMP>(rec, gid, i, i - b0, s_uv, ly, lx, t, s_a, sc);
+    fwd_group4<C, ODDS, CLAMP>(rec, gid, i + 4, i + 4 - b0, s_uv, ly, lx, t, s_a, sc);
     sl += hw_log2(t);
   }
-  for (; i < b1; ++i) {
+  if (i < b1) {   // at most seven pairs left: one product, one log2
     float t = 1.f;
-    fwd_tile_pair<C, ODDS, CLAMP>(rec + (size_t)gid[i] * kRec, s_uv[i - b0], ly, lx, t, s_a, sc);
+    if (i + 4 <= b1) {
+      fwd_group4<C, ODDS, CLAMP>(rec, gid, i, i - b0, s_uv, ly, lx, t, s_a, sc);
+      i += 4;
+    }
+    for (; i < b1; ++i) fwd_tile_pair<C, ODDS, CLAMP>(rec + (size_t)gid[i] * kRec, s_uv[i - b0], ly, lx, t, s_a, sc);
     sl += hw_log2(t);
   }
 }
@@ -131,8 +142,7 @@ __device__ __forceinline__ void fwd_batch(const float* __restrict__ rec, const i
 // batch lane j computes the offsets (u0, v0) of pair j at the tile origin (py0, px0) into the wave's LDS row
 // s_uv, and a ballot tells whether any pair of the batch can reach the alpha clamp; the pixel loop then reads
 // the offsets by broadcast while the pairs' ids and records come through scalar loads (SGPR operands).
-// S_log is accumulated in log2 units, one log2 per group of four pairs (each (1 - a) factor is >= 1e-4, so
-// the group's product stays a normal float).
+// S_log is accumulated in log2 units, one log2 per eight pairs (see fwd_batch).
 template <int C, bool ODDS>
 __device__ __forceinline__ void fwd_tile_pixel(const float* __restrict__ rec, const int* __restrict__ gid, int i0,
                                                int i1, float py0, float px0, float ly, float lx, float2* s_uv,
@@ -862,10 +872,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   // else the direct form over s_defer.
   auto pass = [&](int np, auto mom) {
     constexpr bool MOM = decltype(mom)::value != 0;
-    int Lp = 1;
-    while (np * Lp * 2 <= 64 && Lp * 2 <= NP) Lp <<= 1;
-    const int pr = lane / Lp, sub = lane % Lp;
-    const int npx = NP / Lp;
+    int lg = 0;   // Lp = 2^lg (shifts, not divisions: Lp is a runtime value)
+    while ((np << (lg + 1)) <= 64 && (2 << lg) <= NP) ++lg;
+    const int Lp = 1 << lg;
+    const int pr = lane >> lg, sub = lane & (Lp - 1);
+    const int npx = NP >> lg;
     const bool act = pr < np;
     const int i = act ? (MOM ? s_mi[pr] : s_defer[pr]) : 0;
     const int g = act ? gid[i] : 0;
