@@ -62,14 +62,17 @@ class KernelTimer:
 
     def __init__(self):
         self.enabled = False
+        self.names = None
         self.events = {}
 
-    def enable(self, on=True):
+    def enable(self, on=True, names=None):
+        """names: the stages to bracket (all when None)."""
         self.enabled = on
+        self.names = None if names is None else set(names)
         self.events = {}
 
     def record(self, name):
-        if not self.enabled:
+        if not self.enabled or (self.names is not None and name not in self.names):
             return None
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
