@@ -64,25 +64,33 @@ class KernelTimer:
         self.enabled = False
         self.names = None
         self.events = {}
+        self._pool = []   # events of earlier brackets, reused (creating one costs more host time than recording)
 
     def enable(self, on=True, names=None):
         """names: the stages to bracket (all when None)."""
         self.enabled = on
         self.names = None if names is None else set(names)
+        self._recycle()
+
+    def _event(self):
+        ev = self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def _recycle(self):
+        for v in self.events.values():
+            for a, b in v:
+                self._pool += [a, b]
         self.events = {}
 
     def record(self, name):
         if not self.enabled or (self.names is not None and name not in self.names):
             return None
-        ev = torch.cuda.Event(enable_timing=True)
-        ev.record()
-        return ev
+        return self._event()
 
     def close(self, name, start):
         if start is not None:
-            end = torch.cuda.Event(enable_timing=True)
-            end.record()
-            self.events.setdefault(name, []).append((start, end))
+            self.events.setdefault(name, []).append((start, self._event()))
 
     def elapsed_ms(self):
         torch.cuda.synchronize()
@@ -450,6 +458,20 @@ def _grads_out(B, N, C, dev, has_th):
             _empty((B, N), dev) if has_th else None)
 
 
+def _grads_bg_out(B, N, C, dev, has_th):
+    """g_mu [B,N,2], g_scale [B,N,2], g_col [B,N,C], g_op [B,N], g_th [B,N] (or None) and g_bg [B,C]: views of one
+    allocation (each a contiguous tensor of its own shape)."""
+    n2, nc, n1 = B * N * 2, B * N * C, B * N
+    sizes = [n2, n2, nc, n1, n1 if has_th else 0, B * C]
+    buf = torch.empty(sum(sizes), device=dev)
+    out, o = [], 0
+    for k in sizes:
+        out.append(buf[o:o + k])
+        o += k
+    return (out[0].view(B, N, 2), out[1].view(B, N, 2), out[2].view(B, N, C), out[3].view(B, N),
+            out[4].view(B, N) if has_th else None, out[5].view(B, C))
+
+
 def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stream):
     """splat_render_bwd for batch b over levels lev = (begin, end); upstream = (bg, T, asum, fg, gout, dslog,
     dsa, dsac) with Nones where unused."""
@@ -496,19 +518,25 @@ def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream, lsc=N
 
 def _backward_cull(grad_out, mu, scale, color, opacity, bg, theta, T, asum, fg, bins, H, W, TILE=8, odds=False,
                    scale_is_log=False):
-    """render_triton.py:723-765: grads for mu, scale, color, opacity, bg, theta (None without theta).
-    scale_is_log: `scale` holds the raw log-scales the binning activated; g_scale is w.r.t. them."""
+    """render_triton.py:723-765: grads for mu, scale, color, opacity, bg, theta (None without theta) from
+    grad_out [B,P,C]. scale_is_log: `scale` holds the raw log-scales the binning activated; g_scale is w.r.t.
+    them."""
     B, N, C = color.shape
-    dev = mu.device
-    grads = _grads_out(B, N, C, dev, theta is not None)
-    g_bg = _empty((B, C), dev)
+    return _backward_cull_raw(grad_out, bg, scale if scale_is_log else None, B, N, C, mu.device, theta is not None,
+                              T, asum, fg, bins, odds)
+
+
+def _backward_cull_raw(grad_out, bg, lsc, B, N, C, dev, has_th, T, asum, fg, bins, odds):
+    """_backward_cull on what it reads: grad_out [B,P,C], bg, the raw log-scales lsc (or None) and shapes."""
+    g_mu, g_scale, g_col, g_op, g_th, g_bg = _grads_bg_out(B, N, C, dev, has_th)
+    grads = (g_mu, g_scale, g_col, g_op, g_th)
     go, bgf = _f32(grad_out), _f32(bg)
+    lsc = _f32(lsc)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
         up = (bgf[b], T[b], asum[b], fg[b], go[b], None, None, None)
-        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream, _f32(scale) if scale_is_log else None)
-    g_mu, g_scale, g_col, g_op, g_th = grads
+        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream, lsc)
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
@@ -566,29 +594,36 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
 class _AlphaRenderCull(torch.autograd.Function):
     """render_triton.py:813-833. Inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds).
     scale_is_log=True: `scale` is the fp32 raw log-scale, activated inside the binning's decode pass, and its
-    gradient is w.r.t. the log-scale (what activate_scale + this Function would give, in one node)."""
+    gradient is w.r.t. the log-scale (what activate_scale + this Function would give, in one node).
+
+    The output is the [B,C,H,W] view of the [B,H*W,C] composite that render_alpha_full_triton returns (:347), made
+    here so that no view nodes follow the Function; the backward reads bg (and the raw log-scales) only, the
+    forward's composite buffers (T, asum, fg) are kept on ctx."""
 
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=False, scale_is_log=False):
+        B, N, C = color.shape
         out, (T, asum, fg), bins = _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=odds,
                                                  with_maps=any(ctx.needs_input_grad[:6]), scale_is_log=scale_is_log)
-        ctx.has_theta = theta is not None
-        ctx.HW = (H, W, TILE)
-        ctx.odds = odds
-        ctx.scale_is_log = scale_is_log
+        ctx.meta = (B, N, C, mu.device, theta is not None, H, W, TILE, odds, scale_is_log)
         ctx.tiles = bins
-        ctx.save_for_backward(mu, scale, color, opacity, bg, theta if theta is not None else mu.new_zeros(1),
-                              T, asum, fg)
-        return out
+        ctx.fwd = (T, asum, fg)
+        if scale_is_log:
+            ctx.save_for_backward(bg, scale)
+        else:
+            ctx.save_for_backward(bg)
+        return out.view(B, H, W, C).permute(0, 3, 1, 2)
 
     @staticmethod
     def backward(ctx, grad_out):
-        mu, scale, color, opacity, bg, theta, T, asum, fg = ctx.saved_tensors
-        H, W, TILE = ctx.HW
-        th = theta if ctx.has_theta else None
-        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_cull(grad_out, mu, scale, color, opacity, bg, th, T, asum,
-                                                                fg, ctx.tiles, H, W, TILE, odds=ctx.odds,
-                                                                scale_is_log=ctx.scale_is_log)
+        B, N, C, dev, has_th, H, W, TILE, odds, scale_is_log = ctx.meta
+        saved = ctx.saved_tensors
+        bg = saved[0]
+        lsc = saved[1] if scale_is_log else None
+        T, asum, fg = ctx.fwd
+        go = grad_out.permute(0, 2, 3, 1).reshape(B, H * W, C)   # a view when the gradient has the image's layout
+        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_cull_raw(go, bg, lsc, B, N, C, dev, has_th, T, asum, fg,
+                                                                    ctx.tiles, odds)
         return g_mu, g_scale, g_col, g_op, g_bg, g_th, None, None, None, None, None, None
 
 
@@ -736,7 +771,7 @@ def render_alpha_full_triton(mu, log_scale, color, opacity, bg, H, W, theta=None
     B, N, C = color.shape
     if cull:
         scale, is_log = _scale_arg(log_scale)
-        out = _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds, is_log)
+        return _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds, is_log)
     else:
         scale = activate_scale(log_scale)
         if odds:

@@ -35,6 +35,7 @@ def test_configs_bit_exact(dev, name, TILE):
     (8, 8, 8, 3.0, 50, 0.5),           # a single tile: no radix pass
     (2100, 2100, 8, 3.0, 20000, 0.0),  # 69,169 tiles: 17-bit keys, two 9-bit radix passes
     (1000, 700, 8, 3.0, 20000, 0.05),  # 11,000 tiles: two-phase sort on a ragged super-tile range
+    (6000, 100, 8, 3.0, 20000, 0.0),   # 9,750 tiles: two-phase sort, super-tiles spanning several tile rows
 ])
 def test_edge_cases_bit_exact(dev, H, W, TILE, cutoff, n, margin):
     mu, ls, *_ = random_scene(n, H, W, seed=H + W + n, dev=dev, margin=margin, B=2)
