@@ -255,8 +255,12 @@ __global__ __launch_bounds__((fwd_threads<TILE, S>())) void k_fwd_cull(
   const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
   const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
   const float px = ((float)xp + 0.5f) / (float)ta.W;
-  const float py0 = ((float)(ta.ty * TILE) + 0.5f) / (float)ta.H;   // the tile's first pixel centre
-  const float px0 = ((float)(ta.tx * TILE) + 0.5f) / (float)ta.W;
+  // the tile's first pixel centre: lane 0's own when every wave starts at the tile's first pixel
+  constexpr bool kLane0First = S > 1 || tile_threads(TILE) == 64;
+  const float py0 = kLane0First ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(py)))
+                                : ((float)(ta.ty * TILE) + 0.5f) / (float)ta.H;
+  const float px0 = kLane0First ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(px)))
+                                : ((float)(ta.tx * TILE) + 0.5f) / (float)ta.W;
   int g0 = starts[ta.t], g1 = starts[ta.t + 1];
   if (S > 1) {
     const int chunk = ((g1 - g0 + S - 1) / S + 3) & ~3;
@@ -666,7 +670,10 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, fl
   float lxp[TILE];   // the column offsets lx', once per pair
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) lxp[xx] = co.lx[xx] - ex;
-  float m0 = 0.f, my = 0.f, myy = 0.f, mx = 0.f, mxy = 0.f, mxx = 0.f;   // sum q {1, ly', ly'^2, lx', lx' ly', lx'^2}
+  // sum q {1, ly', ly'^2, lx' ly'} by rows; sum q {lx', lx'^2} from the column sums cq of q after the rows
+  float m0 = 0.f, my = 0.f, myy = 0.f, mxy = 0.f, cq[TILE];
+#pragma unroll
+  for (int xx = 0; xx < TILE; ++xx) cq[xx] = 0.f;
 #pragma nounroll
   for (int yy = row0; yy < row0 + nrows; ++yy) {
     const float ly = s_lyc[yy] - ey;
@@ -674,7 +681,7 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, fl
     const float a0 = fmaf(uy, uy, vy * vy), a1 = fmaf(uy, b2, vy * d2);
     const float4* pa_row = s_pa + yy * up_stride<TILE>();
     const float4* pb_row = s_pb + yy * up_stride<TILE>();
-    float r0 = 0.f, r1 = 0.f, r2 = 0.f;
+    float r0 = 0.f, r1 = 0.f;
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
       const float4 pa = pa_row[xx];
@@ -682,17 +689,21 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, fl
       const float lx = lxp[xx];
       const float f = hw_exp2(-fmaf(fmaf(a2, lx, a1), lx, a0));
       const float q = bwd_q<C, ODDS>(f, fmaf(-op, f, 1.f), col, pa, pb, s.gc);
-      const float ql = q * lx;
       r0 += q;
-      r1 += ql;
-      r2 = fmaf(ql, lx, r2);
+      cq[xx] += q;
+      r1 = fmaf(q, lx, r1);
     }
     m0 += r0;
     my = fmaf(ly, r0, my);
     myy = fmaf(ly * ly, r0, myy);
-    mx += r1;
     mxy = fmaf(ly, r1, mxy);
-    mxx += r2;
+  }
+  float mx = 0.f, mxx = 0.f;
+#pragma unroll
+  for (int xx = 0; xx < TILE; ++xx) {
+    const float t = cq[xx] * lxp[xx];
+    mx += t;
+    mxx = fmaf(t, lxp[xx], mxx);
   }
   // with du = u - up = A ly' + B lx' and dv = v - vp = Cc ly' + D lx':
   const float su = fmaf(g.A, my, g.B * mx);                                   // sum q du
