@@ -1,7 +1,8 @@
 // Splat -> tile binning on gfx950, bit-exact with render_triton.py:351-409 (`_build_tiles`):
 //   k_decode_count   one coalesced pass over the splat parameters: the decoded render record, the tile
 //                    rect and the pair count of every splat, and per-block count sums
-//   k_offsets_fused  exclusive scan of the counts into per-splat pair offsets (offsets[N] = tot);
+//   k_offsets_fused  exclusive scan of the counts into per-splat pair offsets (offsets[N] = tot), and the
+//                    totals, also into the caller's pinned host buffer (no copy before the host's one read);
 //                    k_scan_sums + k_offsets beyond kFusedScanBlocks blocks
 //   k_scatter_pairs  load-balanced expansion of every splat's rect into (tile, splat) pairs, splat-major
 //                    as the reference generates them (:396-404), fused with the first radix histogram
@@ -17,8 +18,11 @@
 //
 // This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
 // operation separately (a fused mu*W - r*W changes floor() near tile edges).
+#include <limits.h>
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <atomic>
 
 #include "splat_common.h"
 
@@ -118,10 +122,17 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   if (threadIdx.x < kMaxLevels) block_sums[(size_t)blockIdx.x * kSumCols + 1 + threadIdx.x] = s_lev[threadIdx.x];
 }
 
+// One entry of the count phase's totals, into `info` and, when the caller gave one, into its mirror in pinned
+// host memory (a system-scope store: the host reads it after waiting for an event recorded behind the kernel).
+__device__ __forceinline__ void put_info(long long* info, long long* mirror, int i, long long v) {
+  info[i] = v;
+  if (mirror) __hip_atomic_store(mirror + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Exclusive scan of the per-block count sums in one workgroup. info[0] = total pairs, info[1] = error bits
-// (1: empty/inverted rect, 2: total exceeds int32), info[2 + l] = pairs on level l < nlev.
+// (1: empty/inverted rect, 2: total exceeds int32), info[2 + l] = pairs on level l < nlev (also into mirror).
 __global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums, int n, int nlev,
-                                                    long long* __restrict__ info) {
+                                                    long long* __restrict__ info, long long* __restrict__ mirror) {
   __shared__ long long s_w[16];
   __shared__ long long s_carry;
   __shared__ long long s_bad;
@@ -170,10 +181,11 @@ __global__ __launch_bounds__(1024) void k_scan_sums(long long* __restrict__ sums
   __syncthreads();
   if (threadIdx.x == 0) {
     const long long tot = s_carry;
-    info[0] = tot;
-    info[1] = (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0);
+    put_info(info, mirror, 0, tot);
+    put_info(info, mirror, 1, (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0));
   }
-  if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
+  if (threadIdx.x < nlev) put_info(info, mirror, 2 + threadIdx.x, s_lev[threadIdx.x]);
+  if (mirror) __threadfence_system();
 }
 
 // counts -> exclusive offsets in place; offsets[N] = total. Block prefixes come from k_scan_sums.
@@ -195,12 +207,14 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, c
 
 // counts -> exclusive offsets in place without a separate scan launch (for up to kFusedScanBlocks blocks):
 // every block sums its predecessors' block totals itself (L2-resident, at most a few thousand loads per
-// block). The last block also writes info: total pairs, error bits and the per-level totals (l < nlev).
+// block). The last block also writes info (and its mirror): total pairs, error bits and the per-level totals
+// (l < nlev).
 constexpr int kFusedScanBlocks = 4096;
 
 __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offsets,
                                                           const long long* __restrict__ sums, int N, int nb,
-                                                          int nlev, long long* __restrict__ info) {
+                                                          int nlev, long long* __restrict__ info,
+                                                          long long* __restrict__ mirror) {
   __shared__ long long s_r[kWaves];
   __shared__ long long s_lev[kMaxLevels];
   __shared__ int s_w[kWaves];
@@ -251,10 +265,11 @@ __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offs
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    info[0] = tot;
-    info[1] = (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0);
+    put_info(info, mirror, 0, tot);
+    put_info(info, mirror, 1, (s_bad ? 1 : 0) | (tot > 0x7fffffffLL - 64 ? 2 : 0));
   }
-  if (threadIdx.x < nlev) info[2 + threadIdx.x] = s_lev[threadIdx.x];
+  if (threadIdx.x < nlev) put_info(info, mirror, 2 + threadIdx.x, s_lev[threadIdx.x]);
+  if (mirror) __threadfence_system();
 }
 
 // Pair count of a pair-phase launch. With `info` (a launch queued before the host has read the count,
@@ -912,7 +927,8 @@ namespace {
 // Launches of the count phase (decode + route + count + offsets + info). Arguments already validated.
 int bin_count_launch(const float* mu, const float* scale, const float* theta, const float* opacity,
                      const float* color, int C, int N, const LevelTable& L, const Routing& R, int TILE, float cutoff,
-                     int flags, float* rec, int* rect, int* offsets, long long* info, void* ws, hipStream_t st) {
+                     int flags, float* rec, int* rect, int* offsets, long long* info, long long* mirror, void* ws,
+                     hipStream_t st) {
   const int nb = div_up(N, kBlock);
   long long* sums = (long long*)ws;
 #define SPLAT_DC(CC)                                                                                         \
@@ -924,9 +940,9 @@ int bin_count_launch(const float* mu, const float* scale, const float* theta, co
                case 3: SPLAT_DC(3); break; default: SPLAT_DC(4); break; }
 #undef SPLAT_DC
   if (nb <= kFusedScanBlocks) {
-    k_offsets_fused<<<nb, kBlock, 0, st>>>(offsets, sums, N, nb, L.n, info);
+    k_offsets_fused<<<nb, kBlock, 0, st>>>(offsets, sums, N, nb, L.n, info, mirror);
   } else {
-    k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info);
+    k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info, mirror);
     k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
   }
   return check_launch("splat_bin_count");
@@ -998,6 +1014,22 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
 }
 
 // One event per thread and device, recorded after the read-back of the pair count (splat_bin).
+// Device address of the pinned host buffer `h` (hipHostMalloc), or NULL when `h` is not pinned, or after a
+// mirror write was once found not to have reached the host (the count is then copied).
+constexpr long long kUnsetInfo = LLONG_MIN;   // an info entry not (yet) written
+std::atomic<bool> g_mirror_off{false};
+long long* host_mirror(long long* h) {
+  if (g_mirror_off.load(std::memory_order_relaxed)) return nullptr;
+  hipPointerAttribute_t at{};
+  void* d = nullptr;
+  if (hipPointerGetAttributes(&at, h) != hipSuccess || at.type != hipMemoryTypeHost ||
+      hipHostGetDevicePointer(&d, h, 0) != hipSuccess || !d) {
+    (void)hipGetLastError();   // pageable memory: not an error of the render
+    return nullptr;
+  }
+  return (long long*)d;
+}
+
 hipEvent_t readback_event() {
   static thread_local hipEvent_t ev[64] = {};
   int dev = 0;
@@ -1022,7 +1054,7 @@ int splat_bin_count(const float* mu, const float* scale, const float* theta, con
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
     return set_error(kInvalid, "splat_bin_count: null pointer");
   if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
-  return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets, info,
+  return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets, info, nullptr,
                           ws, (hipStream_t)stream);
 }
 
@@ -1060,12 +1092,20 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
     return set_error(kInvalid, "splat_bin: null pointer");
   if (ws_count_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin: count workspace too small");
   hipStream_t st = (hipStream_t)stream;
+  // the one device -> host read of the render (totals and error bits): the offsets kernel writes them into
+  // info_host itself when it is pinned memory, else they are copied. Entries the kernel has not written keep
+  // the value kUnsetInfo.
+  const int ninfo = 2 + L.n;
+  long long* mirror = host_mirror(info_host);
+  volatile long long* ih = info_host;
+  if (mirror)
+    for (int i = 0; i < ninfo; ++i) ih[i] = kUnsetInfo;
   int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets,
-                            info, ws_count, st);
+                            info, mirror, ws_count, st);
   if (rc) return rc;
-  // the one device -> host read of the render: totals and error bits
   hipEvent_t ev = readback_event();
-  if (!ev || hipMemcpyAsync(info_host, info, sizeof(long long) * (2 + L.n), hipMemcpyDeviceToHost, st) != hipSuccess ||
+  if (!ev ||
+      (!mirror && hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess) ||
       hipEventRecord(ev, st) != hipSuccess)
     return set_error(kHipError, "splat_bin: queueing the read of the pair totals failed");
   // With buffers for pair_cap > 0 pairs the pair phase is queued before the host waits for the count: the GPU
@@ -1078,6 +1118,16 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
     if (rc) return rc;
   }
   if (hipEventSynchronize(ev) != hipSuccess) return set_error(kHipError, "splat_bin: reading the pair totals failed");
+  if (mirror) {
+    bool seen = true;
+    for (int i = 0; i < ninfo; ++i) seen = seen && ih[i] != kUnsetInfo;
+    if (!seen) {   // the kernel's stores did not reach the host: copy from now on
+      g_mirror_off.store(true);
+      if (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return set_error(kHipError, "splat_bin: reading the pair totals failed");
+    }
+  }
   const long long tot = info_host[0];
   if (info_host[1] & 1) return set_error(kInvalid, "splat_bin: a splat has an empty tile rect (negative cutoff or scale)");
   if (info_host[1] & 2) return set_error(kOverflow, "splat_bin: %lld pairs exceed the int32 pair index range", tot);

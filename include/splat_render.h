@@ -95,8 +95,9 @@ int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, in
                     const splat_levels *lv, long long tot, int *gid_sorted, int *tile_starts,
                     int *pair_splat, int *pair_q, void *ws, size_t ws_bytes, void *stream);
 
-/* Binning in one call: phase 1 (splat_bin_count), one read of info into pinned host memory info_host
- * (2 + L int64), then phase 2 (splat_bin_pairs). With pair_cap > 0 (buffers for pair_cap pairs, ws_pairs
+/* Binning in one call: phase 1 (splat_bin_count), one read of info into host memory info_host (2 + L int64),
+ * then phase 2 (splat_bin_pairs). When info_host is pinned (hipHostMalloc) the offsets kernel writes the totals
+ * into it directly; pageable memory gets a copy. With pair_cap > 0 (buffers for pair_cap pairs, ws_pairs
  * sized by splat_bin_pairs_workspace_bytes(N, nt, pair_cap)) phase 2 is queued BEFORE the host waits for
  * the read: its kernels take the pair count from info on the device, so the GPU runs the pair phase while
  * the host checks the count; a count above pair_cap (or an error bit) makes that launch write an empty

@@ -102,6 +102,19 @@ def test_speculative_pair_phase_bit_exact(dev):
         check_equal(mu, sc, 200, 160, 8, 3.0)
 
 
+def test_pageable_count_buffer(dev, monkeypatch):
+    """The pair totals reach the host both ways: written by the offsets kernel into the pinned landing buffer,
+    and copied into pageable memory (hipHostGetDevicePointer refuses it). Same lists either way."""
+    mu, ls, *_ = random_scene(3000, 200, 160, seed=14, dev=dev, B=2)
+    sc = activate_scale(ls)
+    check_equal(mu, sc, 200, 160, 8, 3.0)
+    t = torch.empty(2 + RH._lib.MAX_LEVELS, dtype=torch.int64)
+    assert not t.is_pinned()
+    monkeypatch.setattr(RH, "_info_host", lambda: (t, t.numpy()))
+    check_equal(mu, sc, 200, 160, 8, 3.0)
+    check_equal(mu, sc, 200, 160, 8, 3.0)
+
+
 def test_speculative_capacity_exceeded(dev):
     """A scene with many more pairs than the remembered capacity: the speculative launch leaves an empty
     list, the host sees the count and redoes the pair phase with buffers of the right size."""
