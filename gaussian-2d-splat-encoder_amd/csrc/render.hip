@@ -21,6 +21,8 @@
 // which is the reference's per-pixel chain rule (:697-710) with the per-splat factors taken out of the sums.
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "splat_common.h"
 
 namespace splat {
@@ -1387,6 +1389,36 @@ using namespace splat;
 
 extern "C" {
 
+}  // extern "C"
+
+namespace {
+
+// Events for the next tile-kernel launch of this thread (splat_time_next_launch), or nulls.
+thread_local hipEvent_t g_time_start = nullptr, g_time_stop = nullptr;
+
+// Launch of a forward or backward tile kernel; with events armed by splat_time_next_launch the kernel records
+// them itself at its start and end (hipExtLaunchKernel), and the events are disarmed.
+template <typename... KArgs, typename... Args>
+void launch_tile_kernel(void (*kernel)(KArgs...), unsigned grid, unsigned block, hipStream_t st, Args... args) {
+  if (g_time_start && g_time_stop) {
+    hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, st, g_time_start, g_time_stop, 0, args...);
+    g_time_start = g_time_stop = nullptr;
+  } else {
+    kernel<<<grid, block, 0, st>>>(args...);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int splat_time_next_launch(void* start, void* stop) {
+  const int pending = g_time_start != nullptr;
+  g_time_start = (hipEvent_t)start;
+  g_time_stop = (hipEvent_t)stop;
+  return pending;
+}
+
 int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_starts, int C, int H, int W, int TILE,
                      int flags, const splat_levels* lv, int lev_begin, int lev_end, unsigned levmask, const float* bg,
                      float* out, float* T, float* asum, float* fg, float* slog, float* sa, float* sac, void* stream) {
@@ -1410,12 +1442,12 @@ int splat_render_fwd(const float* rec, const int* gid_sorted, const int* tile_st
         constexpr bool FL = decltype(fl)::value != 0, OD = decltype(od)::value != 0, UP = decltype(up)::value != 0;
         if (TT == 8 && (flags & kFlagWide)) {
           constexpr int S = fwd_split<TT, true>();
-          k_fwd_cull<CC, FL, OD, UP, TT, S><<<ntiles, fwd_threads<TT, S>(), 0, st>>>(
-              rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
+          launch_tile_kernel(k_fwd_cull<CC, FL, OD, UP, TT, S>, ntiles, fwd_threads<TT, S>(), st, rec, gid_sorted,
+                             tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
         } else {
           constexpr int S = fwd_split<TT, false>();
-          k_fwd_cull<CC, FL, OD, UP, TT, S><<<ntiles, fwd_threads<TT, S>(), 0, st>>>(
-              rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
+          launch_tile_kernel(k_fwd_cull<CC, FL, OD, UP, TT, S>, ntiles, fwd_threads<TT, S>(), st, rec, gid_sorted,
+                             tile_starts, L, tb0, ntiles, bg, out, T, asum, fg, slog, sa, sac);
         }
         return check_launch("k_fwd_cull");
       });
@@ -1449,9 +1481,10 @@ int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_st
     return with_tile(TILE, [&](auto tt) {
       return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
-        k_bwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0, decltype(up)::value != 0, TT>
-            <<<ntiles, 64, 0, st>>>(rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa,
-                                    dsac, pair_q, pair_sums, bg_part);
+        launch_tile_kernel(k_bwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0,
+                                      decltype(up)::value != 0, TT>,
+                           ntiles, 64, st, rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, T, asum, fg, gout, dslog,
+                           dsa, dsac, pair_q, pair_sums, bg_part);
         return check_launch("k_bwd_cull");
       });
     });

@@ -44,6 +44,7 @@ _SIGS = {
     "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                        _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_time_next_launch": (_I, [_VP, _VP]),
     "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP, _VP,
                               _VP, _VP, _VP]),
     "splat_pair_sums_bytes": (_SZ, [_LL]),

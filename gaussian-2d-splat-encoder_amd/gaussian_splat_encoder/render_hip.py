@@ -57,8 +57,12 @@ def _ws(nbytes, dev):
 
 
 class KernelTimer:
-    """Optional HIP-event brackets around the per-tile forward and backward calls, recorded on the stream
-    the kernels run on. Enabled by `kernel_timer.enable()`; `elapsed_ms()` syncs and returns per-name lists."""
+    """Optional HIP-event brackets of the render's stages, recorded on the stream the kernels run on. Enabled by
+    `kernel_timer.enable()`; `elapsed_ms()` syncs and returns per-name lists. The tile kernels ("fwd", "bwd")
+    record their events themselves at their own start and end (splat_time_next_launch), so a bracket holds the
+    kernel alone even when the GPU waits for the host's launch; other stages are bracketed on the stream."""
+
+    KERNEL_STAGES = ("fwd", "bwd")
 
     def __init__(self):
         self.enabled = False
@@ -72,8 +76,15 @@ class KernelTimer:
         self.names = None if names is None else set(names)
         self._recycle()
 
+    def _take(self):
+        if self._pool:
+            return self._pool.pop()
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()   # creates the HIP event (torch creates it lazily)
+        return ev
+
     def _event(self):
-        ev = self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
+        ev = self._take()
         ev.record()
         return ev
 
@@ -86,10 +97,21 @@ class KernelTimer:
     def record(self, name):
         if not self.enabled or (self.names is not None and name not in self.names):
             return None
+        if name in self.KERNEL_STAGES:
+            a, b = self._take(), self._take()
+            _lib.load().splat_time_next_launch(a.cuda_event, b.cuda_event)
+            return (a, b)
         return self._event()
 
     def close(self, name, start):
-        if start is not None:
+        if start is None:
+            return
+        if isinstance(start, tuple):
+            if _lib.load().splat_time_next_launch(None, None):   # no launch took the events
+                self._pool += list(start)
+            else:
+                self.events.setdefault(name, []).append(start)
+        else:
             self.events.setdefault(name, []).append((start, self._event()))
 
     def elapsed_ms(self):

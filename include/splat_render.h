@@ -116,6 +116,13 @@ int splat_bin(const float *mu, const float *scale, const float *theta, const flo
               void *ws_count, size_t ws_count_bytes, long long pair_cap, int *gid_sorted, int *tile_starts,
               int *pair_splat, int *pair_q, void *ws_pairs, size_t ws_pairs_bytes, void *stream);
 
+/* Measurement only, no counterpart in the reference: the calling thread's next tile-kernel launch (the
+ * kernel of splat_render_fwd or splat_render_bwd) records the hipEvent_t events start and stop itself, at the
+ * kernel's start and end (hipExtLaunchKernel), so their elapsed time is the kernel's duration without the host's
+ * launch latency. The events are then disarmed; NULL, NULL disarms. Returns 1 when a pair armed earlier had not
+ * been used by a launch, else 0. For benchmarks that bracket the kernels inside render steps. */
+int splat_time_next_launch(void *start, void *stop);
+
 /* Per-tile forward over the binned pairs of levels [lev_begin, lev_end) (TILE in {4, 8, 16}); levels
  * whose bit in levmask is clear are skipped (their pixels are not written).
  * Composite (no FIELDS; levels [0, 1) only): out[P,C], T[P], asum[P], fg[P,C] with background bg[C],

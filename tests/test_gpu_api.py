@@ -202,3 +202,23 @@ def test_scale_activation_in_decode_matches_torch_bits(dev, monkeypatch, kind):
     assert torch.equal(out_f, out_t)
     for n in NAMES:
         assert torch.equal(gd_f[n], gd_t[n]), (n, (gd_f[n] - gd_t[n]).abs().max().item())
+
+
+def test_kernel_timer_brackets(dev):
+    """The tile kernels record the timer's events themselves (splat_time_next_launch): every armed pair is taken
+    by exactly one launch, the brackets are positive and no pair stays armed; the binning is bracketed on the
+    stream."""
+    mu, ls, col, op, bg, th = random_scene(600, 64, 48, seed=21, dev=dev)
+    leaves = [t.clone().requires_grad_(True) for t in (mu, ls, col, op, bg, th)]
+    RH.kernel_timer.enable(True, names=("fwd", "bwd", "bin"))
+    try:
+        for _ in range(3):
+            out = RH.render_alpha_full_triton(*leaves[:5], 64, 48, theta=leaves[5], cull=True)
+            out.backward(torch.ones_like(out))
+        ms = RH.kernel_timer.elapsed_ms()
+    finally:
+        RH.kernel_timer.enable(False)
+    assert sorted(ms) == ["bin", "bwd", "fwd"]
+    for k, v in ms.items():
+        assert len(v) == 3 and all(0.0 < x < 1e3 for x in v), (k, v)
+    assert RH._lib.load().splat_time_next_launch(None, None) == 0
