@@ -10,7 +10,7 @@ fwd+bwd step.
 Also reported: forward-only, the render_alpha_octave entry point, the 2048x2048 stress set
 (configs[4]: fwd and fwd+bwd, single-res and octave), the encoder end-to-end frame (configs[3]: per-stage
 ms), per-stage event times (back-to-back launches), the roofline of the dominant kernel from HIP events
-around its launches in fwd+bwd steps (on the stream it runs on), and
+that its launches record at their own start and end in fwd+bwd steps, and
 the reference's CPU renderer (render.py math) on a bounded band of the same frame, on the host cores.
 """
 
@@ -303,9 +303,9 @@ def main():
 
     # the headline: fwd + bwd, then the other measurements
     ms, wall_ms = time_loop(fwd_bwd, args.steps, args.warmup)
-    # the roofline's launch durations: HIP events (reused from a pool) bracket the forward and backward tile
-    # kernels on the stream they run on, over K more steps of the same loop (kept out of the timed steps: on a
-    # host-bound box their host time would lower `value`)
+    # the roofline's launch durations: the forward and backward tile kernels record HIP events (reused from a
+    # pool) at their own start and end (hipExtLaunchKernel), over K more steps of the same loop (kept out of the
+    # timed steps: on a host-bound box the timer's host time would lower `value`)
     RH.kernel_timer.enable(True, names=("fwd", "bwd"))
     time_loop(fwd_bwd, args.steps, 2)                     # creates the events
     RH.kernel_timer.enable(True, names=("fwd", "bwd"))    # and returns them to the pool for the measured steps
