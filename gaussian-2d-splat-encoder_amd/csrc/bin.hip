@@ -22,7 +22,6 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <atomic>
 
 #include "splat_common.h"
 
@@ -1013,13 +1012,10 @@ int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTabl
   return check_launch("k_tile_starts");
 }
 
-// One event per thread and device, recorded after the read-back of the pair count (splat_bin).
-// Device address of the pinned host buffer `h` (hipHostMalloc), or NULL when `h` is not pinned, or after a
-// mirror write was once found not to have reached the host (the count is then copied).
+// Device address of the pinned host buffer `h` (hipHostMalloc), or NULL when `h` is not pinned (the count is
+// then copied).
 constexpr long long kUnsetInfo = LLONG_MIN;   // an info entry not (yet) written
-std::atomic<bool> g_mirror_off{false};
 long long* host_mirror(long long* h) {
-  if (g_mirror_off.load(std::memory_order_relaxed)) return nullptr;
   hipPointerAttribute_t at{};
   void* d = nullptr;
   if (hipPointerGetAttributes(&at, h) != hipSuccess || at.type != hipMemoryTypeHost ||
@@ -1030,6 +1026,7 @@ long long* host_mirror(long long* h) {
   return (long long*)d;
 }
 
+// One event per thread and device, recorded after the read-back of the pair count (splat_bin).
 hipEvent_t readback_event() {
   static thread_local hipEvent_t ev[64] = {};
   int dev = 0;
@@ -1121,8 +1118,7 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   if (mirror) {
     bool seen = true;
     for (int i = 0; i < ninfo; ++i) seen = seen && ih[i] != kUnsetInfo;
-    if (!seen) {   // the kernel's stores did not reach the host: copy from now on
-      g_mirror_off.store(true);
+    if (!seen) {   // the kernel's stores did not reach the host: this call copies them (the next tries again)
       if (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
           hipStreamSynchronize(st) != hipSuccess)
         return set_error(kHipError, "splat_bin: reading the pair totals failed");

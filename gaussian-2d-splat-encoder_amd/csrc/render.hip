@@ -589,10 +589,12 @@ struct CentredOffsets {
   float lx[TILE];
 };
 
-// Pairs whose op * falloff stays below 2^-kCullLog2 (about 1e-9) at every pixel centre of the tile add nothing
-// the backward keeps: their sums would change a splat's gradients by about 1e-9 of their size (the splat's
-// own tiles near its centre carry falloffs near 1). They get a zero record and no lanes of the row loops. At
-// the 768 x 768 benchmark about a tenth of the pairs qualify, mostly elongated splats' tiles across their
+// Pairs whose falloff stays below 2^-kCullLog2 (about 1e-9) at every pixel centre of the tile add nothing the
+// backward keeps: their sums would change a splat's gradients by about 1e-9 of their size (the splat's own
+// tiles near its centre carry falloffs near 1). They get a zero record and no lanes of the row loops. The test
+// is on the falloff alone, not on op * falloff: the opacity gradient sum da * falloff (render_triton.py:698)
+// carries no opacity factor, so a near-transparent splat's far tiles weigh as much in it as an opaque one's.
+// At the 768 x 768 benchmark about a tenth of the pairs qualify, mostly elongated splats' tiles across their
 // narrow axis. The test is a lower bound of m = u^2 + v^2 over the box of the tile's pixel centres: u and v are
 // linear in the pixel offsets, so over the box each lies in an interval given by the corners, and
 // m >= dist(0, u-interval)^2 + dist(0, v-interval)^2.
@@ -842,7 +844,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   __syncthreads();
   const int g0 = starts[t], g1 = starts[t + 1];
   const unsigned long long below = (1ull << lane) - 1ull;
-  // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (op * falloff below
+  // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (falloff below
   // 2^-kCullLog2 at every pixel centre: a zero record), near-opaque (summed by careful_pair at once), small
   // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi / s_muv with
   // their offsets at the tile origin, for a moment pass). Only queued pairs occupy lanes of the row loops.
@@ -856,7 +858,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
     const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
     const PairGeo pg{uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
-    const bool negl = act && r1.w - box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) < -kCullLog2;
+    const bool negl = act && box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) > kCullLog2;
     const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
     const bool defer = act && !negl && !near && !moment_span_ok<TILE>(pg, co);
     const bool mom = act && !negl && !near && !defer;

@@ -104,6 +104,9 @@ class KernelTimer:
         return self._event()
 
     def close(self, name, start):
+        """Ends a bracket opened by record(). Called in a `finally:` after the stage, so that events armed for a
+        launch that never happened (the stage raised first) are disarmed: the library then holds no handle of
+        events that could be destroyed before its next launch. Unused events go back to the pool."""
         if start is None:
             return
         if isinstance(start, tuple):
@@ -277,10 +280,11 @@ def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, w
     scale_is_log: `scale` holds fp32 raw log-scales, activated in the decode pass (params.py:18-28)."""
     _dev_check(mu, scale, color, opacity, theta)
     ev = kernel_timer.record("bin")
-    bins = _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv,
-                     FLAG_LOG_SCALE if scale_is_log else 0)
-    kernel_timer.close("bin", ev)
-    return bins
+    try:
+        return _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv,
+                         FLAG_LOG_SCALE if scale_is_log else 0)
+    finally:
+        kernel_timer.close("bin", ev)
 
 
 def _budget_error(n, max_pairs, H, W, TILE, cutoff, N):
@@ -416,9 +420,11 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     for b in range(B):
         ev = kernel_timer.record("fwd")
-        _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, bins.tot_b[b]), (0, 1), 1,
-                    (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
-        kernel_timer.close("fwd", ev)
+        try:
+            _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, bins.tot_b[b]), (0, 1), 1,
+                        (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
+        finally:
+            kernel_timer.close("fwd", ev)
     return out, (T, asum, fg), bins
 
 
@@ -461,17 +467,19 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
         mask = bins.level_mask(b)
         lt = bins.level_tot_b[b]
         ev = kernel_timer.record("fwd")
-        if mask & ~1:
-            dense = _dense_levels(bins, lt, mask)
-            light = mask & ~1 & ~sum(1 << l for l in dense)
-            if light:
-                _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5, fl, stream)
-            for l in dense:
-                _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5, fl,
-                            stream)
-        _render_fwd(lib, bins, b, C, FLAG_UPS | odd | _wide(TILE, nt0, lt[0]), (0, 1), mask,
-                    (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
-        kernel_timer.close("fwd", ev)
+        try:
+            if mask & ~1:
+                dense = _dense_levels(bins, lt, mask)
+                light = mask & ~1 & ~sum(1 << l for l in dense)
+                if light:
+                    _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5, fl, stream)
+                for l in dense:
+                    _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5, fl,
+                                stream)
+            _render_fwd(lib, bins, b, C, FLAG_UPS | odd | _wide(TILE, nt0, lt[0]), (0, 1), mask,
+                        (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
+        finally:
+            kernel_timer.close("fwd", ev)
     return out, (T, asum, fg), bins
 
 
@@ -509,14 +517,16 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
     lsc: the fp32 raw log-scales [B,N,2] of a scale_is_log binning; g_scale is then w.r.t. them."""
     tot = bins.tot_b[b]
     N = bins.N
-    ev = kernel_timer.record("reduce")
     g_mu, g_scale, g_col, g_op, g_th = grads
     sl = lambda t: None if (t is None or N == 0) else ptr(t[b])
-    check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
-                                 bins.p(b, "psplat") if tot else None, tot, N, C, ptr(sums), ptr(bg_part),
-                                 bins.ntiles0, sl(lsc), sl(g_mu),
-                                 sl(g_scale), sl(g_th), sl(g_op), sl(g_col), ptr(g_bg), stream), "splat_reduce_pairs")
-    kernel_timer.close("reduce", ev)
+    ev = kernel_timer.record("reduce")
+    try:
+        check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
+                                     bins.p(b, "psplat") if tot else None, tot, N, C, ptr(sums), ptr(bg_part),
+                                     bins.ntiles0, sl(lsc), sl(g_mu), sl(g_scale), sl(g_th), sl(g_op), sl(g_col),
+                                     ptr(g_bg), stream), "splat_reduce_pairs")
+    finally:
+        kernel_timer.close("reduce", ev)
 
 
 def _bwd_buffers(lib, bins, b, C, with_bg, dev):
@@ -533,8 +543,10 @@ def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream, lsc=N
     dev = bins.blocks[b].buf.device
     sums, bg_part = _bwd_buffers(lib, bins, b, C, g_bg is not None, dev)
     ev = kernel_timer.record("bwd")
-    _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
-    kernel_timer.close("bwd", ev)
+    try:
+        _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
+    finally:
+        kernel_timer.close("bwd", ev)
     _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc)
 
 
@@ -601,13 +613,15 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
         mask = bins.level_mask(b)
         sums, bg_part = _bwd_buffers(lib, bins, b, C, True, dev)
         ev = kernel_timer.record("bwd")
-        _render_bwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], T[b], asum[b], fg[b], go[b], *dS), sums,
-                    bg_part, stream)
-        if mask & ~1:
-            check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
-                                             ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
-            _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5 + dS, sums, None, stream)
-        kernel_timer.close("bwd", ev)
+        try:
+            _render_bwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], T[b], asum[b], fg[b], go[b], *dS),
+                        sums, bg_part, stream)
+            if mask & ~1:
+                check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
+                                                 ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
+                _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5 + dS, sums, None, stream)
+        finally:
+            kernel_timer.close("bwd", ev)
         _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream, lsc)
     g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th

@@ -12,8 +12,14 @@
  *                                             fields or composite, alpha or odds weights
  *   orc_bwd_cull  render_triton.py:602-720   cull backward: the reference's per-pair analytic gradient
  *                 render_triton.py:723-810   formulas in float64, summed per splat; g_bg (:764)
+ *
+ * The per-tile loops run on OpenMP threads (tiles are independent; the backward sums per-thread
+ * accumulators in thread order), so full-size frames (2048 x 2048, 31M pairs) check in seconds.
  */
 #include <math.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -115,10 +121,11 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
     for (int i = 0; i < tile_starts[ntx * nty]; ++i) if (gid_sorted[i] + 1 > N) N = gid_sorted[i] + 1;
     orc_splats s = {mu, scale, theta, opacity, color, NULL, NULL};
     trig_tables(&s, N);
-    double acc[16];
-    for (int ty = 0; ty < nty; ++ty)
-        for (int tx = 0; tx < ntx; ++tx) {
-            const int t = ty * ntx + tx;
+    /* tiles are independent: one thread per tile at a time */
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int t = 0; t < ntx * nty; ++t) {
+            const int ty = t / ntx, tx = t % ntx;
+            double acc[16];
             for (int ly = 0; ly < TILE; ++ly)
                 for (int lx = 0; lx < TILE; ++lx) {
                     const int yp = ty * TILE + ly, xp = tx * TILE + lx;
@@ -154,26 +161,41 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
 }
 
 /* Backward over one batch. fields != 0: upstream dS_log[P], dS_a[P], dS_ac[P*C]; else upstream gout[P*C]
- * with the saved T, asum, fg and bg. Per-splat outputs are zeroed here and summed over pairs. */
+ * with the saved T, asum, fg and bg. Per-splat outputs are zeroed here and summed over pairs.
+ * g_op_scale (optional, [N]): the sum over the splat's pixel-pairs of the magnitudes of every term that
+ * enters its opacity gradient, f * (|dS_log u| + (|dS_a| + sum_c |dS_ac[c] col[c]|) u^k) with k = 2 for odds
+ * and 0 for alpha: the scale against which a per-splat relative error of g_op is meaningful.
+ * Tiles run in parallel (OpenMP), each thread into accumulators of its own, summed in thread order. */
+enum { ACC_MU = 0, ACC_SC = 2, ACC_TH = 4, ACC_OP = 5, ACC_OPS = 6, ACC_COL = 7 };
+
 void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const float* opacity,
                   const float* color, int C, int N, const int* gid_sorted, const int* tile_starts, int H,
                   int W, int TILE, int odds, int fields, const float* bg, const double* T,
                   const double* asum, const double* fg, const double* gout, const double* dslog_in,
                   const double* dsa_in, const double* dsac_in, double* g_mu, double* g_scale,
-                  double* g_theta, double* g_op, double* g_col, double* g_bg) {
+                  double* g_theta, double* g_op, double* g_col, double* g_bg, double* g_op_scale) {
     orc_splats s = {mu, scale, theta, opacity, color, NULL, NULL};
     trig_tables(&s, N);
     const int ntx = (W + TILE - 1) / TILE, nty = (H + TILE - 1) / TILE;
-    memset(g_mu, 0, sizeof(double) * 2 * N);
-    memset(g_scale, 0, sizeof(double) * 2 * N);
-    if (g_theta) memset(g_theta, 0, sizeof(double) * N);
-    memset(g_op, 0, sizeof(double) * N);
-    memset(g_col, 0, sizeof(double) * N * C);
-    if (g_bg) memset(g_bg, 0, sizeof(double) * C);
-    double dS_ac[16];
-    for (int ty = 0; ty < nty; ++ty)
-        for (int tx = 0; tx < ntx; ++tx) {
-            const int t = ty * ntx + tx;
+    const int K = ACC_COL + C;
+    int nth = 1;
+#ifdef _OPENMP
+    nth = omp_get_max_threads();
+#endif
+    double* acc = (double*)calloc((size_t)nth * (size_t)(N > 0 ? N : 1) * K, sizeof(double));
+    double* bgacc = (double*)calloc((size_t)nth * 16, sizeof(double));
+#pragma omp parallel num_threads(nth)
+    {
+        int tid = 0;
+#ifdef _OPENMP
+        tid = omp_get_thread_num();
+#endif
+        double* A = acc + (size_t)tid * (size_t)(N > 0 ? N : 1) * K;
+        double* gb = bgacc + (size_t)tid * 16;
+        double dS_ac[16];
+#pragma omp for schedule(dynamic, 4)
+        for (int t = 0; t < ntx * nty; ++t) {
+            const int ty = t / ntx, tx = t % ntx;
             for (int ly = 0; ly < TILE; ++ly)
                 for (int lx = 0; lx < TILE; ++lx) {
                     const int yp = ty * TILE + ly, xp = tx * TILE + lx;
@@ -192,43 +214,76 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
                             dTp += go * ((double)bg[c] - fg[p * C + c]);
                             sfg += dfg * fg[p * C + c];
                             dS_ac[c] = dfg / asum[p];
-                            if (g_bg) g_bg[c] += go * T[p];
+                            gb[c] += go * T[p];
                         }
                         dS_log = dTp * T[p];
                         dS_a = -sfg / asum[p];
                     }
                     for (int i = tile_starts[t]; i < tile_starts[t + 1]; ++i) {
                         const int g = gid_sorted[i];
+                        double* a_g = A + (size_t)g * K;
                         double ry, rx, f, fo, a;
                         splat_alpha(&s, g, py, px, &ry, &rx, &f, &fo, &a);
                         /* render_triton.py:688-710 */
                         const double u = 1.0 / (1.0 - a);
-                        double col_term = 0.0;
-                        for (int c = 0; c < C; ++c) col_term += dS_ac[c] * (double)color[g * C + c];
-                        double da, cw;
-                        if (odds) { da = -dS_log * u + (dS_a + col_term) * u * u; cw = a * u; }
-                        else { da = -dS_log * u + dS_a + col_term; cw = a; }
-                        for (int c = 0; c < C; ++c) g_col[g * C + c] += cw * dS_ac[c];
+                        double col_term = 0.0, col_abs = 0.0;
+                        for (int c = 0; c < C; ++c) {
+                            col_term += dS_ac[c] * (double)color[g * C + c];
+                            col_abs += fabs(dS_ac[c] * (double)color[g * C + c]);
+                        }
+                        double da, cw, mag;
+                        if (odds) {
+                            da = -dS_log * u + (dS_a + col_term) * u * u; cw = a * u;
+                            mag = fabs(dS_log * u) + (fabs(dS_a) + col_abs) * u * u;
+                        } else {
+                            da = -dS_log * u + dS_a + col_term; cw = a;
+                            mag = fabs(dS_log * u) + fabs(dS_a) + col_abs;
+                        }
+                        for (int c = 0; c < C; ++c) a_g[ACC_COL + c] += cw * dS_ac[c];
                         const double da_fo = fo < ORC_CLAMP ? da : 0.0;
                         const double op = (double)opacity[g];
                         const double sy = (double)scale[2 * g], sx = (double)scale[2 * g + 1];
-                        g_op[g] += da_fo * f;
+                        a_g[ACC_OP] += da_fo * f;
+                        if (fo < ORC_CLAMP) a_g[ACC_OPS] += mag * f;
                         const double gm = (da_fo * op) * (-0.5 * f);
-                        g_scale[2 * g + 0] += gm * (-2.0 * ry * ry) / (sy * sy * sy);
-                        g_scale[2 * g + 1] += gm * (-2.0 * rx * rx) / (sx * sx * sx);
+                        a_g[ACC_SC + 0] += gm * (-2.0 * ry * ry) / (sy * sy * sy);
+                        a_g[ACC_SC + 1] += gm * (-2.0 * rx * rx) / (sx * sx * sx);
                         const double gry = gm * 2.0 * ry / (sy * sy), grx = gm * 2.0 * rx / (sx * sx);
                         if (theta) {
                             const double cth = s.cs[g], sth = s.sn[g];
-                            g_theta[g] += gry * rx - grx * ry;
-                            g_mu[2 * g + 0] += -(gry * cth - grx * sth);
-                            g_mu[2 * g + 1] += -(gry * sth + grx * cth);
+                            a_g[ACC_TH] += gry * rx - grx * ry;
+                            a_g[ACC_MU + 0] += -(gry * cth - grx * sth);
+                            a_g[ACC_MU + 1] += -(gry * sth + grx * cth);
                         } else {
-                            g_mu[2 * g + 0] += -gry;
-                            g_mu[2 * g + 1] += -grx;
+                            a_g[ACC_MU + 0] += -gry;
+                            a_g[ACC_MU + 1] += -grx;
                         }
                     }
                 }
         }
+    }
+    for (int g = 0; g < N; ++g) {
+        double v[ACC_COL + 16];
+        for (int k = 0; k < K; ++k) v[k] = 0.0;
+        for (int th = 0; th < nth; ++th) {
+            const double* a_g = acc + ((size_t)th * (size_t)N + (size_t)g) * K;
+            for (int k = 0; k < K; ++k) v[k] += a_g[k];
+        }
+        g_mu[2 * g] = v[ACC_MU]; g_mu[2 * g + 1] = v[ACC_MU + 1];
+        g_scale[2 * g] = v[ACC_SC]; g_scale[2 * g + 1] = v[ACC_SC + 1];
+        if (g_theta) g_theta[g] = v[ACC_TH];
+        g_op[g] = v[ACC_OP];
+        if (g_op_scale) g_op_scale[g] = v[ACC_OPS];
+        for (int c = 0; c < C; ++c) g_col[g * C + c] = v[ACC_COL + c];
+    }
+    if (g_bg)
+        for (int c = 0; c < C; ++c) {
+            double x = 0.0;
+            for (int th = 0; th < nth; ++th) x += bgacc[th * 16 + c];
+            g_bg[c] = x;
+        }
+    free(acc);
+    free(bgacc);
     trig_free(&s);
 }
 

@@ -121,7 +121,8 @@ def test_upsample_adjoint_matches_torch(dev):
 
 def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=3.0):
     """float64 oracle of one batch: C-oracle fields per level, torch float64 glue, C-oracle fields backward.
-    Returns the image [P, C] and the gradients w.r.t. (mu, activated scale, colour, opacity, bg, theta)."""
+    Returns the image [P, C] and the gradients w.r.t. (mu, activated scale, colour, opacity, bg, theta), plus
+    each splat's opacity-gradient scale ("op_scale", see c_oracle.bwd_cull)."""
     mu_, sc_, col_, op_, bg_ = np_(mu), np_(sc), np_(col), np_(op), np_(bg)
     th_ = None if th is None else np_(th)
     N, C = col_.shape
@@ -149,17 +150,20 @@ def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=
     out = R.composite(*S, bg64, straight_through=False)[0]
     (out * torch.from_numpy(np_(gout)).double()).sum().backward()
     grads = {"mu": np.zeros((N, 2)), "scale": np.zeros((N, 2)), "col": np.zeros((N, C)), "op": np.zeros(N),
-             "theta": np.zeros(N) if th is not None else None, "bg": bg64.grad.numpy()}
+             "theta": np.zeros(N) if th is not None else None, "bg": bg64.grad.numpy(), "op_scale": np.zeros(N)}
     for (l, idx, args, gid, st, Hl, Wl), f in zip(per_level, leaves):
         d = [x.grad.numpy() if x.grad is not None else np.zeros(x.shape) for x in f]
         gl = c_oracle.bwd_cull(*args, gid, st, Hl, Wl, TILE, odds=odds, fields=True, dslog=d[0], dsa=d[1], dsac=d[2])
-        for k in ("mu", "scale", "col", "op", "theta"):
+        for k in ("mu", "scale", "col", "op", "theta", "op_scale"):
             if grads[k] is not None:
                 grads[k][idx] = gl[k]
     return out.detach().numpy(), grads
 
 
-def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL):
+def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL,
+               want_grads=False):
+    """Fused level render of one batch against composed_oracle. Returns the bins, and with want_grads also the
+    device gradients by name and the oracle's."""
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
     out, (T, asum, fg), bins = RH._forward_levels(mu, sc, col, op, bg, th, H, W, TILE, 3.0, None, odds, lv)
@@ -175,6 +179,8 @@ def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_
             continue
         e = rel_err(np_(got[0]), gref[name])
         assert e <= grad_tol, f"grad {name}: rel {e:.2e}"
+    if want_grads:
+        return bins, {"mu": g_mu, "scale": g_sc, "col": g_col, "op": g_op, "bg": g_bg, "theta": g_th}, gref
     return bins
 
 

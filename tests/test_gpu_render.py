@@ -17,6 +17,8 @@ def oracle_pairs(mu, sc, H, W, TILE, cutoff=3.0):
 
 
 def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True):
+    """Forward (and backward) of one batch against the C oracle over the oracle's pair list. Returns the
+    device gradients by name and the oracle's (None without the backward)."""
     dev = mu.device
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
@@ -60,6 +62,7 @@ def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bw
         r = gref[name]
         e = rel_err(np_(got[0]), r)
         assert e <= GRAD_REL_TOL, f"{name}: rel {e:.2e}"
+    return dict(zip(names, grads)), gref
 
 
 @pytest.mark.parametrize("odds", [False, True])
