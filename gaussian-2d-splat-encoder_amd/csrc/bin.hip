@@ -19,6 +19,7 @@
 // This file is compiled with -ffp-contract=off: the rect arithmetic below must round every float32
 // operation separately (a fused mu*W - r*W changes floor() near tile edges).
 #include <limits.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -1026,6 +1027,38 @@ long long* host_mirror(long long* h) {
   return (long long*)d;
 }
 
+// Scratch of splat_bin_noalloc: the count and pair-phase workspaces of one binning, in a file-scope device
+// array. Each GPU the library runs on holds its own copy until the process ends. Host code never uses the
+// array's name as an address (in host code it is a host-side stand-in): the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current and kept in g_scratch_dev.
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up on the device's first call), or NULL with the
+// error set.
+void* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(kHipError, "splat_bin_noalloc: no current device (or device %d >= %d)", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error(kHipError, "splat_bin_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_dev[dev] = ptr;
+  }
+  return g_scratch_dev[dev];
+}
+
 // One event per thread and device, recorded after the read-back of the pair count (splat_bin).
 hipEvent_t readback_event() {
   static thread_local hipEvent_t ev[64] = {};
@@ -1138,6 +1171,31 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   if (ws_pairs_bytes < plan_pairs(L.tbase[L.n], tot).total) return set_error(kWorkspace, "splat_bin: pair workspace too small");
   return bin_pairs_launch(rect, offsets, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs,
                           st);
+}
+
+int splat_bin_noalloc(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,
+                      int C, int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, int flags,
+                      long long max_pairs, float* rec, int* rect, int* offsets, long long* info, long long* info_host,
+                      long long pair_cap, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q,
+                      void* stream) {
+  if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1)
+    return set_error(kInvalid, "splat_bin_noalloc: N=%d C=%d H=%d W=%d TILE=%d", N, C, H, W, TILE);
+  if (pair_cap < 1 || pair_cap > 0x7fffffffLL - 64 || !gid_sorted || !tile_starts)
+    return set_error(kInvalid, "splat_bin_noalloc: needs pair buffers (pair_cap=%lld)", pair_cap);
+  LevelTable L;
+  if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_noalloc: bad levels");
+  const size_t cbytes = splat_bin_count_workspace_bytes(N);
+  const size_t pbytes = plan_pairs(L.tbase[L.n], pair_cap).total;
+  if (cbytes + pbytes > kNoAllocScratchBytes)
+    return set_error(kWorkspace,
+                     "splat_bin_noalloc: N=%d splats with pair_cap=%lld need %zu bytes of scratch, above its %zu "
+                     "(about 25 bytes per pair: at most ~2.6M pairs); use splat_bin with a workspace",
+                     N, pair_cap, cbytes + pbytes, kNoAllocScratchBytes);
+  char* ws = (char*)noalloc_scratch();
+  if (!ws) return kHipError;
+  return splat_bin(mu, scale, theta, opacity, color, C, N, H, W, TILE, cutoff, lv, flags, max_pairs, rec, rect,
+                   offsets, info, info_host, ws, cbytes, pair_cap, gid_sorted, tile_starts, pair_splat, pair_q,
+                   ws + cbytes, pbytes, stream);
 }
 
 }  // extern "C"

@@ -44,6 +44,8 @@ _SIGS = {
     "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                        _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_bin_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP,
+                               _LL, _VP, _VP, _VP, _VP, _VP]),
     "splat_time_next_launch": (_I, [_VP, _VP]),
     "splat_render_fwd": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP, _VP,
                               _VP, _VP, _VP]),
@@ -68,6 +70,7 @@ FLAG_WIDE = 8
 FLAG_LOG_SCALE = 16
 MAX_LEVELS = 12   # kMaxLevels of the library
 
+STATUS_WORKSPACE = 5
 STATUS_CAPACITY = 6
 STATUS_BUDGET = 7
 _STATUS = {1: "invalid argument", 2: "HIP error", 3: "unsupported configuration", 4: "overflow",

@@ -1,8 +1,9 @@
 /* C-ABI of the gfx950 tile-binned Gaussian-splat renderer (libsplat_hip.so).
  *
  * Every entry point takes raw device pointers (fp32 / int32, contiguous), sizes and a hipStream_t passed
- * as `void *stream`; all work is enqueued on that stream. No entry point allocates; only splat_bin
- * waits (for the one read-back of the pair totals that sizes the pair buffers and applies the budget).
+ * as `void *stream`; all work is enqueued on that stream. No entry point allocates; only splat_bin and
+ * splat_bin_noalloc wait (for the one read-back of the pair totals that sizes the pair buffers and applies
+ * the budget).
  * Buffers are owned by the caller; scratch memory comes in as (ws, ws_bytes), sized by the matching
  * *_workspace_bytes query. Every call returns 0 on success or a status code, with a message available
  * from splat_last_error() (thread-local):
@@ -115,6 +116,24 @@ int splat_bin(const float *mu, const float *scale, const float *theta, const flo
               int flags, long long max_pairs, float *rec, int *rect, int *offsets, long long *info, long long *info_host,
               void *ws_count, size_t ws_count_bytes, long long pair_cap, int *gid_sorted, int *tile_starts,
               int *pair_splat, int *pair_q, void *ws_pairs, size_t ws_pairs_bytes, void *stream);
+
+/* No counterpart in the reference: splat_bin for callers that cannot allocate device memory (code in tight
+ * serving loops, harnesses that forbid hipMalloc). The same binning as splat_bin with pair_cap > 0, but the
+ * count and pair-phase workspaces live in the library's own device scratch, a static array of 64 MiB per
+ * GPU, held from the library's load until the process ends. The caller still passes every input and output
+ * (rec, rect, offsets, info, info_host and the pair buffers for pair_cap >= 1 pairs). Limit: the workspaces
+ * of N splats and pair_cap pairs must fit the scratch, about 25 bytes per pair (pair_cap up to ~2.6M for
+ * TILE 8 at 768 x 768; the count workspace adds 104 bytes per 256 splats); a larger request returns status 5
+ * before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device (per
+ * thread) looks up the scratch address and creates the read-back event. Statuses as splat_bin. Every call
+ * on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams or threads before the
+ * previous call's kernels have finished) race; calls in one stream do not. Nothing in the scratch needs to
+ * start at zero: every region is written before it is read within a call. */
+int splat_bin_noalloc(const float *mu, const float *scale, const float *theta, const float *opacity,
+                      const float *color, int C, int N, int H, int W, int TILE, float cutoff, const splat_levels *lv,
+                      int flags, long long max_pairs, float *rec, int *rect, int *offsets, long long *info,
+                      long long *info_host, long long pair_cap, int *gid_sorted, int *tile_starts, int *pair_splat,
+                      int *pair_q, void *stream);
 
 /* Measurement only, no counterpart in the reference: the calling thread's next tile-kernel launch (the
  * kernel of splat_render_fwd or splat_render_bwd) records the hipEvent_t events start and stop itself, at the
