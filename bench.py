@@ -9,9 +9,10 @@ fwd+bwd step.
 
 Also reported: forward-only, the render_alpha_octave entry point, the 2048x2048 stress set
 (configs[4]: fwd and fwd+bwd, single-res and octave), the encoder end-to-end frame (configs[3]: per-stage
-ms), per-stage event times (back-to-back launches), the roofline of the dominant kernel from HIP events
-that its launches record at their own start and end in fwd+bwd steps, and
-the reference's CPU renderer (render.py math) on a bounded band of the same frame, on the host cores.
+ms), per-stage event times (back-to-back launches), the device time of the step's kernel chain, per-step
+median / p10 / p90, the roofline of the dominant kernel from HIP events that its launches record at their own
+start and end in fwd+bwd steps, and the reference's CPU renderer (render.py math) on the host cores: a bounded
+band of the same frame, and configs[0] (64x64, 1,024 splats) as BASELINE.md plans it.
 """
 
 from __future__ import annotations
@@ -25,6 +26,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "gaussian-2d-splat-encoder_amd"))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 from gaussian_splat_encoder import render_hip as RH  # noqa: E402
@@ -142,34 +144,127 @@ def kernel_times(leaves, H, W, odds, reps):
         "bwd": span(lambda: RH._render_bwd(lib, bins, 0, C, flags, (0, 1), 1, up, sums, bg_part, stream)),
         "reduce": span(lambda: RH._reduce(lib, bins, 0, C, sums, bg_part, grads, g_bg[0], stream)),
     }
+    # the binning's kernels alone: count phase then pair phase for the known pair count, back to back (no host
+    # read between them), into the frame's own binning buffers
+    lsf = ls.contiguous()
+    N, tot = mu.shape[1], bins.tot_b[0]
+    blk, pb = bins.blocks[0], bins.pairs[0]
+    thp = None if th is None else th.data_ptr()
+
+    def bin_kernels():
+        RH._lib.check(lib.splat_bin_count(mu.data_ptr(), lsf.data_ptr(), thp, op.data_ptr(), col.data_ptr(), C, N, H, W,
+                                          8, 3.0, None, RH.FLAG_LOG_SCALE, blk.ptr(0), blk.ptr(1), blk.ptr(2),
+                                          blk.ptr(3), blk.ptr(4), blk.nbytes(4), stream), "splat_bin_count")
+        RH._lib.check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), N, H, W, 8, None, tot, pb.ptr(0), pb.ptr(1),
+                                          pb.ptr(2), pb.ptr(3), pb.ptr(4), pb.nbytes(4), stream), "splat_bin_pairs")
+
+    ms["bin_kernels"] = span(bin_kernels)
     RH.kernel_timer.enable(True)
     for _ in range(reps):
-        RH._bin(mu, sc, col, op, th, H, W, 8, 3.0)
+        RH._bin(mu, lsf, col, op, th, H, W, 8, 3.0, scale_is_log=True)
     ev = RH.kernel_timer.elapsed_ms()
     RH.kernel_timer.enable(False)
-    ms["bin"] = sum(ev["bin"]) / len(ev["bin"])
+    ms["bin_call"] = sum(ev["bin"]) / len(ev["bin"])
     return ms, bins
 
 
-def cpu_baseline(s, rows=(368, 400), threads=None):
-    """The reference's CPU renderer (render.py:90-110 math, fp32 torch, materialised falloff), restated in
-    oracle/render_ref.py, over a band of rows of the same frame; scaled to a full frame."""
+def step_times(fn, steps, warmup):
+    """Per-step wall times (ms) of `steps` steps, each ended by a device synchronisation: median, p10, p90."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        out.append((time.perf_counter() - t0) * 1e3)
+    return percentiles(out)
+
+
+def percentiles(v):
+    """(median, p10, p90) of a list of times."""
+    a = np.asarray(v, np.float64)
+    return tuple(float(x) for x in np.percentile(a, [50, 10, 90]))
+
+
+def cpu_share():
+    """(CPU model, cores in this process's affinity mask, threads used): the threads are the affinity mask's
+    cores, capped by OMP_NUM_THREADS where the host sets it (the GPU boxes give a process a 16-core share and
+    say so there)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    aff = len(os.sched_getaffinity(0))
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", aff))
+    except ValueError:
+        share = aff
+    return model, aff, max(1, min(aff, share))
+
+
+def cpu_runs(fn, warmup, runs):
+    for _ in range(warmup):
+        fn()
+    out = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        out.append(time.perf_counter() - t0)
+    return out
+
+
+def cpu_baseline(s_c1, band_rows=(368, 372), band_runs=10):
+    """The reference's CPU renderer (render.py:34-110 math: exact, every pixel x every splat, fp32 torch with the
+    falloff materialised in pixel chunks), restated in oracle/render_ref.render_alpha_full_f32, forward only, on
+    the host cores of this box:
+    * the headline workload's frame (768 x 768, 92,160 splats): a band of rows rendered 1 + band_runs times,
+      median scaled to a frame (`value`);
+    * configs[0], the CPU-runnable case (64 x 64, 1,024 splats, seed 0, black background): 3 warm-ups and 20
+      timed runs (`c0`).
+    Times are perf_counter medians with p10 / p90."""
     sys.path.insert(0, ROOT)
     from oracle import render_ref
-    n = threads or min(16, len(os.sched_getaffinity(0)))
+    model, aff, n = cpu_share()
     torch.set_num_threads(n)
-    args = (s.mu, s.log_scale, s.color, s.opacity, s.bg, s.H, s.W)
-    render_ref.render_alpha_full_f32(*args, theta=s.theta, chunk_pixels=256, rows=(rows[0], rows[0] + 1))  # warm
-    t0 = time.perf_counter()
-    render_ref.render_alpha_full_f32(*args, theta=s.theta, chunk_pixels=256, rows=rows)
-    dt = time.perf_counter() - t0
-    frame_s = dt * s.H / (rows[1] - rows[0])
+    c0 = synth.config("c0")
+    P0 = c0.H * c0.W
+
+    def run_c0():
+        render_ref.render_alpha_full_f32(c0.mu, c0.log_scale, c0.color, c0.opacity, c0.bg, c0.H, c0.W,
+                                         theta=c0.theta, chunk_pixels=4096)
+
+    t0s = percentiles(cpu_runs(run_c0, 3, 20))
+    s = s_c1
+    rows = band_rows[1] - band_rows[0]
+
+    def run_band():
+        render_ref.render_alpha_full_f32(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.H, s.W, theta=s.theta,
+                                         chunk_pixels=256, rows=band_rows)
+
+    tb = percentiles(cpu_runs(run_band, 1, band_runs))
+    scale = s.H / rows
+    frame_s = tb[0] * scale
+    ppe_band = rows * s.W * s.n
     return {"value": round(s.H * s.W / 1e6 / frame_s, 6), "unit": "Mpix/s", "cores": n, "kind": "port",
             "ms_per_frame": round(frame_s * 1e3, 1),
-            "sample": f"render.py exact fp32 forward (oracle/render_ref.render_alpha_full_f32, torch CPU, "
-                      f"{n} threads) over rows {rows[0]}-{rows[1] - 1} of the 768x768 / 92,160-splat frame "
-                      f"({(rows[1] - rows[0]) * s.W * s.n / 1e9:.2f} G pixel-pairs, {dt:.1f} s), "
-                      f"scaled to a full frame; forward only"}
+            "ms_per_frame_p10_p90": [round(tb[1] * scale * 1e3, 1), round(tb[2] * scale * 1e3, 1)],
+            "ppe_per_s": round(ppe_band / tb[0], 1),
+            "cpu_model": model, "affinity_cores": aff, "threads": n,
+            "sample": f"render.py exact fp32 forward (oracle/render_ref.render_alpha_full_f32, torch CPU, {n} threads "
+                      f"of {aff} in the affinity mask, {model}) over rows {band_rows[0]}-{band_rows[1] - 1} of the "
+                      f"768x768 / 92,160-splat frame ({ppe_band / 1e9:.3f} G pixel-pairs per run, 1 warm-up + "
+                      f"{band_runs} runs, median scaled to a frame); forward only",
+            "c0": {"workload": "configs[0]: 64x64 RGB, 1,024 splats, seed 0, black background, forward only",
+                   "ms_per_frame": round(t0s[0] * 1e3, 3), "ms_p10": round(t0s[1] * 1e3, 3),
+                   "ms_p90": round(t0s[2] * 1e3, 3), "mpix_s": round(P0 / 1e6 / t0s[0], 4),
+                   "ppe_per_s": round(P0 * c0.n / t0s[0], 1), "runs": "3 warm-ups + 20 timed"}}
 
 
 def stress_c4(steps, warmup, odds):
@@ -312,6 +407,9 @@ def main():
     time_loop(fwd_bwd, args.steps, 0)
     in_step = {k: sum(v[-args.steps:]) / len(v[-args.steps:]) for k, v in RH.kernel_timer.elapsed_ms().items()}
     RH.kernel_timer.enable(False)
+    # per-step statistics of the same steps (each step ended by a synchronisation)
+    st_fb = step_times(fwd_bwd, args.steps, 2)
+    st_f = step_times(fwd, args.steps, args.warmup)
     ms_fwd, _ = time_loop(fwd, args.steps, args.warmup)
     ms_oct_fwd, _ = time_loop(oct_fwd, args.steps, args.warmup)
     ms_oct, _ = time_loop(oct_fwd_bwd, args.steps, args.warmup)
@@ -327,6 +425,7 @@ def main():
         "bwd": {"ms": in_step["bwd"], "tflops": fl_b / (in_step["bwd"] * 1e-3) / 1e12,
                 "gbs": algorithmic_bytes_bwd(N, tot, P) / (in_step["bwd"] * 1e-3) / 1e9},
     }
+    chain = avg["bin_kernels"] + in_step["fwd"] + in_step["bwd"] + avg["reduce"]
     dom = "bwd" if in_step["bwd"] >= in_step["fwd"] else "fwd"
     dk = kern[dom]
     traffic = measured_traffic(f"k_{dom}_cull")
@@ -360,6 +459,12 @@ def main():
         "octave_fwd_ms": round(ms_oct_fwd, 4),
         "octave_fwd_bwd_ms": round(ms_oct, 4),
         "wall_ms_per_step": round(wall_ms, 4),
+        "step_ms_median_p10_p90": [round(x, 4) for x in st_fb],
+        "fwd_step_ms_median_p10_p90": [round(x, 4) for x in st_f],
+        # device time of the step's kernels alone: the binning's kernels back to back, the two tile kernels as
+        # they ran inside the fwd+bwd steps, the reduction back to back
+        "gpu_chain_ms": round(chain, 4),
+        "gpu_chain_mpix_s": round(mpix / (chain * 1e-3), 2),
     }
     if not args.no_c4:
         line["c4"] = stress_c4(max(5, args.steps // 5), max(2, args.warmup // 5), odds)
