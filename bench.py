@@ -155,8 +155,8 @@ def kernel_times(leaves, H, W, odds, reps):
         RH._lib.check(lib.splat_bin_count(mu.data_ptr(), lsf.data_ptr(), thp, op.data_ptr(), col.data_ptr(), C, N, H, W,
                                           8, 3.0, None, RH.FLAG_LOG_SCALE, blk.ptr(0), blk.ptr(1), blk.ptr(2),
                                           blk.ptr(3), blk.ptr(4), blk.nbytes(4), stream), "splat_bin_count")
-        RH._lib.check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), N, H, W, 8, None, tot, pb.ptr(0), pb.ptr(1),
-                                          pb.ptr(2), pb.ptr(3), pb.ptr(4), pb.nbytes(4), stream), "splat_bin_pairs")
+        RH._lib.check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), blk.ptr(4), N, H, W, 8, None, tot, pb.ptr(0), pb.ptr(1),
+                                          None, pb.ptr(2), pb.ptr(3), pb.nbytes(3), stream), "splat_bin_pairs")
 
     ms["bin_kernels"] = span(bin_kernels)
     RH.kernel_timer.enable(True)

@@ -37,22 +37,60 @@ constexpr long long kBadBit = 1LL << 62;        // marks a block holding an empt
 constexpr int kMaxRadixBits = 9;                // radix passes sort on digits of at most 9 bits
 constexpr int kMaxRadix = 1 << kMaxRadixBits;
 
+// Exclusive prefix of `v` over a 256-thread block (4 waves) with op = sum (MAX = false) or max (MAX = true,
+// identity -1). Returns the block total / maximum in `total`. Every thread must call it.
+template <bool MAX>
+__device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc = MAX ? max(inc, o) : inc + o;
+  }
+  if (lane == 63) s_w[wv] = inc;
+  __syncthreads();
+  int pre = MAX ? -1 : 0, tot = MAX ? -1 : 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int x = s_w[w];
+    if (w < wv) pre = MAX ? max(pre, x) : pre + x;
+    tot = MAX ? max(tot, x) : tot + x;
+  }
+  int ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = MAX ? -1 : 0;
+  total = tot;
+  __syncthreads();
+  return MAX ? max(pre, ex) : pre + ex;
+}
+
 // ----------------------------------------------------------------------------------------------------
 // decode + level + rect + count. block_sums[blk * kSumCols + 0] = the block's pair count (| kBadBit),
 // block_sums[blk * kSumCols + 1 + l] = its pairs on level l.
+// With `rowhist` (the row plan of the pair phase, below): also the block's histogram over the global tile rows
+// of its splats' units (one unit = one splat x one tile row of its rect), rowhist[r * nb + blk] = (units of
+// row r, pairs of row r) for every row r < L.rbase[L.n], from difference arrays in LDS.
 constexpr int kSumCols = 1 + kMaxLevels;
+constexpr int kMaxRows = 1024;   // the row plan takes level tables of at most this many tile rows
 
 template <int C>
 __global__ __launch_bounds__(kBlock) void k_decode_count(
     const float* __restrict__ mu, const float* __restrict__ scale, const float* __restrict__ theta,
     const float* __restrict__ opacity, const float* __restrict__ color, int N, LevelTable L, Routing R, float fT,
     float cutoff, int do_bin, int act, float4* __restrict__ rec, int4* __restrict__ rect, int* __restrict__ counts,
-    long long* __restrict__ block_sums) {
+    long long* __restrict__ block_sums, int2* __restrict__ rowhist, int nb) {
   __shared__ long long s_part[kWaves];
   __shared__ int s_lev[kMaxLevels];
+  __shared__ int s_du[kMaxRows + 1], s_dp[kMaxRows + 1];
   const int g = blockIdx.x * kBlock + threadIdx.x;
+  const int nrows = L.rbase[L.n];
   if (do_bin) {
     for (int i = threadIdx.x; i < kMaxLevels; i += kBlock) s_lev[i] = 0;
+    if (rowhist)
+      for (int i = threadIdx.x; i <= nrows; i += kBlock) {
+        s_du[i] = 0;
+        s_dp[i] = 0;
+      }
     __syncthreads();
   }
   int cnt = 0;
@@ -103,7 +141,16 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
       cnt = bad ? 0 : w * h;
       rect[g] = make_int4(tx0, ty0, w, lev);   // the rect height is not needed past this point
       counts[g] = cnt;
-      if (cnt) atomicAdd(&s_lev[lev], cnt);
+      if (cnt) {
+        atomicAdd(&s_lev[lev], cnt);
+        if (rowhist) {   // rows [r0, r0 + h) each get one unit of w pairs
+          const int r0 = L.rbase[lev] + ty0;
+          atomicAdd(&s_du[r0], 1);
+          atomicAdd(&s_du[r0 + h], -1);
+          atomicAdd(&s_dp[r0], w);
+          atomicAdd(&s_dp[r0 + h], -w);
+        }
+      }
     }
   }
   if (!do_bin) return;
@@ -120,6 +167,29 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     block_sums[(size_t)blockIdx.x * kSumCols] = t | b;
   }
   if (threadIdx.x < kMaxLevels) block_sums[(size_t)blockIdx.x * kSumCols + 1 + threadIdx.x] = s_lev[threadIdx.x];
+  if (!rowhist) return;
+  // inclusive scan of the difference arrays over the rows: thread t takes rows [4 t, 4 t + 4)
+  static_assert(kMaxRows <= 4 * kBlock, "rows per thread");
+  __shared__ int s_w[kWaves];
+  int du[4], dp[4], su = 0, sp = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = 4 * (int)threadIdx.x + k;
+    du[k] = r < nrows ? s_du[r] : 0;
+    dp[k] = r < nrows ? s_dp[r] : 0;
+    su += du[k];
+    sp += dp[k];
+  }
+  int t_u, t_p;
+  int pu = block256_excl<false>(su, s_w, t_u);
+  int pp = block256_excl<false>(sp, s_w, t_p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = 4 * (int)threadIdx.x + k;
+    pu += du[k];
+    pp += dp[k];
+    if (r < nrows) rowhist[(size_t)r * nb + blockIdx.x] = make_int2(pu, pp);
+  }
 }
 
 // One entry of the count phase's totals, into `info` and, when the caller gave one, into its mirror in pinned
@@ -205,16 +275,59 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int* __restrict__ offsets, c
   if (g == N - 1) offsets[N] = (int)info[0];
 }
 
+// Row r of the row histogram (row plan): rowhist[r * nb + b].x, the units of row r in block b, becomes the
+// exclusive prefix over the blocks before b; rtot[r] = (units, pairs) of row r over all blocks. 256 threads.
+__device__ __forceinline__ void row_scan(int2* __restrict__ rowhist, int nb, int r, int2* __restrict__ rtot) {
+  __shared__ int s_w[kWaves];
+  __shared__ int s_wp[kWaves];
+  int2* row = rowhist + (size_t)r * nb;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int carry = 0, pairs = 0;
+  for (int base = 0; base < nb; base += kBlock * 8) {
+    const int i0 = base + (int)threadIdx.x * 8;
+    int v[8], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int2 e = i0 + k < nb ? row[i0 + k] : make_int2(0, 0);
+      v[k] = e.x;
+      sum += e.x;
+      pairs += e.y;
+    }
+    int total;
+    int run = carry + block256_excl<false>(sum, s_w, total);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (i0 + k < nb) row[i0 + k].x = run;
+      run += v[k];
+    }
+    carry += total;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) pairs += __shfl_xor(pairs, m, 64);
+  if (lane == 0) s_wp[wv] = pairs;
+  __syncthreads();
+  if (threadIdx.x == 0) rtot[r] = make_int2(carry, s_wp[0] + s_wp[1] + s_wp[2] + s_wp[3]);
+}
+
+__global__ __launch_bounds__(kBlock) void k_row_scan(int2* __restrict__ rowhist, int nb, int2* __restrict__ rtot) {
+  row_scan(rowhist, nb, blockIdx.x, rtot);
+}
+
 // counts -> exclusive offsets in place without a separate scan launch (for up to kFusedScanBlocks blocks):
 // every block sums its predecessors' block totals itself (L2-resident, at most a few thousand loads per
 // block). The last block also writes info (and its mirror): total pairs, error bits and the per-level totals
-// (l < nlev).
+// (l < nlev). With rowhist, workgroups nb, nb + 1, ... scan the row plan's histogram rows (row_scan).
 constexpr int kFusedScanBlocks = 4096;
 
 __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offsets,
                                                           const long long* __restrict__ sums, int N, int nb,
                                                           int nlev, long long* __restrict__ info,
-                                                          long long* __restrict__ mirror) {
+                                                          long long* __restrict__ mirror, int2* __restrict__ rowhist,
+                                                          int2* __restrict__ rtot) {
+  if ((int)blockIdx.x >= nb) {   // the row plan's histogram rows, one workgroup each, in the same launch
+    row_scan(rowhist, nb, blockIdx.x - nb, rtot);
+    return;
+  }
   __shared__ long long s_r[kWaves];
   __shared__ long long s_lev[kMaxLevels];
   __shared__ int s_w[kWaves];
@@ -333,32 +446,6 @@ __device__ __forceinline__ int block_last_le(const int* __restrict__ a, int n, i
   return lo;
 }
 
-// Exclusive prefix of `v` over a 256-thread block (4 waves) with op = sum (MAX = false) or max (MAX = true,
-// identity -1). Returns the block total / maximum in `total`. Every thread must call it.
-template <bool MAX>
-__device__ __forceinline__ int block256_excl(int v, int* s_w, int& total) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  int inc = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(inc, d, 64);
-    if (lane >= d) inc = MAX ? max(inc, o) : inc + o;
-  }
-  if (lane == 63) s_w[wv] = inc;
-  __syncthreads();
-  int pre = MAX ? -1 : 0, tot = MAX ? -1 : 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int x = s_w[w];
-    if (w < wv) pre = MAX ? max(pre, x) : pre + x;
-    tot = MAX ? max(tot, x) : tot + x;
-  }
-  int ex = __shfl_up(inc, 1, 64);
-  if (lane == 0) ex = MAX ? -1 : 0;
-  total = tot;
-  __syncthreads();
-  return MAX ? max(pre, ex) : pre + ex;
-}
 
 // Block = kSortKeys consecutive pairs. Each splat with pairs in the block marks its first pair there with its
 // id; an inclusive max-scan over the block then gives every pair its owner (splat ids grow with p).
@@ -827,6 +914,356 @@ __global__ void k_fill_i32(int* __restrict__ a, int n, int v) {
   if (i < n) a[i] = v;
 }
 
+// ---------------------------------------------------------------------------------------------- row plan
+// Pair phase of the row plan (level tables of at most kMaxRows tile rows). A unit is one splat x one tile row
+// of its rect: units are 4-5x fewer than pairs at the benchmark size. The pairs of tile row r in (tile, splat)
+// order are the row's units in splat order, expanded column by column; so the sort is a stable partition of
+// the units by row (k_scatter_units, from the decode pass's per-block row histogram), and the per-row
+// expansion (k_expand_row) writes the pair list, the maps and the CSR starts of the row's tiles.
+// Unit arrays (index = position in row-major, splat-ascending order): ug = splat, uq = splat-major index of
+// the unit's first pair (offsets[g] + k w for the splat's k-th row), uspan = tx0 | w << 16.
+
+// Stable scatter of the units of block `blockIdx.x` (the decode pass's 256 splats) to their row's range:
+// position = first unit of row r (prefix of the row totals) + the block's offset within row r (the scanned
+// histogram) + the unit's rank among the block's units of row r in splat order. The block's units are
+// walked in splat order, kSortKeys per round: wave w ranks units [512 w, 512 w + 512) of the round 64 at a
+// time, equal rows by ballots on top of the wave's running counts; the waves' counts are scanned per row.
+__global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict__ rect, const int* __restrict__ offsets,
+                                                          int N, LevelTable L, const long long* __restrict__ info,
+                                                          int cap, const int2* __restrict__ rowhist,
+                                                          const int2* __restrict__ rtot, int nb, int* __restrict__ ug,
+                                                          int* __restrict__ uq, int* __restrict__ uspan) {
+  __shared__ int s_own[kSortKeys];
+  __shared__ int s_u0[kBlock], s_r0[kBlock], s_q0[kBlock], s_span[kBlock];
+  __shared__ int s_cnt[kWaves * kMaxRows];   // [wave][row - rmin]
+  __shared__ int s_base[kMaxRows];            // [row]: where the block's next unit of the row goes
+  __shared__ int s_w[kWaves];
+  const int tot = pair_count(info, cap);
+  if (tot == 0) return;   // no pairs, or a speculative launch past its capacity: no units to place
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int blk = blockIdx.x;
+  const int t = threadIdx.x;
+  const int g = blk * kBlock + t;
+  const int nrows = L.rbase[L.n];
+  int h = 0, r0 = nrows, r1 = -1, q0 = 0, span = 0, w = 1;
+  if (g < N) {
+    const int4 rc = rect[g];
+    q0 = offsets[g];
+    const int cnt = offsets[g + 1] - q0;
+    if (cnt > 0 && rc.z > 0) {
+      w = rc.z;
+      h = cnt / w;
+      r0 = L.rbase[rc.w] + rc.y;
+      r1 = r0 + h - 1;
+      span = rc.x | (w << 16);
+    }
+  }
+  // the block's row range [rmin, rmax] (block-uniform; maxima of values >= -1, the max-scan's identity)
+  int rmax, rmin;
+  block256_excl<true>(r1, s_w, rmax);
+  block256_excl<true>(nrows - r0, s_w, rmin);
+  rmin = nrows - rmin;
+  if (rmax < rmin) return;   // the block holds no units
+  const int nr = rmax - rmin + 1;
+  int nu;
+  const int u0 = block256_excl<false>(h, s_w, nu);   // first unit of splat t within the block; nu = block total
+  s_u0[t] = u0;
+  s_r0[t] = r0;
+  s_q0[t] = q0;
+  s_span[t] = span;
+  // first unit of every row: exclusive prefix of the row totals (rows [4 t, 4 t + 4) per thread)
+  {
+    int v[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * t + k;
+      v[k] = r < nrows ? rtot[r].x : 0;
+      sum += v[k];
+    }
+    int total;
+    int run = block256_excl<false>(sum, s_w, total);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * t + k;
+      if (r >= rmin && r <= rmax) s_base[r] = run + rowhist[(size_t)r * nb + blk].x;
+      run += v[k];
+    }
+  }
+  int nbits = 0;
+  while ((1 << nbits) < nr) ++nbits;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int rb = 0; rb < nu; rb += kSortKeys) {
+    for (int i = t; i < kSortKeys; i += kBlock) s_own[i] = -1;
+    for (int i = t; i < kWaves * nr; i += kBlock) s_cnt[(i / nr) * kMaxRows + i % nr] = 0;
+    __syncthreads();
+    if (h > 0 && u0 < rb + kSortKeys && u0 + h > rb) s_own[max(u0, rb) - rb] = t;   // one splat per entry
+    __syncthreads();
+    {   // owner of every unit of the round: inclusive max-scan (thread t: entries [8 t, 8 t + 8))
+      int loc[8], run = -1;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        run = max(run, s_own[8 * t + k]);
+        loc[k] = run;
+      }
+      int total;
+      const int ex = block256_excl<true>(run, s_w, total);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s_own[8 * t + k] = max(loc[k], ex);
+    }
+    __syncthreads();
+    int rk[kItems], rr[kItems], own[kItems], kk[kItems];
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      const int i = wv * kWaveKeys + j * 64 + lane;
+      const bool act = rb + i < nu;
+      const int o = act ? s_own[i] : 0;
+      const int k = act ? rb + i - s_u0[o] : 0;
+      const int r = act ? s_r0[o] + k - rmin : 0;
+      unsigned long long peers = __ballot(act);
+      for (int b = 0; b < nbits; ++b) {
+        const bool bit = (r >> b) & 1;
+        const unsigned long long m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int below = __popcll(peers & lt);
+      const int before = act ? s_cnt[wv * kMaxRows + r] : 0;
+      if (act && below == 0) s_cnt[wv * kMaxRows + r] = before + __popcll(peers);
+      rk[j] = before + below;
+      rr[j] = act ? r : -1;
+      own[j] = o;
+      kk[j] = k;
+    }
+    __syncthreads();
+    for (int r = t; r < nr; r += kBlock) {   // per row: the waves' starts, in wave order
+      int run = s_base[rmin + r];
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const int c = s_cnt[ww * kMaxRows + r];
+        s_cnt[ww * kMaxRows + r] = run;
+        run += c;
+      }
+      s_base[rmin + r] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      if (rr[j] < 0) continue;
+      const int pos = s_cnt[wv * kMaxRows + rr[j]] + rk[j];
+      const int o = own[j];
+      const int sp = s_span[o];
+      if ((unsigned)pos < (unsigned)cap) {
+        ug[pos] = blk * kBlock + o;
+        uq[pos] = s_q0[o] + kk[j] * (sp >> 16);
+        uspan[pos] = sp;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// One workgroup of kRowThreads per tile row and chunk of at most kRowCols tile columns (blockIdx.y = global
+// row r, blockIdx.x = chunk of cw columns). The row's units are read kRowUnits at a time and those meeting the
+// chunk are kept, in order, in an LDS list; a difference array over their column ranges (LDS atomics) gives
+// the chunk's column counts, so its tile starts follow the row's pairs before the chunk (counted on the way).
+// Each wave then owns the columns j = wave, wave + 8, ...: it walks the list 64 units at a time and, per
+// column, the units covering it (one ballot) are that tile's next pairs in splat order, written by consecutive
+// lanes at the column's running position. A row of one round is read once; longer rows twice (counting, then
+// writing round by round, the running positions carried over).
+constexpr int kRowThreads = 512;
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kRowItems = 4;                          // units per thread and round
+constexpr int kRowUnits = kRowThreads * kRowItems;   // 2048 units per round
+constexpr int kRowCols = 128;                         // columns per chunk, at most
+constexpr int kRowColsPerWave = kRowCols / kRowWaves;
+
+__global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const long long* __restrict__ info, int cap,
+                                                            const int2* __restrict__ rtot, int cw,
+                                                            const int* __restrict__ ug, const int* __restrict__ uq,
+                                                            const int* __restrict__ uspan, int* __restrict__ gid_sorted,
+                                                            int* __restrict__ tile_starts, int* __restrict__ pair_splat,
+                                                            int* __restrict__ pair_q) {
+  __shared__ int s_cg[kRowUnits], s_cq[kRowUnits], s_cs[kRowUnits];   // the round's units meeting the chunk
+  __shared__ int s_diff[kRowCols + 1];   // difference array, then per column its first position
+  __shared__ int s_kc[kRowItems][kRowWaves];
+  __shared__ int s_red[3][kRowWaves];
+  __shared__ int s_n;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int r = blockIdx.y;
+  const int l = level_of_row(L, r);
+  const int ntx = L.ntx[l];
+  const int c0 = blockIdx.x * cw;
+  if (c0 >= ntx) return;
+  const int c1 = min(c0 + cw, ntx), ncol = c1 - c0;
+  const int tile0 = L.tbase[l] + (r - L.rbase[l]) * ntx + c0;
+  const int nt = L.tbase[L.n];
+  const int tot = pair_count(info, cap);
+  if (tot == 0) {   // no pairs (or a speculative launch past its capacity): the empty list
+    if (t < ncol) tile_starts[tile0 + t] = 0;
+    if (r == 0 && c0 == 0 && t == 0) {
+      tile_starts[nt] = 0;
+      gid_sorted[0] = 0;
+    }
+    return;
+  }
+  if (r == 0 && c0 == 0 && t == 0) tile_starts[nt] = tot;
+  // units and pairs of the rows before r
+  int us = 0, pr = 0;
+  for (int i = t; i < r; i += kRowThreads) {
+    const int2 e = rtot[i];
+    us += e.x;
+    pr += e.y;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    us += __shfl_xor(us, m, 64);
+    pr += __shfl_xor(pr, m, 64);
+  }
+  if (lane == 0) {
+    s_red[0][wv] = us;
+    s_red[1][wv] = pr;
+  }
+  if (t <= kRowCols) s_diff[t] = 0;
+  __syncthreads();
+  us = 0;
+  pr = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) {
+    us += s_red[0][w];
+    pr += s_red[1][w];
+  }
+  // the row's units (at most one per pair: within the capacity the unit arrays are sized for)
+  const int ue = min(us + rtot[r].x, cap);
+  us = min(us, ue);
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int nround = (ue - us + kRowUnits - 1) / kRowUnits;
+  // unit rb + 1024 k + t in slot k of thread t: (k, thread) order is unit order
+  int sp[kRowItems], gg[kRowItems], qq[kRowItems];
+  auto load = [&](int rb, bool all) {
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) {
+      const int u = rb + kRowThreads * k + t;
+      const bool act = u < ue;
+      sp[k] = act ? uspan[u] : 0;   // w = 0: meets no column
+      if (all) {
+        gg[k] = act ? ug[u] : 0;
+        qq[k] = act ? uq[u] : 0;
+      }
+    }
+  };
+  auto meets = [&](int s1) {
+    const int a = s1 & 0xffff, z = a + (s1 >> 16);
+    return z > a && a < c1 && z > c0;
+  };
+  // the round's units meeting the chunk into the list, in unit order; returns their number
+  auto compact = [&]() -> int {
+    unsigned long long mk[kRowItems];
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) {
+      mk[k] = __ballot(meets(sp[k]));
+      if (lane == 0) s_kc[k][wv] = __popcll(mk[k]);
+    }
+    __syncthreads();
+    if (t == 0) {   // exclusive prefix in (k, wave) order
+      int run = 0;
+      for (int k = 0; k < kRowItems; ++k)
+        for (int w = 0; w < kRowWaves; ++w) {
+          const int c = s_kc[k][w];
+          s_kc[k][w] = run;
+          run += c;
+        }
+      s_n = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k)
+      if ((mk[k] >> lane) & 1) {
+        const int idx = s_kc[k][wv] + __popcll(mk[k] & lt);
+        s_cg[idx] = gg[k];
+        s_cq[idx] = qq[k];
+        s_cs[idx] = sp[k];
+      }
+    const int n = s_n;
+    __syncthreads();
+    return n;
+  };
+  // counting: the row's pairs before c0 and, per column of the chunk, a difference array of the units meeting it
+  int before = 0;
+  for (int rd = 0; rd < nround; ++rd) {
+    load(us + rd * kRowUnits, nround == 1);
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) {
+      const int a = sp[k] & 0xffff, z = a + (sp[k] >> 16);
+      if (a < c0) before += min(z, c0) - a;
+      if (meets(sp[k])) {
+        atomicAdd(&s_diff[max(a, c0) - c0], 1);
+        atomicAdd(&s_diff[min(z, c1) - c0], -1);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) before += __shfl_xor(before, m, 64);
+  if (lane == 0) s_red[2][wv] = before;
+  __syncthreads();
+  // tile starts: the prefix of the column counts after the row's pairs before c0 (wave 0; s_diff -> starts)
+  if (wv == 0) {
+    int run = pr;
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) run += s_red[2][w];
+    int cnt_run = 0;   // the running column count (inclusive scan of the difference array)
+    for (int jb = 0; jb < ncol; jb += 64) {
+      const int j = jb + lane;
+      const int d = j < ncol ? s_diff[j] : 0;
+      const int cnt = cnt_run + wave_incl_scan<int>(d, lane);   // pairs of column j
+      const int c = j < ncol ? cnt : 0;
+      const int inc = wave_incl_scan<int>(c, lane);
+      if (j < ncol) {
+        s_diff[j] = run + inc - c;
+        tile_starts[tile0 + j] = run + inc - c;
+      }
+      cnt_run = __shfl(cnt, 63, 64);
+      run += __shfl(inc, 63, 64);
+    }
+  }
+  __syncthreads();
+  // writing: wave wv owns columns wv + 16 m; its running positions stay in registers across rounds
+  int pos[kRowColsPerWave];
+#pragma unroll
+  for (int m = 0; m < kRowColsPerWave; ++m) {
+    const int j = wv + kRowWaves * m;
+    pos[m] = j < ncol ? s_diff[j] : 0;
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+    if (nround > 1) load(us + rd * kRowUnits, true);
+    const int n = compact();
+    for (int b = 0; b < n; b += 64) {
+      const int i = b + lane;
+      const bool act = i < n;
+      const int s1 = act ? s_cs[i] : 0;
+      const int g = act ? s_cg[i] : 0, q = act ? s_cq[i] : 0;
+      const int a = s1 & 0xffff, z = a + (s1 >> 16);
+#pragma unroll
+      for (int m = 0; m < kRowColsPerWave; ++m) {
+        const int c = c0 + wv + kRowWaves * m;
+        if (c >= c1) break;
+        const bool cov = act && a <= c && c < z;
+        const unsigned long long msk = __ballot(cov);
+        if (cov) {
+          const int p = pos[m] + __popcll(msk & lt);
+          const int qc = q + (c - a);
+          if ((unsigned)p < (unsigned)cap) {
+            gid_sorted[p] = g;
+            if (pair_q) pair_q[p] = qc;
+          }
+          if (pair_splat && (unsigned)qc < (unsigned)cap) pair_splat[qc] = g;
+        }
+        pos[m] += __popcll(msk);
+      }
+    }
+    __syncthreads();   // before the next round's list
+  }
+}
+
 // ----------------------------------------------------------------------------------------------------
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -876,14 +1313,50 @@ static PairsPlan plan_pairs(int nt, long long tot) {
   return p;
 }
 
+// Row plan (k_scatter_units + k_expand_row) when the level table has at most kMaxRows tile rows and the row
+// histogram (rows x decode blocks) stays below kMaxRowHist entries; else the pair-sort plans of plan_pairs.
+// Count workspace: the block sums, then (row plan) the row histogram int2[nrows][nb] and the row totals
+// int2[nrows]. Pair workspace of the row plan: the unit arrays ug, uq, uspan for up to `tot` units (a rect
+// row holds at least one pair, so units <= pairs).
+constexpr long long kMaxRowHist = 1LL << 22;
+
+struct CountPlan {
+  int nb, rows, nrows;
+  size_t off_rowhist, off_rtot, total;
+};
+
+static CountPlan plan_count(const LevelTable& L, int N) {
+  CountPlan c{};
+  c.nb = N > 0 ? div_up(N, kBlock) : 1;
+  c.nrows = L.rbase[L.n];
+  c.rows = c.nrows >= 1 && c.nrows <= kMaxRows && (long long)c.nrows * c.nb <= kMaxRowHist;
+  size_t o = align256(sizeof(long long) * kSumCols * (size_t)c.nb);
+  if (c.rows) {
+    c.off_rowhist = o; o += align256(sizeof(int2) * (size_t)c.nrows * c.nb);
+    c.off_rtot = o;    o += align256(sizeof(int2) * (size_t)c.nrows);
+  }
+  c.total = o;
+  return c;
+}
+
+static size_t unit_bytes(long long tot) { return align256(sizeof(int) * (size_t)(tot > 0 ? tot : 1)); }
+
+// Bytes of the pair workspace for `tot` pairs under the plan the level table takes.
+static size_t pairs_ws_bytes(const LevelTable& L, int N, long long tot) {
+  return plan_count(L, N).rows ? 3 * unit_bytes(tot) : plan_pairs(L.tbase[L.n], tot).total;
+}
+
+
 }  // namespace splat
 
 using namespace splat;
 
 extern "C" {
 
-size_t splat_bin_count_workspace_bytes(int N) {
-  return align256(sizeof(long long) * kSumCols * (size_t)(N > 0 ? div_up(N, kBlock) : 1));
+size_t splat_bin_count_workspace_bytes(int N, int H, int W, int TILE, const splat_levels* lv) {
+  LevelTable L;
+  if (N < 0 || H < 1 || W < 1 || TILE < 1 || make_levels(H, W, TILE, lv, &L, nullptr)) return 0;
+  return plan_count(L, N).total;
 }
 
 int splat_levels_geometry(int H, int W, int TILE, const splat_levels* lv, int* out, int cap) {
@@ -913,7 +1386,7 @@ int splat_decode(const float* mu, const float* scale, const float* theta, const 
   Routing R{};
 #define SPLAT_DECODE(CC)                                                                                      \
   k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, 1.f, 0.f, 0, 0,     \
-                                            reinterpret_cast<float4*>(rec), nullptr, nullptr, nullptr)
+                                            reinterpret_cast<float4*>(rec), nullptr, nullptr, nullptr, nullptr, 0)
   switch (C) { case 1: SPLAT_DECODE(1); break; case 2: SPLAT_DECODE(2); break;
                case 3: SPLAT_DECODE(3); break; default: SPLAT_DECODE(4); break; }
 #undef SPLAT_DECODE
@@ -929,21 +1402,26 @@ int bin_count_launch(const float* mu, const float* scale, const float* theta, co
                      const float* color, int C, int N, const LevelTable& L, const Routing& R, int TILE, float cutoff,
                      int flags, float* rec, int* rect, int* offsets, long long* info, long long* mirror, void* ws,
                      hipStream_t st) {
-  const int nb = div_up(N, kBlock);
+  const CountPlan cp = plan_count(L, N);
+  const int nb = cp.nb;
   long long* sums = (long long*)ws;
+  int2* rowhist = cp.rows ? (int2*)((char*)ws + cp.off_rowhist) : nullptr;
+  int2* rtot = cp.rows ? (int2*)((char*)ws + cp.off_rtot) : nullptr;
 #define SPLAT_DC(CC)                                                                                         \
   k_decode_count<CC><<<nb, kBlock, 0, st>>>(mu, scale, theta, opacity, color, N, L, R, (float)TILE, cutoff, 1, \
                                             (flags & kFlagLogScale) ? 1 : 0,                                \
                                             reinterpret_cast<float4*>(rec), reinterpret_cast<int4*>(rect), \
-                                            offsets, sums)
+                                            offsets, sums, rowhist, nb)
   switch (C) { case 1: SPLAT_DC(1); break; case 2: SPLAT_DC(2); break;
                case 3: SPLAT_DC(3); break; default: SPLAT_DC(4); break; }
 #undef SPLAT_DC
   if (nb <= kFusedScanBlocks) {
-    k_offsets_fused<<<nb, kBlock, 0, st>>>(offsets, sums, N, nb, L.n, info, mirror);
+    k_offsets_fused<<<nb + (cp.rows ? cp.nrows : 0), kBlock, 0, st>>>(offsets, sums, N, nb, L.n, info, mirror, rowhist,
+                                                                      rtot);
   } else {
     k_scan_sums<<<1, 1024, 0, st>>>(sums, nb, L.n, info, mirror);
     k_offsets<<<nb, kBlock, 0, st>>>(offsets, sums, N, info);
+    if (cp.rows) k_row_scan<<<cp.nrows, kBlock, 0, st>>>(rowhist, nb, rtot);
   }
   return check_launch("splat_bin_count");
 }
@@ -951,16 +1429,38 @@ int bin_count_launch(const float* mu, const float* scale, const float* theta, co
 // Launches of the pair phase. Exact (dinfo NULL): `t` is the pair count. Speculative (dinfo = the count
 // phase's device info): `t` is the capacity the buffers and the grids are sized for, and the kernels take
 // the count from dinfo (an empty list when it exceeds t). Arguments already validated; ws holds
-// plan_pairs(nt, t).
-int bin_pairs_launch(const int* rect, const int* offsets, int N, const LevelTable& L, int t, const long long* dinfo,
-                     int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws, hipStream_t st) {
+// pairs_ws_bytes(L, N, t); ws_count the count phase's workspace (the row plan's histogram).
+int bin_pairs_launch(const int* rect, const int* offsets, const void* ws_count, int N, const LevelTable& L, int t,
+                     const long long* dinfo, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws,
+                     hipStream_t st) {
   const int nt = L.tbase[L.n];
-  const PairsPlan pl = plan_pairs(nt, t);
   if (t == 0) {
     k_fill_i32<<<div_up(nt + 1, 256), 256, 0, st>>>(tile_starts, nt + 1, 0);
     k_fill_i32<<<1, 64, 0, st>>>(gid_sorted, 1, 0);
     return check_launch("splat_bin_pairs(empty)");
   }
+  const CountPlan cp = plan_count(L, N);
+  if (cp.rows) {
+    const int2* rowhist = (const int2*)((const char*)ws_count + cp.off_rowhist);
+    const int2* rtot = (const int2*)((const char*)ws_count + cp.off_rtot);
+    const size_t ub = unit_bytes(t);
+    int* ug = (int*)ws;
+    int* uq = (int*)((char*)ws + ub);
+    int* uspan = (int*)((char*)ws + 2 * ub);
+    k_scatter_units<<<cp.nb, kBlock, 0, st>>>(reinterpret_cast<const int4*>(rect), offsets, N, L, dinfo, t, rowhist, rtot,
+                                              cp.nb, ug, uq, uspan);
+    int rc = check_launch("k_scatter_units");
+    if (rc) return rc;
+    int mxtx = 1;
+    for (int l = 0; l < L.n; ++l) mxtx = L.ntx[l] > mxtx ? L.ntx[l] : mxtx;
+    // chunks of at most kRowCols columns, about 8 per row of the widest level (measured: 4 to 12 chunks, 256 to
+    // 1024 threads, 2 to 8 units per thread; this is the fastest at 768 x 768 and 2048 x 2048)
+    const int cw = min(kRowCols, max(8, div_up(mxtx, 8)));
+    k_expand_row<<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(L, dinfo, t, rtot, cw, ug, uq, uspan,
+                                                                            gid_sorted, tile_starts, pair_splat, pair_q);
+    return check_launch("k_expand_row");
+  }
+  const PairsPlan pl = plan_pairs(nt, t);
   char* base = (char*)ws;
   int* S[2][3];   // workspace sets: keys, splat ids, splat-major indices
   for (int s = 0; s < 2; ++s)
@@ -1083,28 +1583,30 @@ int splat_bin_count(const float* mu, const float* scale, const float* theta, con
   if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin_count: bad levels");
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info)
     return set_error(kInvalid, "splat_bin_count: null pointer");
-  if (ws_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin_count: workspace too small");
+  if (ws_bytes < plan_count(L, N).total) return set_error(kWorkspace, "splat_bin_count: workspace too small");
   return bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets, info, nullptr,
                           ws, (hipStream_t)stream);
 }
 
-size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot) {
-  (void)N;
-  return plan_pairs(nt, tot).total;
+size_t splat_bin_pairs_workspace_bytes(int N, int H, int W, int TILE, const splat_levels* lv, long long tot) {
+  LevelTable L;
+  if (N < 0 || H < 1 || W < 1 || TILE < 1 || tot < 0 || make_levels(H, W, TILE, lv, &L, nullptr)) return 0;
+  return pairs_ws_bytes(L, N, tot);
 }
 
-int splat_bin_pairs(const int* rect, const int* offsets, int N, int H, int W, int TILE, const splat_levels* lv,
-                    long long tot, int* gid_sorted, int* tile_starts, int* pair_splat, int* pair_q, void* ws,
-                    size_t ws_bytes, void* stream) {
+int splat_bin_pairs(const int* rect, const int* offsets, const void* ws_count, int N, int H, int W, int TILE,
+                    const splat_levels* lv, long long tot, int* gid_sorted, int* tile_starts, int* pair_splat,
+                    int* pair_q, void* ws, size_t ws_bytes, void* stream) {
   if (N < 1 || H < 1 || W < 1 || TILE < 1 || tot < 0 || tot > 0x7fffffffLL - 64)
     return set_error(kInvalid, "splat_bin_pairs: N=%d H=%d W=%d TILE=%d tot=%lld", N, H, W, TILE, tot);
-  if (!rect || !offsets || !gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin_pairs: null pointer");
+  if (!rect || !offsets || !ws_count || !gid_sorted || !tile_starts)
+    return set_error(kInvalid, "splat_bin_pairs: null pointer");
   LevelTable L;
   if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_pairs: bad levels");
-  const PairsPlan pl = plan_pairs(L.tbase[L.n], tot);
-  if (ws_bytes < pl.total) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, pl.total);
-  return bin_pairs_launch(rect, offsets, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws,
-                          (hipStream_t)stream);
+  const size_t need = pairs_ws_bytes(L, N, tot);
+  if (ws_bytes < need) return set_error(kWorkspace, "splat_bin_pairs: workspace %zu < %zu bytes", ws_bytes, need);
+  return bin_pairs_launch(rect, offsets, ws_count, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q,
+                          ws, (hipStream_t)stream);
 }
 
 int splat_bin(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color, int C,
@@ -1120,7 +1622,7 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin: bad levels");
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info || !info_host)
     return set_error(kInvalid, "splat_bin: null pointer");
-  if (ws_count_bytes < splat_bin_count_workspace_bytes(N)) return set_error(kWorkspace, "splat_bin: count workspace too small");
+  if (ws_count_bytes < plan_count(L, N).total) return set_error(kWorkspace, "splat_bin: count workspace too small");
   hipStream_t st = (hipStream_t)stream;
   // the one device -> host read of the render (totals and error bits): the offsets kernel writes them into
   // info_host itself when it is pinned memory, else they are copied. Entries the kernel has not written keep
@@ -1141,9 +1643,9 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   // With buffers for pair_cap > 0 pairs the pair phase is queued before the host waits for the count: the GPU
   // goes on with it while the host reads the count (kernels past the count, or past pair_cap, do nothing).
   const bool spec = pair_cap > 0 && pair_cap <= 0x7fffffffLL - 64 && gid_sorted && tile_starts &&
-                    ws_pairs_bytes >= plan_pairs(L.tbase[L.n], pair_cap).total;
+                    ws_pairs_bytes >= pairs_ws_bytes(L, N, pair_cap);
   if (spec) {
-    rc = bin_pairs_launch(rect, offsets, N, L, (int)pair_cap, info, gid_sorted, tile_starts, pair_splat, pair_q,
+    rc = bin_pairs_launch(rect, offsets, ws_count, N, L, (int)pair_cap, info, gid_sorted, tile_starts, pair_splat, pair_q,
                           ws_pairs, st);
     if (rc) return rc;
   }
@@ -1168,8 +1670,8 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   if (tot > pair_cap) return set_error(kCapacity, "splat_bin: %lld pairs exceed the capacity %lld", tot, pair_cap);
   if (spec) return kOk;
   if (!gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin: null pair buffers");
-  if (ws_pairs_bytes < plan_pairs(L.tbase[L.n], tot).total) return set_error(kWorkspace, "splat_bin: pair workspace too small");
-  return bin_pairs_launch(rect, offsets, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs,
+  if (ws_pairs_bytes < pairs_ws_bytes(L, N, tot)) return set_error(kWorkspace, "splat_bin: pair workspace too small");
+  return bin_pairs_launch(rect, offsets, ws_count, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs,
                           st);
 }
 
@@ -1184,13 +1686,13 @@ int splat_bin_noalloc(const float* mu, const float* scale, const float* theta, c
     return set_error(kInvalid, "splat_bin_noalloc: needs pair buffers (pair_cap=%lld)", pair_cap);
   LevelTable L;
   if (make_levels(H, W, TILE, lv, &L, nullptr)) return set_error(kInvalid, "splat_bin_noalloc: bad levels");
-  const size_t cbytes = splat_bin_count_workspace_bytes(N);
-  const size_t pbytes = plan_pairs(L.tbase[L.n], pair_cap).total;
+  const size_t cbytes = plan_count(L, N).total;
+  const size_t pbytes = pairs_ws_bytes(L, N, pair_cap);
   if (cbytes + pbytes > kNoAllocScratchBytes)
     return set_error(kWorkspace,
                      "splat_bin_noalloc: N=%d splats with pair_cap=%lld need %zu bytes of scratch, above its %zu "
-                     "(about 25 bytes per pair: at most ~2.6M pairs); use splat_bin with a workspace",
-                     N, pair_cap, cbytes + pbytes, kNoAllocScratchBytes);
+                     "(12 bytes per pair at most, 25 past %d tile rows); use splat_bin with a workspace",
+                     N, pair_cap, cbytes + pbytes, kNoAllocScratchBytes, kMaxRows);
   char* ws = (char*)noalloc_scratch();
   if (!ws) return kHipError;
   return splat_bin(mu, scale, theta, opacity, color, C, N, H, W, TILE, cutoff, lv, flags, max_pairs, rec, rect,

@@ -28,6 +28,6 @@ extern "C" {
 
 const char* splat_last_error(void) { return splat::g_last_error; }
 
-int splat_abi_version(void) { return 2; }
+int splat_abi_version(void) { return 3; }
 
 }  // extern "C"

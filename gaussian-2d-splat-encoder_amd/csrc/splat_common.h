@@ -135,6 +135,7 @@ struct LevelTable {
   unsigned mask;   // levels holding at least one pair; kernels skip the others
   int H[kMaxLevels], W[kMaxLevels], ntx[kMaxLevels];
   int tbase[kMaxLevels + 1], pbase[kMaxLevels + 1];
+  int rbase[kMaxLevels + 1];   // global tile-row ids: level l's tile rows are [rbase[l], rbase[l + 1])
 };
 
 // Splat -> level routing, evaluated in the decode pass.
@@ -145,6 +146,13 @@ struct Routing {
   float inv_base;   // mode 1: fp32 1 / base_texels (a tensor divided by a CPU scalar is a multiply by its reciprocal)
   int n_coarse;     // mode 2: splats [0, n_coarse) are level 1
 };
+
+// Level of global tile row r.
+__device__ __forceinline__ int level_of_row(const LevelTable& L, int r) {
+  int l = 0;
+  while (l + 1 < L.n && r >= L.rbase[l + 1]) ++l;
+  return l;
+}
 
 __device__ __forceinline__ int level_of(const LevelTable& L, int t) {
   int l = 0;
@@ -223,11 +231,13 @@ inline int make_levels(int H, int W, int TILE, const splat_levels* lv, LevelTabl
   t.mask = (t.n >= 32) ? 0xffffffffu : ((1u << t.n) - 1u);
   t.tbase[0] = 0;
   t.pbase[0] = 0;
+  t.rbase[0] = 0;
   for (int l = 0; l < t.n; ++l) {
     t.ntx[l] = (t.W[l] + TILE - 1) / TILE;
     const long long nty = (t.H[l] + TILE - 1) / TILE;
     t.tbase[l + 1] = (int)(t.tbase[l] + (long long)t.ntx[l] * nty);
     t.pbase[l + 1] = (int)(t.pbase[l] + (long long)t.H[l] * t.W[l]);
+    t.rbase[l + 1] = (int)(t.rbase[l] + nty);
   }
   *L = t;
   if (R) *R = r;

@@ -36,14 +36,14 @@ _SIGS = {
     "splat_last_error": (ctypes.c_char_p, []),
     "splat_abi_version": (_I, []),
     "splat_decode": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP]),
-    "splat_bin_count_workspace_bytes": (_SZ, [_I]),
+    "splat_bin_count_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV]),
     "splat_levels_geometry": (_I, [_I, _I, _I, _LV, _VP, _I]),
     "splat_bin_count": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _VP, _VP, _VP, _VP, _VP, _SZ,
                              _VP]),
-    "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _LL]),
+    "splat_bin_pairs_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV, _LL]),
     "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                        _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
-    "splat_bin_pairs": (_I, [_VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_bin_pairs": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP,
                                _LL, _VP, _VP, _VP, _VP, _VP]),
     "splat_time_next_launch": (_I, [_VP, _VP]),

@@ -128,18 +128,17 @@ kernel_timer = KernelTimer()
 class TileBins:
     """Per-batch binning result: decoded splat records, pair list ordered by (tile, splat) and CSR tile
     starts (`gid_b`/`starts_b`/`ntx`/`nt` carry the meaning of the reference's `tiles` tuple), plus the
-    maps the backward uses between sorted and splat-major pair order (offsets, splat-major pair -> splat,
-    sorted pair -> splat-major index).
+    map the backward uses from sorted to splat-major pair order (`pq`: sorted pair -> splat-major index; the
+    splat of splat-major pair q is the g with offsets[g] <= q < offsets[g + 1]).
 
     Each image's buffers live in two allocations (`blocks[b]`: rec, rect, offsets; `pairs[b]`: gid, starts,
-    pair_splat, pair_q); kernels take raw pointers (`p(b, name)`), tensor views are built on first use.
+    pair_q); kernels take raw pointers (`p(b, name)`), tensor views are built on first use.
 
     With levels (`lv` set) the tile ids are global over the levels: `geom[l] = (H_l, W_l, ntx_l, tbase_l,
     pbase_l)`, `nt` / `npix` are the totals, `level_tot_b[b][l]` the pairs of level l and `rect_b[b][:, 3]`
     each splat's level."""
 
-    _SLOT = {"rec": (0, 0), "rect": (0, 1), "off": (0, 2), "gid": (1, 0), "starts": (1, 1), "psplat": (1, 2),
-             "pq": (1, 3)}
+    _SLOT = {"rec": (0, 0), "rect": (0, 1), "off": (0, 2), "gid": (1, 0), "starts": (1, 1), "pq": (1, 2)}
 
     def __init__(self, N, tot_b, H, W, TILE, ntx, nt, blocks, pairs, with_maps, lv=None, geom=None, npix=None,
                  level_tot_b=None):
@@ -174,7 +173,7 @@ class TileBins:
                 elif name == "starts":
                     out.append(pb.view(1, self.nt + 1, torch.int32))
                 else:
-                    out.append(pb.view(2 if name == "psplat" else 3, n, torch.int32) if self.with_maps else None)
+                    out.append(pb.view(2, n, torch.int32) if self.with_maps else None)
             v = self._views[name] = out
         return v
 
@@ -183,7 +182,6 @@ class TileBins:
     off_b = property(lambda self: self._list("off"))
     gid_b = property(lambda self: self._list("gid"))
     starts_b = property(lambda self: self._list("starts"))
-    psplat_b = property(lambda self: self._list("psplat"))
     pq_b = property(lambda self: self._list("pq"))
 
     def as_tuple(self):
@@ -294,11 +292,12 @@ def _budget_error(n, max_pairs, H, W, TILE, cutoff, N):
         f"instead of culling at full res. Refusing to allocate.")
 
 
-def _pair_buffers(lib, N, nt, cap, with_maps, dev):
-    """gid, starts, pair_splat, pair_q and the pair-phase workspace for up to `cap` pairs, one allocation."""
+def _pair_buffers(lib, N, nt, cap, with_maps, dev, geo):
+    """gid, starts, pair_q and the pair-phase workspace for up to `cap` pairs, one allocation.
+    geo = (H, W, TILE, levels byref or None)."""
     c = max(cap, 1)
     m = c if with_maps else 0
-    return _Carve([4 * c, 4 * (nt + 1), 4 * m, 4 * m, lib.splat_bin_pairs_workspace_bytes(N, nt, cap)], dev)
+    return _Carve([4 * c, 4 * (nt + 1), 4 * m, lib.splat_bin_pairs_workspace_bytes(N, *geo, cap)], dev)
 
 
 def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv, sflags):
@@ -322,19 +321,19 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     cap = hw + (hw >> 4) + 1024 if hw else 0
     info_t, info_np = _info_host()
     info_p = info_t.data_ptr()
-    ws1_bytes = lib.splat_bin_count_workspace_bytes(N)
+    geo = (H, W, TILE, lvr)
+    ws1_bytes = lib.splat_bin_count_workspace_bytes(N, *geo)
     budget = -1 if max_pairs is None else int(max_pairs)
     blocks, pairs, tots, level_tots = [], [], [], []
     for b in range(B):
         blk = _Carve([64 * N, 16 * N, 4 * (N + 1), 8 * (2 + L), ws1_bytes], dev)
-        pb = _pair_buffers(lib, N, nt, cap, with_maps, dev) if cap else None
+        pb = _pair_buffers(lib, N, nt, cap, with_maps, dev, geo) if cap else None
         pp = (lambda i: None) if pb is None else pb.ptr
         info_np[0] = info_np[1] = 0
         rc = lib.splat_bin(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]), ptr(col_[b]),
                            C, N, H, W, TILE, float(cutoff), lvr, sflags, budget, blk.ptr(0), blk.ptr(1), blk.ptr(2),
                            blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0), pp(1),
-                           pp(2) if with_maps else None, pp(3) if with_maps else None, pp(4),
-                           0 if pb is None else pb.nbytes(4), stream)
+                           None, pp(2) if with_maps else None, pp(3), 0 if pb is None else pb.nbytes(3), stream)
         tot = int(info_np[0])
         lt = info_np[2:2 + L].tolist()
         if rc == _lib.STATUS_BUDGET:
@@ -346,10 +345,10 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         if rc == 4:
             raise PairBudgetExceeded(f"binning: {tot} pairs exceed the int32 pair index range")
         if rc == _lib.STATUS_CAPACITY:
-            pb = _pair_buffers(lib, N, nt, tot, with_maps, dev)
-            check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), N, H, W, TILE, lvr, tot, pb.ptr(0), pb.ptr(1),
-                                      pb.ptr(2) if with_maps else None, pb.ptr(3) if with_maps else None, pb.ptr(4),
-                                      pb.nbytes(4), stream), "splat_bin_pairs")
+            pb = _pair_buffers(lib, N, nt, tot, with_maps, dev, geo)
+            check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), blk.ptr(4), N, H, W, TILE, lvr, tot, pb.ptr(0), pb.ptr(1),
+                                      None, pb.ptr(2) if with_maps else None, pb.ptr(3), pb.nbytes(3), stream),
+                  "splat_bin_pairs")
         else:
             check(rc, "splat_bin")
         if tot > hw:
@@ -522,7 +521,7 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
     ev = kernel_timer.record("reduce")
     try:
         check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
-                                     bins.p(b, "psplat") if tot else None, tot, N, C, ptr(sums), ptr(bg_part),
+                                     None, tot, N, C, ptr(sums), ptr(bg_part),
                                      bins.ntiles0, sl(lsc), sl(g_mu), sl(g_scale), sl(g_th), sl(g_op), sl(g_col),
                                      ptr(g_bg), stream), "splat_reduce_pairs")
     finally:

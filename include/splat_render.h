@@ -75,15 +75,21 @@ int splat_decode(const float *mu, const float *scale, const float *theta, const 
  * (offsets[N] = total pairs) and info[2 + L] (device int64): info[0] = total pairs, info[1] = error bits
  * (1 empty rect, 2 int32 overflow), info[2 + l] = pairs of level l (L = number of levels).
  * The caller reads info once to size the pair buffers and to apply its pair budget per level.
+ * The workspace (sized for N splats on the level table of H, W, TILE, lv) also carries, for level tables of
+ * at most 1,024 tile rows, a histogram of the splats' rect rows that phase 2 reads: keep it for phase 2.
  * Replaces render_triton.py:362-391 (_build_tiles up to the tot sync), :520-535 (param gathers) and the
  * octave routing / index_select of :950-962. */
-size_t splat_bin_count_workspace_bytes(int N);
+size_t splat_bin_count_workspace_bytes(int N, int H, int W, int TILE, const splat_levels *lv);
 int splat_bin_count(const float *mu, const float *scale, const float *theta, const float *opacity,
                     const float *color, int C, int N, int H, int W, int TILE, float cutoff,
                     const splat_levels *lv, int flags, float *rec, int *rect, int *offsets, long long *info, void *ws,
                     size_t ws_bytes, void *stream);
 
-/* Binning phase 2: expand rects into pairs, stable radix sort on the global tile id, CSR tile starts.
+/* Binning phase 2: the stable sort of the (tile, splat) pairs on the global tile id, and CSR tile starts. Level
+ * tables of at most 1,024 tile rows: a stable partition of the splats' rect rows ("units", 4-5x fewer than
+ * pairs) by tile row, from phase 1's row histogram in ws_count, then each row's units expanded column by
+ * column into the row's pairs; larger tables: expansion of the rects into pairs and radix passes on the tile
+ * id. ws_count is phase 1's workspace, as phase 1 left it.
  * gid_sorted[max(tot,1)] lists splat ids ordered by (tile, splat id); tile_starts[nt+1] with nt the total
  * tile count over all levels (splat_levels_geometry).
  * tot == 0 gives gid_sorted = {0} and all-zero starts, as the reference does.
@@ -91,15 +97,15 @@ int splat_bin_count(const float *mu, const float *scale, const float *theta, con
  * q in [offsets[g], offsets[g+1]), walking its rect row by row), used by the backward:
  * pair_splat[q] = splat of q, pair_q[i] = q of sorted pair i.
  * Replaces render_triton.py:392-409. */
-size_t splat_bin_pairs_workspace_bytes(int N, int nt, long long tot);
-int splat_bin_pairs(const int *rect, const int *offsets, int N, int H, int W, int TILE,
+size_t splat_bin_pairs_workspace_bytes(int N, int H, int W, int TILE, const splat_levels *lv, long long tot);
+int splat_bin_pairs(const int *rect, const int *offsets, const void *ws_count, int N, int H, int W, int TILE,
                     const splat_levels *lv, long long tot, int *gid_sorted, int *tile_starts,
                     int *pair_splat, int *pair_q, void *ws, size_t ws_bytes, void *stream);
 
 /* Binning in one call: phase 1 (splat_bin_count), one read of info into host memory info_host (2 + L int64),
  * then phase 2 (splat_bin_pairs). When info_host is pinned (hipHostMalloc) the offsets kernel writes the totals
  * into it directly; pageable memory gets a copy. With pair_cap > 0 (buffers for pair_cap pairs, ws_pairs
- * sized by splat_bin_pairs_workspace_bytes(N, nt, pair_cap)) phase 2 is queued BEFORE the host waits for
+ * sized by splat_bin_pairs_workspace_bytes(N, H, W, TILE, lv, pair_cap)) phase 2 is queued BEFORE the host waits for
  * the read: its kernels take the pair count from info on the device, so the GPU runs the pair phase while
  * the host checks the count; a count above pair_cap (or an error bit) makes that launch write an empty
  * list (starts 0, gid_sorted[0] = 0) and nothing else. With pair_cap = 0 the host waits first. The call
@@ -122,9 +128,10 @@ int splat_bin(const float *mu, const float *scale, const float *theta, const flo
  * count and pair-phase workspaces live in the library's own device scratch, a static array of 64 MiB per
  * GPU, held from the library's load until the process ends. The caller still passes every input and output
  * (rec, rect, offsets, info, info_host and the pair buffers for pair_cap >= 1 pairs). Limit: the workspaces
- * of N splats and pair_cap pairs must fit the scratch, about 25 bytes per pair (pair_cap up to ~2.6M for
- * TILE 8 at 768 x 768; the count workspace adds 104 bytes per 256 splats); a larger request returns status 5
- * before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device (per
+ * of N splats and pair_cap pairs (splat_bin_count_workspace_bytes + splat_bin_pairs_workspace_bytes) must
+ * fit the scratch: 12 bytes per pair plus 8 bytes per tile row and 256 splats for level tables of at most
+ * 1,024 tile rows (pair_cap up to ~5M at 768 x 768), about 25 bytes per pair past that; a larger request
+ * returns status 5 before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device (per
  * thread) looks up the scratch address and creates the read-back event. Statuses as splat_bin. Every call
  * on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams or threads before the
  * previous call's kernels have finished) race; calls in one stream do not. Nothing in the scratch needs to

@@ -24,14 +24,16 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.splat_abi_version() == 2
+    assert lib.splat_abi_version() == 3
 
 
 def test_workspace_queries_without_gpu():
     lib = _lib.load()
-    assert lib.splat_bin_count_workspace_bytes(92160) >= 8 * (92160 // 256)
-    # three pair-sized int32 arrays for C1's pair count plus histograms
-    assert lib.splat_bin_pairs_workspace_bytes(92160, 9216, 1_836_494) >= 3 * 4 * 1_836_494
+    assert lib.splat_bin_count_workspace_bytes(92160, 768, 768, 8, None) >= 8 * (92160 // 256)
+    # the row plan (96 tile rows): three unit arrays, at most one unit per pair
+    assert lib.splat_bin_pairs_workspace_bytes(92160, 768, 768, 8, None, 1_836_494) >= 3 * 4 * 1_836_494
+    # and its histogram of 96 rows x 360 decode blocks in the count workspace
+    assert lib.splat_bin_count_workspace_bytes(92160, 768, 768, 8, None) >= 8 * 96 * 360
     assert lib.splat_pair_sums_bytes(1_836_494) == 40 * 1_836_494
 
 

@@ -138,3 +138,61 @@ def test_speculative_budget_and_errors(dev):
     with pytest.raises(ValueError, match="empty tile rect"):
         RH._build_tiles(mu, -sc, s.H, s.W, 8, 3.0)
     check_equal(mu, sc, s.H, s.W, 8, 3.0)
+
+
+def splat_bin_maps(mu, sc, H, W, TILE, lv=None):
+    """splat_bin through the C-ABI with both pair maps requested (the renderer asks for pair_q only).
+    Returns tot, offsets, gid_sorted, tile_starts, pair_splat, pair_q as numpy arrays."""
+    lib = RH._lib.load()
+    dev = mu.device
+    N = mu.shape[1]
+    lvr = None if lv is None else RH._lib.ctypes.byref(lv)
+    geom, nt, _ = RH.levels_geometry(H, W, TILE, lv)
+    col = torch.zeros(N, 1, device=dev)
+    op = torch.zeros(N, device=dev)
+    rec = torch.empty(N, 16, device=dev)
+    rect = torch.empty(N, 4, dtype=torch.int32, device=dev)
+    off = torch.empty(N + 1, dtype=torch.int32, device=dev)
+    info = torch.empty(2 + len(geom), dtype=torch.int64, device=dev)
+    info_h = torch.zeros(2 + RH._lib.MAX_LEVELS, dtype=torch.int64, pin_memory=True)
+    ws1 = torch.empty(lib.splat_bin_count_workspace_bytes(N, H, W, TILE, lvr), dtype=torch.uint8, device=dev)
+    s = RH._lib.stream_ptr(dev)
+    p = RH._lib.ptr
+    rc = lib.splat_bin(p(mu[0]), p(sc[0]), None, p(op), p(col), 1, N, H, W, TILE, 3.0, lvr, 0, -1, p(rec), p(rect),
+                       p(off), p(info), info_h.data_ptr(), p(ws1), ws1.numel(), 0, None, None, None, None, None, 0, s)
+    tot = int(info_h[0])
+    assert rc == RH._lib.STATUS_CAPACITY or (rc == 0 and tot == 0)
+    i32 = lambda n: torch.full((max(n, 1),), -1, dtype=torch.int32, device=dev)
+    gid, starts, psplat, pq = i32(tot), i32(nt + 1), i32(tot), i32(tot)
+    ws2 = torch.empty(lib.splat_bin_pairs_workspace_bytes(N, H, W, TILE, lvr, tot), dtype=torch.uint8, device=dev)
+    RH._lib.check(lib.splat_bin_pairs(p(rect), p(off), p(ws1), N, H, W, TILE, lvr, tot, p(gid), p(starts), p(psplat),
+                                      p(pq), p(ws2), ws2.numel(), s), "splat_bin_pairs")
+    torch.cuda.synchronize()
+    return tot, off.cpu().numpy(), gid.cpu().numpy(), starts.cpu().numpy(), psplat.cpu().numpy(), pq.cpu().numpy()
+
+
+@pytest.mark.parametrize("H,W,TILE,n,ls_px", [(768, 768, 8, 20000, 3.0), (200, 120, 4, 3000, 6.0),
+                                              (2100, 2100, 8, 20000, 3.0), (64, 64, 2, 5000, 20.0)])
+def test_pair_maps(dev, H, W, TILE, n, ls_px):
+    """The backward's maps between sorted and splat-major pair order: pair_splat lists each splat's pairs in
+    splat order, pair_q is a permutation with pair_splat[pair_q[i]] = gid_sorted[i], and splat-major pair q of
+    splat g (k = q - offsets[g] walks the rect row by row, render_triton.py:396-404) lies in the tile of its
+    sorted position. Checked against the oracle's rects; the last case is a wide rect per row (list overflow
+    of the row expansion's LDS stash)."""
+    mu, ls, *_ = random_scene(n, H, W, seed=H + n, dev=dev, ls_mean_px=ls_px, margin=0.1)
+    sc = activate_scale(ls)
+    tot, off, gid, st, psplat, pq = splat_bin_maps(mu, sc, H, W, TILE)
+    gid_o, st_o = c_oracle.build_tiles(np_(mu[0]), np_(sc[0]), H, W, TILE, 3.0)
+    assert np.array_equal(st, st_o) and np.array_equal(gid[:tot], gid_o[:tot])
+    assert np.array_equal(psplat[:tot], np.repeat(np.arange(n), np.diff(off)))
+    assert np.array_equal(np.sort(pq[:tot]), np.arange(tot))
+    assert np.array_equal(psplat[pq[:tot]], gid[:tot])
+    tx0, tx1, ty0, ty1, _ = c_oracle.rects(np_(mu[0]), np_(sc[0]), H, W, TILE, 3.0)
+    ntx = (W + TILE - 1) // TILE
+    q = pq[:tot].astype(np.int64)
+    g = gid[:tot]
+    w = (tx1 - tx0 + 1)[g]
+    k = q - off[g]
+    tile_q = (ty0[g] + k // w) * ntx + tx0[g] + k % w
+    tile_i = np.repeat(np.arange(len(st) - 1), np.diff(st))
+    assert np.array_equal(tile_q, tile_i)

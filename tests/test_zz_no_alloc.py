@@ -51,8 +51,12 @@ def assert_same(ref, got, info):
     assert torch.equal(got["rect"], ref.rect_b[0]), "rects"
     assert torch.equal(got["off"], ref.off_b[0]), "offsets"
     assert torch.equal(got["starts"], ref.starts_b[0]), "tile starts"
-    for k, r in (("gid", ref.gid_b[0]), ("psplat", ref.psplat_b[0]), ("pq", ref.pq_b[0])):
+    for k, r in (("gid", ref.gid_b[0]), ("pq", ref.pq_b[0])):
         assert torch.equal(got[k][:tot], r[:tot]), k
+    # pair_splat (not requested by the renderer): the splat of every splat-major pair
+    off = ref.off_b[0].long()
+    want = torch.repeat_interleave(torch.arange(off.numel() - 1, device=off.device), off[1:] - off[:-1])
+    assert torch.equal(got["psplat"][:tot].long(), want), "pair_splat"
 
 
 def test_noalloc_matches_splat_bin_twice(dev):
@@ -82,7 +86,7 @@ def test_noalloc_limits(dev):
     ref = reference_bins(*args, None)
     tot = ref.tot_b[0]
     # a pair capacity whose workspace exceeds the scratch: refused before any launch
-    rc, _, _ = noalloc_bins(*args, None, 40_000_000)
+    rc, _, _ = noalloc_bins(*args, None, 60_000_000)
     assert rc == _lib.STATUS_WORKSPACE and b"scratch" in _lib.load().splat_last_error()
     # a count above the caller's buffers: status 6 with the count in info_host, the pair list left empty
     rc, got, info = noalloc_bins(*args, None, tot - 1)
