@@ -36,6 +36,8 @@ def test_configs_bit_exact(dev, name, TILE):
     (2100, 2100, 8, 3.0, 20000, 0.0),  # 69,169 tiles: 17-bit keys, two 9-bit radix passes
     (1000, 700, 8, 3.0, 20000, 0.05),  # 11,000 tiles: two-phase sort on a ragged super-tile range
     (6000, 100, 8, 3.0, 20000, 0.0),   # 9,750 tiles: two-phase sort, super-tiles spanning several tile rows
+    (8400, 40, 8, 3.0, 6000, 0.0),     # 1,050 tile rows: past the row plan's 1,024, the pair-sort plans
+    (4200, 24, 4, 3.0, 6000, 0.1),     # 1,050 tile rows of 6 tiles
 ])
 def test_edge_cases_bit_exact(dev, H, W, TILE, cutoff, n, margin):
     mu, ls, *_ = random_scene(n, H, W, seed=H + W + n, dev=dev, margin=margin, B=2)
@@ -196,3 +198,11 @@ def test_pair_maps(dev, H, W, TILE, n, ls_px):
     tile_q = (ty0[g] + k // w) * ntx + tx0[g] + k % w
     tile_i = np.repeat(np.arange(len(st) - 1), np.diff(st))
     assert np.array_equal(tile_q, tile_i)
+
+
+def test_many_splats_separate_scan_launches(dev):
+    """1.2M splats (4,688 decode blocks): the offsets take the two-launch scan and the row histogram its own
+    scan launch; pair list and starts against the oracle."""
+    H = W = 1024
+    mu, ls, *_ = random_scene(1_200_000, H, W, seed=71, dev=dev, ls_mean_px=0.8, ls_std=0.3)
+    check_equal(mu, activate_scale(ls), H, W, 8, 3.0)
