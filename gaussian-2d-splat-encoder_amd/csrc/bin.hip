@@ -1609,6 +1609,44 @@ int splat_bin_pairs(const int* rect, const int* offsets, const void* ws_count, i
                           ws, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The one read of a binning's totals (info_host[0, 2 + nlev)): waits for the read-back event recorded behind the
+// count phase, takes a copy when the count kernel's stores into pinned memory were not seen, and applies the
+// checks of splat_bin: error bits, the per-level budget, the capacity.
+int read_totals(const char* who, long long* info_host, const long long* info, int nlev, long long max_pairs,
+                long long pair_cap, hipStream_t st) {
+  const int ninfo = 2 + nlev;
+  hipEvent_t ev = readback_event();
+  if (!ev || hipEventSynchronize(ev) != hipSuccess) return set_error(kHipError, "%s: reading the pair totals failed", who);
+  if (host_mirror(info_host)) {
+    volatile long long* ih = info_host;
+    bool seen = true;
+    for (int i = 0; i < ninfo; ++i) seen = seen && ih[i] != kUnsetInfo;
+    if (!seen) {   // the kernel's stores did not reach the host: this call copies them (the next tries again)
+      if (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return set_error(kHipError, "%s: reading the pair totals failed", who);
+    }
+  }
+  const long long tot = info_host[0];
+  if (info_host[1] & 1) return set_error(kInvalid, "%s: a splat has an empty tile rect (negative cutoff or scale)", who);
+  if (info_host[1] & 2) return set_error(kOverflow, "%s: %lld pairs exceed the int32 pair index range", who, tot);
+  if (max_pairs >= 0)
+    for (int l = 0; l < nlev; ++l)
+      if (info_host[2 + l] > max_pairs)
+        return set_error(kBudget, "%s: %lld pairs on level %d exceed the budget of %lld", who, info_host[2 + l], l,
+                         max_pairs);
+  if (tot > pair_cap) return set_error(kCapacity, "%s: %lld pairs exceed the capacity %lld", who, tot, pair_cap);
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" {
+
 int splat_bin(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color, int C,
               int N, int H, int W, int TILE, float cutoff, const splat_levels* lv, int flags, long long max_pairs,
               float* rec, int* rect, int* offsets, long long* info, long long* info_host, void* ws_count, size_t ws_count_bytes,
@@ -1616,13 +1654,20 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
               size_t ws_pairs_bytes, void* stream) {
   if (N < 1 || C < 1 || C > kMaxC || H < 1 || W < 1 || TILE < 1 || pair_cap < 0)
     return set_error(kInvalid, "splat_bin: N=%d C=%d H=%d W=%d TILE=%d cap=%lld", N, C, H, W, TILE, pair_cap);
-  if (flags & ~kFlagLogScale) return set_error(kInvalid, "splat_bin: unknown flags 0x%x", flags);
+  if (flags & ~(kFlagLogScale | kFlagDefer)) return set_error(kInvalid, "splat_bin: unknown flags 0x%x", flags);
   LevelTable L;
   Routing R;
   if (make_levels(H, W, TILE, lv, &L, &R)) return set_error(kInvalid, "splat_bin: bad levels");
   if (!mu || !scale || !opacity || !color || !rec || !rect || !offsets || !info || !info_host)
     return set_error(kInvalid, "splat_bin: null pointer");
   if (ws_count_bytes < plan_count(L, N).total) return set_error(kWorkspace, "splat_bin: count workspace too small");
+  // With buffers for pair_cap > 0 pairs the pair phase is queued before the host waits for the count: the GPU
+  // goes on with it while the host reads the count (kernels past the count, or past pair_cap, do nothing).
+  const bool spec = pair_cap > 0 && pair_cap <= 0x7fffffffLL - 64 && gid_sorted && tile_starts &&
+                    ws_pairs_bytes >= pairs_ws_bytes(L, N, pair_cap);
+  const bool defer = flags & kFlagDefer;
+  if (defer && !spec)
+    return set_error(kInvalid, "splat_bin: a deferred read needs pair buffers and workspace for pair_cap > 0 pairs");
   hipStream_t st = (hipStream_t)stream;
   // the one device -> host read of the render (totals and error bits): the offsets kernel writes them into
   // info_host itself when it is pinned memory, else they are copied. Entries the kernel has not written keep
@@ -1640,39 +1685,28 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
       (!mirror && hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess) ||
       hipEventRecord(ev, st) != hipSuccess)
     return set_error(kHipError, "splat_bin: queueing the read of the pair totals failed");
-  // With buffers for pair_cap > 0 pairs the pair phase is queued before the host waits for the count: the GPU
-  // goes on with it while the host reads the count (kernels past the count, or past pair_cap, do nothing).
-  const bool spec = pair_cap > 0 && pair_cap <= 0x7fffffffLL - 64 && gid_sorted && tile_starts &&
-                    ws_pairs_bytes >= pairs_ws_bytes(L, N, pair_cap);
   if (spec) {
     rc = bin_pairs_launch(rect, offsets, ws_count, N, L, (int)pair_cap, info, gid_sorted, tile_starts, pair_splat, pair_q,
                           ws_pairs, st);
     if (rc) return rc;
   }
-  if (hipEventSynchronize(ev) != hipSuccess) return set_error(kHipError, "splat_bin: reading the pair totals failed");
-  if (mirror) {
-    bool seen = true;
-    for (int i = 0; i < ninfo; ++i) seen = seen && ih[i] != kUnsetInfo;
-    if (!seen) {   // the kernel's stores did not reach the host: this call copies them (the next tries again)
-      if (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
-          hipStreamSynchronize(st) != hipSuccess)
-        return set_error(kHipError, "splat_bin: reading the pair totals failed");
-    }
-  }
+  if (defer) return kOk;   // splat_bin_finish reads the totals
+  rc = read_totals("splat_bin", info_host, info, L.n, max_pairs, pair_cap, st);
+  if (rc != kOk || spec) return rc;
+  // tot <= pair_cap without a speculative launch (no pairs with pair_cap = 0, or a workspace too small for
+  // pair_cap pairs): the pair phase for the count just read
   const long long tot = info_host[0];
-  if (info_host[1] & 1) return set_error(kInvalid, "splat_bin: a splat has an empty tile rect (negative cutoff or scale)");
-  if (info_host[1] & 2) return set_error(kOverflow, "splat_bin: %lld pairs exceed the int32 pair index range", tot);
-  if (max_pairs >= 0)
-    for (int l = 0; l < L.n; ++l)
-      if (info_host[2 + l] > max_pairs)
-        return set_error(kBudget, "splat_bin: %lld pairs on level %d exceed the budget of %lld", info_host[2 + l], l,
-                         max_pairs);
-  if (tot > pair_cap) return set_error(kCapacity, "splat_bin: %lld pairs exceed the capacity %lld", tot, pair_cap);
-  if (spec) return kOk;
   if (!gid_sorted || !tile_starts) return set_error(kInvalid, "splat_bin: null pair buffers");
   if (ws_pairs_bytes < pairs_ws_bytes(L, N, tot)) return set_error(kWorkspace, "splat_bin: pair workspace too small");
   return bin_pairs_launch(rect, offsets, ws_count, N, L, (int)tot, nullptr, gid_sorted, tile_starts, pair_splat, pair_q, ws_pairs,
                           st);
+}
+
+int splat_bin_finish(long long* info_host, const long long* info, int nlev, long long max_pairs, long long pair_cap,
+                     void* stream) {
+  if (!info_host || !info || nlev < 1 || nlev > kMaxLevels || pair_cap < 0)
+    return set_error(kInvalid, "splat_bin_finish: nlev=%d cap=%lld", nlev, pair_cap);
+  return read_totals("splat_bin_finish", info_host, info, nlev, max_pairs, pair_cap, (hipStream_t)stream);
 }
 
 int splat_bin_noalloc(const float* mu, const float* scale, const float* theta, const float* opacity, const float* color,

@@ -774,14 +774,16 @@ __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ re
 // Backward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
 // Composite (level 0): upstream from T/asum/fg/gout (see pixel_upstream for UPS); per-tile partials of
 // sum_p gout * T go to bg_part[c * ntiles + (t - tb0)]. FIELDS: upstream from the packed fields.
-// One wave per tile: the per-pixel upstream terms are staged in LDS, then the wave takes the tile's pairs
-// 64 at a time (lane = pair) in the moment form, the pairs that need the direct form in passes of their own.
+// S waves per tile (S = 1, or 16 with kFlagWide for few tiles with long pair lists: the dense coarse levels of
+// an octave render): the per-pixel upstream terms are staged in LDS once for the tile, then each wave takes a
+// contiguous share of the tile's pair list (every pair's sums are independent) 64 at a time (lane = pair) in
+// the moment form, the pairs that need the direct form in passes of their own.
 // The last r < 64 pairs of a pass get L lanes each (the largest power of two with r L <= 64), each lane
 // covering a 1/L share of the tile's pixels (whole rows when that share is at least a row) and the L partial
 // sums are combined with xor shuffles. At 5 waves per SIMD (at most 96 VGPRs, no spills) there are enough waves
 // to cover the latency of the VALU, LDS and transcendental pipes.
-template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_bwd_cull(
+template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE, int S>
+__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
@@ -793,14 +795,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   __shared__ float4 s_pb[TILE * RS];
   __shared__ float s_ly[TILE], s_lx[TILE];
   __shared__ float s_lyc[TILE];
-  __shared__ int s_defer[128], s_mi[128];
-  __shared__ float2 s_muv[128];
+  __shared__ int s_defer_w[S][128], s_mi_w[S][128];
+  __shared__ float2 s_muv_w[S][128];
   const TileAt ta = tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
   const int t = ta.t;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wid = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;   // wave-uniform
+  int* s_defer = s_defer_w[wid];
+  int* s_mi = s_mi_w[wid];
+  float2* s_muv = s_muv_w[wid];
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
-  for (int l = lane; l < NP; l += 64) {
+  for (int l = (int)threadIdx.x; l < NP; l += 64 * S) {
     const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
     if (yp < ta.H && xp < ta.W) {
@@ -812,11 +818,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
     s_pa[k] = pa;
     s_pb[k] = pb;
   }
-  if (!FIELDS && bg_part) {
+  if (!FIELDS && bg_part) {   // the tile's partial sums, waves added in wave order
+    __shared__ float s_bgw[S][kMaxC];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const float v = wave_sum(bgp[c]);
-      if (lane == 0) bg_part[(size_t)c * ntiles + (t - tb0)] = v;
+      if (lane == 0) s_bgw[wid][c] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < C) {
+      float v = 0.f;
+      for (int w = 0; w < S; ++w) v += s_bgw[w][threadIdx.x];
+      bg_part[(size_t)threadIdx.x * ntiles + (t - tb0)] = v;
     }
   }
   // the tile's first and last pixel centres (render_triton.py:455-456) and the per-row / per-column offsets
@@ -825,7 +838,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   const float px0 = uniform_f(((float)(ta.tx * TILE) + 0.5f) / fW);
   const float py1 = uniform_f(((float)(ta.ty * TILE + TILE - 1) + 0.5f) / fH);
   const float px1 = uniform_f(((float)(ta.tx * TILE + TILE - 1) + 0.5f) / fW);
-  if (lane < TILE) {
+  if (threadIdx.x < TILE) {
     s_ly[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / fH - py0;
     s_lx[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW - px0;
   }
@@ -837,12 +850,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5))) void k_
   co.tx = px0 + co.cx;
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) co.lx[xx] = uniform_f(s_lx[xx] - co.cx);
-  if (lane < TILE) {
+  if (threadIdx.x < TILE) {
     const float ly = s_ly[lane] - co.cy;
     s_lyc[lane] = ly;
   }
   __syncthreads();
-  const int g0 = starts[t], g1 = starts[t + 1];
+  int g0 = starts[t], g1 = starts[t + 1];
+  if (S > 1) {   // this wave's share of the tile's pairs
+    const int chunk = (g1 - g0 + S - 1) / S;
+    g0 = min(g1, g0 + wid * chunk);
+    g1 = min(g1, g0 + chunk);
+  }
   const unsigned long long below = (1ull << lane) - 1ull;
   // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (falloff below
   // 2^-kCullLog2 at every pixel centre: a zero record), near-opaque (summed by careful_pair at once), small
@@ -1483,10 +1501,13 @@ int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_st
     return with_tile(TILE, [&](auto tt) {
       return with_flags(flags, [&](auto fl, auto od, auto up) {
         constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
-        launch_tile_kernel(k_bwd_cull<CC, decltype(fl)::value != 0, decltype(od)::value != 0,
-                                      decltype(up)::value != 0, TT>,
-                           ntiles, 64, st, rec, gid_sorted, tile_starts, L, tb0, ntiles, bg, T, asum, fg, gout, dslog,
-                           dsa, dsac, pair_q, pair_sums, bg_part);
+        constexpr bool FL = decltype(fl)::value != 0, OD = decltype(od)::value != 0, UP = decltype(up)::value != 0;
+        if (TT == 8 && (flags & kFlagWide))
+          launch_tile_kernel(k_bwd_cull<CC, FL, OD, UP, TT, 16>, ntiles, 64 * 16, st, rec, gid_sorted, tile_starts, L,
+                             tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part);
+        else
+          launch_tile_kernel(k_bwd_cull<CC, FL, OD, UP, TT, 1>, ntiles, 64, st, rec, gid_sorted, tile_starts, L, tb0,
+                             ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part);
         return check_launch("k_bwd_cull");
       });
     });

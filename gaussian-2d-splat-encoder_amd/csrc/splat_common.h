@@ -41,8 +41,9 @@ constexpr float kNearOpaque = 0.9f;
 constexpr int kFlagFields = 1;   // write raw partial sums (S_log, S_a, S_ac) instead of the composite
 constexpr int kFlagOdds = 2;     // weight colour by the odds a / (1 - a) instead of a
 constexpr int kFlagUps = 4;      // composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a
-constexpr int kFlagWide = 8;     // forward of 8x8 tiles: 16 waves per tile instead of 4 (long pair lists)
+constexpr int kFlagWide = 8;     // 8x8 tiles: 16 waves per tile (forward: instead of 4, backward: instead of 1)
 constexpr int kFlagLogScale = 16; // binning: `scale` holds raw log-scales, activated by the decode pass
+constexpr int kFlagDefer = 32;    // splat_bin: return once everything is queued; splat_bin_finish reads the totals
 
 // Status codes of the C-ABI.
 enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2, kUnsupported = 3, kOverflow = 4, kWorkspace = 5,

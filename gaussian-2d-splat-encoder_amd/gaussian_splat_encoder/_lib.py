@@ -44,6 +44,7 @@ _SIGS = {
     "splat_bin": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP, _VP, _SZ,
                        _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_bin_pairs": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _LV, _LL, _VP, _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "splat_bin_finish": (_I, [_VP, _VP, _I, _LL, _LL, _VP]),
     "splat_bin_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _F, _LV, _I, _LL, _VP, _VP, _VP, _VP, _VP,
                                _LL, _VP, _VP, _VP, _VP, _VP]),
     "splat_time_next_launch": (_I, [_VP, _VP]),
@@ -68,6 +69,7 @@ FLAG_ODDS = 2
 FLAG_UPS = 4
 FLAG_WIDE = 8
 FLAG_LOG_SCALE = 16
+FLAG_DEFER = 32
 MAX_LEVELS = 12   # kMaxLevels of the library
 
 STATUS_WORKSPACE = 5

@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from ._lib import FLAG_FIELDS, FLAG_LOG_SCALE, FLAG_ODDS, FLAG_UPS, FLAG_WIDE, SplatLevels, check, ptr
+from ._lib import FLAG_DEFER, FLAG_FIELDS, FLAG_LOG_SCALE, FLAG_ODDS, FLAG_UPS, FLAG_WIDE, SplatLevels, check, ptr
 from .params import activate_scale
 from .render import _pixels
 
@@ -146,6 +146,7 @@ class TileBins:
         self.H, self.W, self.TILE, self.ntx, self.nt = H, W, TILE, ntx, nt
         self.blocks, self.pairs, self.with_maps = blocks, pairs, with_maps
         self.lv, self.geom, self.npix, self.level_tot_b = lv, geom, npix, level_tot_b
+        self.pending = None   # a _Pending while the pair count of a deferred binning is unread
         self._views = {}
 
     def p(self, b, name):
@@ -198,13 +199,16 @@ class TileBins:
 
     def level_mask(self, b):
         """Levels of batch b holding pairs, with level 0 always set (the composite covers every pixel)."""
-        if self.level_tot_b is None:
-            return 1
-        m = 1
-        for l, n in enumerate(self.level_tot_b[b]):
-            if n > 0:
-                m |= 1 << l
-        return m
+        return 1 if self.level_tot_b is None else _mask_of(self.level_tot_b[b])
+
+
+def _mask_of(lt):
+    """Level mask of per-level pair totals lt: the levels holding pairs, and level 0."""
+    m = 1
+    for l, n in enumerate(lt):
+        if n > 0:
+            m |= 1 << l
+    return m
 
 
 def levels_geometry(H, W, TILE, lv):
@@ -231,6 +235,7 @@ def _lv_key(lv):
 
 _GEOM = {}          # (H, W, TILE, levels) -> levels_geometry result
 _PAIRS_HW = {}      # binning configuration -> most pairs one image needed so far (sizes the next capacity)
+_LEVELS_SEEN = {}   # binning configuration -> per-level pair totals of its last binning (plans deferred launches)
 _tls = threading.local()
 
 
@@ -271,16 +276,19 @@ class _Carve:
 
 
 def _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs=None, with_maps=True, lv=None,
-         scale_is_log=False) -> TileBins:
+         scale_is_log=False, defer=False) -> TileBins:
     """Decode + bin every batch (render_triton.py:351-409). One host read of the pair totals per image.
     with_maps=False skips the pair maps only the backward needs (forward-only renders). `lv` (a
     _lib.SplatLevels) routes splats to levels (octave / coarse-fine renders, render_triton.py:879-980).
-    scale_is_log: `scale` holds fp32 raw log-scales, activated in the decode pass (params.py:18-28)."""
+    scale_is_log: `scale` holds fp32 raw log-scales, activated in the decode pass (params.py:18-28).
+    defer: for one image whose configuration has been binned before, return with the read of the pair count
+    still pending (bins.pending): the caller queues its launches on the speculative pair list first, then calls
+    _finish (which redoes the pair phase when the count exceeded the capacity)."""
     _dev_check(mu, scale, color, opacity, theta)
     ev = kernel_timer.record("bin")
     try:
         return _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv,
-                         FLAG_LOG_SCALE if scale_is_log else 0)
+                         FLAG_LOG_SCALE if scale_is_log else 0, defer)
     finally:
         kernel_timer.close("bin", ev)
 
@@ -300,7 +308,49 @@ def _pair_buffers(lib, N, nt, cap, with_maps, dev, geo):
     return _Carve([4 * c, 4 * (nt + 1), 4 * m, lib.splat_bin_pairs_workspace_bytes(N, *geo, cap)], dev)
 
 
-def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv, sflags):
+class _Pending:
+    """A binning whose pair count has not been read yet (FLAG_DEFER): what settling it needs."""
+
+    __slots__ = ("lib", "info_p", "info_np", "blk", "cap", "budget", "key", "geo", "N", "L", "nt", "geom", "cutoff",
+                 "max_pairs", "with_maps", "stream", "dev")
+
+    def __init__(self, **kw):
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+def _settle(p, rc, pb):
+    """The checks after the read of one image's totals (p: a _Pending): raises for the budget and bad rects,
+    redoes the pair phase with exact buffers when the count exceeded the capacity. Returns (pair buffers, tot,
+    level totals, redone)."""
+    lib, info_np, L, geom = p.lib, p.info_np, p.L, p.geom
+    H, W, TILE, lvr = p.geo
+    tot = int(info_np[0])
+    lt = info_np[2:2 + L].tolist()
+    if rc == _lib.STATUS_BUDGET:
+        l = max(range(L), key=lambda i: lt[i])
+        Hl, Wl = (H, W) if geom is None else geom[l][:2]
+        raise _budget_error(lt[l], p.max_pairs, Hl, Wl, TILE, p.cutoff, p.N)
+    if rc == 1 and info_np[1] & 1:
+        raise ValueError("binning: a splat has an empty tile rect (negative cutoff or scale)")
+    if rc == 4:
+        raise PairBudgetExceeded(f"binning: {tot} pairs exceed the int32 pair index range")
+    redone = rc == _lib.STATUS_CAPACITY
+    if redone:
+        pb = _pair_buffers(lib, p.N, p.nt, tot, p.with_maps, p.dev, p.geo)
+        blk = p.blk
+        check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), blk.ptr(4), p.N, H, W, TILE, lvr, tot, pb.ptr(0), pb.ptr(1),
+                                  None, pb.ptr(2) if p.with_maps else None, pb.ptr(3), pb.nbytes(3), p.stream),
+              "splat_bin_pairs")
+    else:
+        check(rc, "splat_bin")
+    if tot > _PAIRS_HW.get(p.key, 0):
+        _PAIRS_HW[p.key] = tot
+    _LEVELS_SEEN[p.key] = lt
+    return pb, tot, lt, redone
+
+
+def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv, sflags, defer=False):
     B, N, C = color.shape
     dev = mu.device
     lib = _lib.load()
@@ -324,6 +374,7 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     geo = (H, W, TILE, lvr)
     ws1_bytes = lib.splat_bin_count_workspace_bytes(N, *geo)
     budget = -1 if max_pairs is None else int(max_pairs)
+    defer = defer and B == 1 and cap > 0
     blocks, pairs, tots, level_tots = [], [], [], []
     for b in range(B):
         blk = _Carve([64 * N, 16 * N, 4 * (N + 1), 8 * (2 + L), ws1_bytes], dev)
@@ -331,33 +382,47 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         pp = (lambda i: None) if pb is None else pb.ptr
         info_np[0] = info_np[1] = 0
         rc = lib.splat_bin(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]), ptr(col_[b]),
-                           C, N, H, W, TILE, float(cutoff), lvr, sflags, budget, blk.ptr(0), blk.ptr(1), blk.ptr(2),
-                           blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0), pp(1),
-                           None, pp(2) if with_maps else None, pp(3), 0 if pb is None else pb.nbytes(3), stream)
-        tot = int(info_np[0])
-        lt = info_np[2:2 + L].tolist()
-        if rc == _lib.STATUS_BUDGET:
-            l = max(range(L), key=lambda i: lt[i])
-            Hl, Wl = (H, W) if geom is None else geom[l][:2]
-            raise _budget_error(lt[l], max_pairs, Hl, Wl, TILE, cutoff, N)
-        if rc == 1 and info_np[1] & 1:
-            raise ValueError("binning: a splat has an empty tile rect (negative cutoff or scale)")
-        if rc == 4:
-            raise PairBudgetExceeded(f"binning: {tot} pairs exceed the int32 pair index range")
-        if rc == _lib.STATUS_CAPACITY:
-            pb = _pair_buffers(lib, N, nt, tot, with_maps, dev, geo)
-            check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), blk.ptr(4), N, H, W, TILE, lvr, tot, pb.ptr(0), pb.ptr(1),
-                                      None, pb.ptr(2) if with_maps else None, pb.ptr(3), pb.nbytes(3), stream),
-                  "splat_bin_pairs")
-        else:
+                           C, N, H, W, TILE, float(cutoff), lvr, sflags | (FLAG_DEFER if defer else 0), budget,
+                           blk.ptr(0), blk.ptr(1), blk.ptr(2), blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0),
+                           pp(1), None, pp(2) if with_maps else None, pp(3), 0 if pb is None else pb.nbytes(3), stream)
+        pend = _Pending(lib=lib, info_p=info_p, info_np=info_np, blk=blk, cap=cap, budget=budget, key=key, geo=geo, N=N,
+                        L=L, nt=nt, geom=geom, cutoff=cutoff, max_pairs=max_pairs, with_maps=with_maps, stream=stream,
+                        dev=dev)
+        if defer:
             check(rc, "splat_bin")
-        if tot > hw:
-            _PAIRS_HW[key] = hw = tot
+            bins = TileBins(N, [None], H, W, TILE, ntx, nt, [blk], [pb], with_maps, lv, geom, npix, [None])
+            bins.pending = pend
+            return bins
+        pb, tot, lt, _ = _settle(pend, rc, pb)
         blocks.append(blk)
         pairs.append(pb)
         tots.append(tot)
         level_tots.append(lt)
     return TileBins(N, tots, H, W, TILE, ntx, nt, blocks, pairs, with_maps, lv, geom, npix, level_tots)
+
+
+def _finish(bins):
+    """Reads the totals of a deferred binning (one image) and settles it; True when its pair phase had to be
+    redone (the count exceeded the speculated capacity), so that launches queued on the speculative pair list
+    must be repeated."""
+    p = bins.pending
+    if p is None:
+        return False
+    bins.pending = None
+    rc = p.lib.splat_bin_finish(p.info_p, p.blk.ptr(3), p.L, p.budget, p.cap, p.stream)
+    pb, tot, lt, redone = _settle(p, rc, bins.pairs[0])
+    bins.pairs[0] = pb
+    bins.tot_b[0] = tot
+    bins.level_tot_b[0] = lt
+    bins._views = {}
+    return redone
+
+
+def _speculated_levels(bins):
+    """Per-level pair totals to plan the launches of a deferred binning by: the last totals of this configuration."""
+    if bins.pending is None:
+        return bins.level_tot_b[0]
+    return _LEVELS_SEEN.get(bins.pending.key)
 
 
 def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
@@ -370,14 +435,14 @@ def _build_tiles(mu, scale, H, W, TILE, cutoff, max_pairs=None):
 
 # ----------------------------------------------------------------------------------------------- cull path
 def _wide(TILE, ntiles, pairs):
-    """FLAG_WIDE (16 waves per 8x8 tile instead of 4) for a forward launch over few tiles with long pair lists,
-    where 4 waves per tile would leave most of the GPU idle."""
+    """FLAG_WIDE (16 waves per 8x8 tile instead of 4 in the forward, instead of 1 in the backward) for a launch over
+    few tiles with long pair lists, where fewer waves per tile would leave most of the GPU idle."""
     return FLAG_WIDE if TILE == 8 and 0 < ntiles < 2048 and pairs >= 128 * ntiles else 0
 
 
 def _dense_levels(bins, lt, mask):
-    """Coarse levels (>= 1, present in `mask`) whose tiles hold long pair lists: each gets a forward launch of
-    its own with FLAG_WIDE; the other coarse levels share one launch."""
+    """Coarse levels (>= 1, present in `mask`) whose tiles hold long pair lists: each gets a forward and a backward
+    launch of its own with FLAG_WIDE; the other coarse levels share one launch."""
     if bins.TILE != 8:
         return []
     geom, L = bins.geom, bins.n_levels
@@ -412,18 +477,28 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
     B, N, C = color.shape
     P = H * W
     dev = mu.device
-    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, scale_is_log=scale_is_log)
+    bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, scale_is_log=scale_is_log,
+                defer=True)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     bgf = _f32(bg)
     flags = FLAG_ODDS if odds else 0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
-    for b in range(B):
-        ev = kernel_timer.record("fwd")
-        try:
-            _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, bins.tot_b[b]), (0, 1), 1,
-                        (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
-        finally:
-            kernel_timer.close("fwd", ev)
+
+    def launch(tots):
+        for b in range(B):
+            ev = kernel_timer.record("fwd")
+            try:
+                _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, tots[b]), (0, 1), 1,
+                            (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
+            finally:
+                kernel_timer.close("fwd", ev)
+
+    if bins.pending is not None:   # queued on the speculative pair list before the count is read
+        launch([_speculated_levels(bins)[0]])
+        if _finish(bins):
+            launch(bins.tot_b)
+    else:
+        launch(bins.tot_b)
     return out, (T, asum, fg), bins
 
 
@@ -452,7 +527,7 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     P = H * W
     dev = mu.device
     bins = _bin(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, with_maps, lv=lv,
-                scale_is_log=scale_is_log)
+                scale_is_log=scale_is_log, defer=True)
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     L = bins.n_levels
     # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
@@ -462,9 +537,10 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     odd = FLAG_ODDS if odds else 0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     nt0 = bins.ntiles0
-    for b in range(B):
-        mask = bins.level_mask(b)
-        lt = bins.level_tot_b[b]
+
+    def launch(b, lt, mask):
+        """The launches of image b for per-level pair totals lt (to pick the 16-wave launches) over the levels in
+        mask (a level in mask that holds no pair renders zeros)."""
         ev = kernel_timer.record("fwd")
         try:
             if mask & ~1:
@@ -479,6 +555,17 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
                         (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
         finally:
             kernel_timer.close("fwd", ev)
+
+    if bins.pending is not None:   # queued on the speculative pair list and levels before the count is read
+        lt_spec = _speculated_levels(bins)
+        mask_spec = _mask_of(lt_spec)
+        launch(0, lt_spec, mask_spec)
+        redone = _finish(bins)
+        if redone or bins.level_mask(0) & ~mask_spec:
+            launch(0, bins.level_tot_b[0], bins.level_mask(0))
+    else:
+        for b in range(B):
+            launch(b, bins.level_tot_b[b], bins.level_mask(b))
     return out, (T, asum, fg), bins
 
 
@@ -541,6 +628,7 @@ def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream, lsc=N
     reduction into `grads`."""
     dev = bins.blocks[b].buf.device
     sums, bg_part = _bwd_buffers(lib, bins, b, C, g_bg is not None, dev)
+    flags |= _wide(bins.TILE, bins.nt, bins.tot_b[b])
     ev = kernel_timer.record("bwd")
     try:
         _render_bwd(lib, bins, b, C, flags, (0, 1), 1, upstream, sums, bg_part, stream)
@@ -596,33 +684,42 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
     log-scales of a scale_is_log binning (g_scale is then w.r.t. them)."""
     B, N, C = color.shape
     dev = color.device
-    grads = _grads_out(B, N, C, dev, has_theta)
-    g_bg = _empty((B, C), dev)
+    g_mu, g_scale, g_col, g_op, g_th, g_bg = _grads_bg_out(B, N, C, dev, has_theta)
+    grads = (g_mu, g_scale, g_col, g_op, g_th)
     go, bgf = _f32(grad_out), _f32(bg)
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     odd = FLAG_ODDS if odds else 0
     L = bins.n_levels
     npix = bins.npix if L > 1 else bins.H * bins.W
-    dS = (_empty((npix,), dev), _empty((npix,), dev), _empty((npix, C), dev))    # reused across the batch
+    dsb = _empty((npix * (2 + C),), dev)   # the pixel upstream dS_log, dS_a, dS_ac, reused across the batch
+    dS = (dsb[:npix], dsb[npix:2 * npix], dsb[2 * npix:].view(npix, C))
     lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
     adj_ws = _ws(lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr), dev) if L > 1 \
         else None
     lsc = None if log_scale is None else _f32(log_scale)
+    nt0 = bins.ntiles0
     for b in range(B):
         mask = bins.level_mask(b)
+        lt = bins.level_tot_b[b]
         sums, bg_part = _bwd_buffers(lib, bins, b, C, True, dev)
         ev = kernel_timer.record("bwd")
         try:
-            _render_bwd(lib, bins, b, C, FLAG_UPS | odd, (0, 1), mask, (bgf[b], T[b], asum[b], fg[b], go[b], *dS),
-                        sums, bg_part, stream)
+            _render_bwd(lib, bins, b, C, FLAG_UPS | odd | _wide(bins.TILE, nt0, lt[0]), (0, 1), mask,
+                        (bgf[b], T[b], asum[b], fg[b], go[b], *dS), sums, bg_part, stream)
             if mask & ~1:
                 check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
                                                  ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
-                _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), mask, (None,) * 5 + dS, sums, None, stream)
+                dense = _dense_levels(bins, lt, mask)
+                light = mask & ~1 & ~sum(1 << l for l in dense)
+                if light:
+                    _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5 + dS, sums, None,
+                                stream)
+                for l in dense:
+                    _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5 + dS,
+                                sums, None, stream)
         finally:
             kernel_timer.close("bwd", ev)
         _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream, lsc)
-    g_mu, g_scale, g_col, g_op, g_th = grads
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
@@ -695,7 +792,8 @@ class _AlphaRenderCullFields(torch.autograd.Function):
 class _AlphaRenderLevels(torch.autograd.Function):
     """Fused octave / coarse-fine render (render_triton.py:879-980) with the levels described by `lv`:
     inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, scale_is_log)
-    -> out [B,P,C]. scale_is_log as in _AlphaRenderCull."""
+    -> the [B,C,H,W] view of the [B,H*W,C] composite (made here, so that no view nodes follow the Function).
+    scale_is_log as in _AlphaRenderCull."""
 
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
@@ -708,12 +806,15 @@ class _AlphaRenderLevels(torch.autograd.Function):
         ctx.tiles = bins
         ctx.scale_is_log = scale_is_log
         ctx.save_for_backward(color, bg, T, asum, fg, scale if scale_is_log else None)
-        return out
+        B, P, C = out.shape
+        return out.view(B, H, W, C).permute(0, 3, 1, 2)
 
     @staticmethod
     def backward(ctx, grad_out):
         color, bg, T, asum, fg, log_scale = ctx.saved_tensors
-        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(grad_out, color, bg, ctx.has_theta, T, asum, fg,
+        B, C, H, W = grad_out.shape
+        go = grad_out.permute(0, 2, 3, 1).reshape(B, H * W, C)   # a view when the gradient has the image's layout
+        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(go, color, bg, ctx.has_theta, T, asum, fg,
                                                                   ctx.tiles, ctx.odds, log_scale)
         return (g_mu, g_scale, g_col, g_op, g_bg, g_th) + (None,) * 8
 
@@ -855,8 +956,7 @@ def render_alpha_multires(mu, log_scale, color, opacity, bg, H, W, theta=None, n
     both canvases and one composite kernel that upsamples the coarse fields in its epilogue."""
     B, N, C = color.shape
     lv = _multires_levels(H, W, N, n_coarse, coarse_factor)
-    out = _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
-    return out.reshape(B, H, W, C).permute(0, 3, 1, 2)
+    return _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
 
 
 def _octave_of(scale_px, base_texels=8.0, max_octaves=6):
@@ -883,5 +983,4 @@ def render_alpha_octave(mu, log_scale, color, opacity, bg, H, W, theta=None, cut
     level, which sums the same fields)."""
     B, N, C = color.shape
     lv = _octave_levels(H, W, base_texels, max_octaves)
-    out = _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)
-    return out.reshape(B, H, W, C).permute(0, 3, 1, 2)
+    return _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)

@@ -30,13 +30,18 @@ extern "C" {
 #define SPLAT_FLAG_FIELDS 1 /* forward writes raw sums (S_log, S_a, S_ac); backward takes dS_* upstream */
 #define SPLAT_FLAG_ODDS 2   /* colour weight a/(1-a) instead of a */
 #define SPLAT_FLAG_UPS 4    /* composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a */
-#define SPLAT_FLAG_WIDE 8   /* forward, TILE 8: 16 waves share each tile's pair list instead of 4 (a performance
-                               hint for launches of few tiles with long lists; results are identical up to the
-                               order the partial sums are added in) */
+#define SPLAT_FLAG_WIDE 8   /* TILE 8: 16 waves share each tile's pair list, instead of 4 in the forward and 1 in
+                               the backward (a performance hint for launches of few tiles with long lists; forward
+                               results are identical up to the order the partial sums are added in, backward
+                               results are identical) */
 #define SPLAT_FLAG_LOG_SCALE 16 /* binning (splat_bin, splat_bin_count): `scale` holds the raw log-scales [N,2]; the
                                    decode pass activates them, softplus(x) + 1e-4 with the bits torch's fp32
                                    F.softplus(x) + 1e-4 gives (params.py:18-28), so callers need no activation
                                    pass of their own; rec holds the activated scale either way */
+#define SPLAT_FLAG_DEFER 32 /* splat_bin / splat_bin_noalloc with pair_cap > 0: return as soon as the count, the read-back
+                               and the speculative pair phase are queued, without waiting for the read; the
+                               caller may queue launches that read the pair list (a count above pair_cap leaves
+                               them an empty list) and then calls splat_bin_finish for the statuses */
 
 /* Levels of a render. A NULL splat_levels* (or mode 0) is the single canvas (H, W). Otherwise splats are
  * routed to canvases ("levels"): level 0 is (H, W); coarser levels are rendered into packed fields and
@@ -122,6 +127,16 @@ int splat_bin(const float *mu, const float *scale, const float *theta, const flo
               int flags, long long max_pairs, float *rec, int *rect, int *offsets, long long *info, long long *info_host,
               void *ws_count, size_t ws_count_bytes, long long pair_cap, int *gid_sorted, int *tile_starts,
               int *pair_splat, int *pair_q, void *ws_pairs, size_t ws_pairs_bytes, void *stream);
+
+/* The read of a binning queued with SPLAT_FLAG_DEFER (no counterpart in the reference: its read is the wait at
+ * render_triton.py:391, which splat_bin does inside): waits for the totals to land in info_host[0, 2 + nlev) and
+ * returns splat_bin's status for them (0, 6 past pair_cap, 7 over max_pairs, 1 / 4 error bits), with the same
+ * info, info_host, max_pairs and pair_cap as that call. Call it on the thread (and current device) that queued the binning,
+ * before that thread's next splat_bin: the wait is on a read-back event per thread and device. Launches queued in between on the
+ * speculative pair list have run on the right list when it returns 0; on status 6 they read an empty list and
+ * must be repeated after splat_bin_pairs. */
+int splat_bin_finish(long long *info_host, const long long *info, int nlev, long long max_pairs, long long pair_cap,
+                     void *stream);
 
 /* No counterpart in the reference: splat_bin for callers that cannot allocate device memory (code in tight
  * serving loops, harnesses that forbid hipMalloc). The same binning as splat_bin with pair_cap > 0, but the

@@ -112,12 +112,29 @@ def test_host_rejects_cpu_tensors():
 
 
 def test_bin_rejects_unknown_flags():
-    """splat_bin / splat_bin_count accept only SPLAT_FLAG_LOG_SCALE; the check precedes any device work."""
+    """splat_bin_count accepts only SPLAT_FLAG_LOG_SCALE, splat_bin also SPLAT_FLAG_DEFER; the check precedes any
+    device work."""
     lib = _lib.load()
     for bad in (1, 8, 32, 16 | 2):
         assert lib.splat_bin_count(None, None, None, None, None, 3, 4, 16, 16, 8, 3.0, None, bad, None, None, None,
                                    None, None, 0, None) == 1
         assert b"unknown flags" in lib.splat_last_error()
+    for bad in (1, 8, 64, 32 | 2):
         assert lib.splat_bin(None, None, None, None, None, 3, 4, 16, 16, 8, 3.0, None, bad, -1, None, None, None,
                              None, None, None, 0, 0, None, None, None, None, None, 0, None) == 1
         assert b"unknown flags" in lib.splat_last_error()
+
+
+def test_deferred_read_needs_pair_buffers():
+    """SPLAT_FLAG_DEFER without buffers for pair_cap > 0 pairs is refused before any device work (the pointers
+    below are never dereferenced), and splat_bin_finish checks its arguments."""
+    lib = _lib.load()
+    fake = 256
+    N, H, W = 4, 16, 16
+    ws = lib.splat_bin_count_workspace_bytes(N, H, W, 8, None)
+    assert lib.splat_bin(fake, fake, None, fake, fake, 3, N, H, W, 8, 3.0, None, _lib.FLAG_DEFER, -1, fake, fake,
+                         fake, fake, fake, fake, ws, 0, None, None, None, None, None, 0, None) == 1
+    assert b"deferred read" in lib.splat_last_error()
+    for nlev, cap in ((0, 1), (_lib.MAX_LEVELS + 1, 1), (1, -1)):
+        assert lib.splat_bin_finish(fake, fake, nlev, -1, cap, None) == 1
+        assert b"splat_bin_finish" in lib.splat_last_error()
