@@ -353,6 +353,9 @@ def main():
     ap.add_argument("--odds", action="store_true", help="odds compositing instead of alpha")
     ap.add_argument("--no-c4", action="store_true", help="skip the 2048x2048 stress configuration")
     ap.add_argument("--no-c3", action="store_true", help="skip the encoder end-to-end configuration")
+    ap.add_argument("--only", choices=("c3", "c4"), default=None,
+                    help="run only the encoder end-to-end frame (c3) or the 2048x2048 stress set (c4) and print its "
+                         "JSON object (for profiling one configuration)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a MIB-MiB copy kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -365,6 +368,12 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.only == "c3":
+        print(json.dumps({"c3": e2e_c3(max(10, args.steps // 2), max(3, args.warmup // 2))}), flush=True)
+        return
+    if args.only == "c4":
+        print(json.dumps({"c4": stress_c4(max(5, args.steps // 5), max(2, args.warmup // 5), args.odds)}), flush=True)
         return
     dev = torch.device("cuda:0")
     s_cpu = synth.config("c2")

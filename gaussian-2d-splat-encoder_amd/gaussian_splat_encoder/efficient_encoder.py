@@ -276,6 +276,7 @@ class EfficientGaussianEncoder(nn.Module):
         coarse = self.coarse_head(fused)
         if self.coarse_ls_floor is not None:
             coarse["log_scale"] = coarse["log_scale"].clamp(min=self.coarse_ls_floor)
+        self._mark("coarse_head")
         rg = self.residual_grid
         c_render = render_alpha_octave(coarse["mu"], coarse["log_scale"], coarse["color"], coarse["opacity"], bg,
                                        rg, rg, coarse["theta"], odds=self.odds)
