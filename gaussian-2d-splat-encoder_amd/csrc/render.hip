@@ -69,6 +69,11 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// A value every lane of the wave holds, as a wave-uniform (scalar) value.
+__device__ __forceinline__ float uniform_f(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
 // Whitened offsets (u, v) of the pixel centre (py0, px0) from a splat with centre (gy, gx) and rotation rows
 // (A, B), (Cc, D), evaluated in float64 and rounded once. A tile's pixels add their own offsets from the tile's
 // first pixel centre to these, so their rounding error is shared by the whole tile; with one rounding it stays
@@ -209,20 +214,52 @@ __device__ __forceinline__ void add_coarse(const LevelTable& L, int yp, int xp, 
   }
 }
 
-// Global tile t of a launch over tiles [tb0, tb0 + ntiles) (XCD-aware order), its level and coordinates.
+// A global tile, its level and coordinates.
 struct TileAt {
   int t, l, tx, ty, H, W;
 };
-__device__ __forceinline__ TileAt tile_at(const LevelTable& L, int tb0, int ntiles) {
+__device__ __forceinline__ TileAt tile_of(const LevelTable& L, int t, int l) {
   TileAt a;
-  a.t = tb0 + xcd_swizzle(blockIdx.x, ntiles);
-  a.l = level_of(L, a.t);
+  a.t = t;
+  a.l = l;
   const int lt = a.t - L.tbase[a.l];
   a.ty = lt / L.ntx[a.l];
   a.tx = lt - a.ty * L.ntx[a.l];
   a.H = L.H[a.l];
   a.W = L.W[a.l];
   return a;
+}
+// Tile of this workgroup in a launch over tiles [tb0, tb0 + ntiles) (XCD-aware order).
+__device__ __forceinline__ TileAt tile_at(const LevelTable& L, int tb0, int ntiles) {
+  const int t = tb0 + xcd_swizzle(blockIdx.x, ntiles);
+  return tile_of(L, t, level_of(L, t));
+}
+
+// Work items of a split launch over the coarse levels of a FIELDS render: every tile of level l is split into
+// split[l] contiguous chunks of its pair list, one workgroup each (split 0: the level is not in the launch). Item
+// i of level l (ibase[l] <= i < ibase[l + 1]) is chunk (i - ibase[l]) % split[l] of tile
+// tbase[l] + (i - ibase[l]) / split[l]. Dense coarse levels hold few tiles with long pair lists: spread over
+// separate workgroups, their chunks run on every CU instead of the few CUs that one workgroup per tile would
+// occupy. In the forward, the chunks of a level with split > 1 write partial sums (partial item
+// pibase[l] + i - ibase[l]) that k_fields_combine adds in chunk order (its workgroup c takes the tile
+// c - cbase[l] of level l); the backward's per-pair sums need no combine.
+struct SplitTable {
+  int split[kMaxLevels];
+  int ibase[kMaxLevels + 1];
+  int pibase[kMaxLevels];
+  int cbase[kMaxLevels + 1];
+};
+
+// Tile and chunk of work item `item` (returns the tile; *chunk, *nsplit).
+__device__ __forceinline__ TileAt split_item(const LevelTable& L, const SplitTable& P, int item, int* chunk,
+                                             int* nsplit) {
+  int l = 0;
+  while (l + 1 < L.n && item >= P.ibase[l + 1]) ++l;
+  const int j = item - P.ibase[l];
+  const int s = P.split[l];
+  *chunk = j % s;
+  *nsplit = s;
+  return tile_of(L, L.tbase[l] + j / s, l);
 }
 
 // Forward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
@@ -315,6 +352,91 @@ __global__ __launch_bounds__((fwd_threads<TILE, S>())) void k_fwd_cull(
   } else {
     store_composite<C>(p, sl, s_a, sc, bg, out, Tout, asum_out, fg_out);
   }
+}
+
+// Partial sums of a split FIELDS item, [partial item][2 + C][tile_threads(TILE)] floats: S_log in log2 units,
+// S_a, S_ac per channel, one slot per thread of the tile's workgroup.
+template <int C, int TILE>
+__host__ __device__ constexpr int split_part_floats() { return (2 + C) * tile_threads(TILE); }
+
+// FIELDS forward of the split work items of the coarse levels (SplitTable): one workgroup per item, the tile's
+// pixels one per thread, over the item's chunk of the tile's pair list (in pair order, as fwd_tile_pixel walks
+// it). A level with split 1 writes its fields; otherwise the item writes partial sums for k_fields_combine.
+template <int C, bool ODDS, int TILE>
+__global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_fields_split(
+    const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L,
+    SplitTable P, int nitems, float* __restrict__ slog, float* __restrict__ sa, float* __restrict__ sac,
+    float* __restrict__ part) {
+  constexpr int NT = tile_threads(TILE);
+  __shared__ float2 s_uv[NT / 64][64];
+  const int item = xcd_swizzle(blockIdx.x, nitems);
+  int chunk, nsplit;
+  const TileAt ta = split_item(L, P, item, &chunk, &nsplit);
+  const int th = (int)threadIdx.x, lane = th & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(th >> 6);
+  const int yp = ta.ty * TILE + th / TILE, xp = ta.tx * TILE + th % TILE;
+  const bool valid = th < TILE * TILE && yp < ta.H && xp < ta.W;
+  const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
+  const float px = ((float)xp + 0.5f) / (float)ta.W;
+  const float py0 = uniform_f(((float)(ta.ty * TILE) + 0.5f) / (float)ta.H);
+  const float px0 = uniform_f(((float)(ta.tx * TILE) + 0.5f) / (float)ta.W);
+  int g0 = starts[ta.t];
+  const int g1t = starts[ta.t + 1];
+  const int len = ((g1t - g0 + nsplit - 1) / nsplit + 3) & ~3;
+  g0 = min(g1t, g0 + chunk * len);
+  const int g1 = min(g1t, g0 + len);
+  float sl = 0.f, s_a = 0.f, sc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = 0.f;
+  fwd_tile_pixel<C, ODDS>(rec, gid, g0, g1, py0, px0, py - py0, px - px0, s_uv[wid], lane, sl, s_a, sc);
+  if (nsplit > 1) {
+    float* dst = part + (size_t)(P.pibase[ta.l] + item - P.ibase[ta.l]) * split_part_floats<C, TILE>() + th;
+    dst[0] = sl;
+    dst[NT] = s_a;
+#pragma unroll
+    for (int c = 0; c < C; ++c) dst[(2 + c) * NT] = sc[c];
+    return;
+  }
+  if (!valid) return;
+  const size_t pp = (size_t)L.pbase[ta.l] + (size_t)yp * ta.W + xp;
+  slog[pp] = sl * kLn2;
+  sa[pp] = s_a;
+#pragma unroll
+  for (int c = 0; c < C; ++c) sac[pp * C + c] = sc[c];
+}
+
+// Fields of the tiles of split levels: workgroup c is tile c - cbase[l] of level l (cbase[l] <= c < cbase[l + 1]);
+// thread = pixel, the partial sums of the tile's split[l] chunks added in chunk order (deterministic).
+template <int C, int TILE>
+__global__ __launch_bounds__(tile_threads(TILE)) void k_fields_combine(LevelTable L, SplitTable P,
+                                                                       const float* __restrict__ part,
+                                                                       float* __restrict__ slog, float* __restrict__ sa,
+                                                                       float* __restrict__ sac) {
+  constexpr int NT = tile_threads(TILE);
+  const int cidx = blockIdx.x;
+  int l = 0;
+  while (l + 1 < L.n && cidx >= P.cbase[l + 1]) ++l;
+  const int j = cidx - P.cbase[l];
+  const TileAt ta = tile_of(L, L.tbase[l] + j, l);
+  const int th = (int)threadIdx.x;
+  const int yp = ta.ty * TILE + th / TILE, xp = ta.tx * TILE + th % TILE;
+  if (!(th < TILE * TILE && yp < ta.H && xp < ta.W)) return;
+  const int s = P.split[l];
+  const float* src = part + (size_t)(P.pibase[l] + j * s) * split_part_floats<C, TILE>() + th;
+  float sl = 0.f, s_a = 0.f, sc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) sc[c] = 0.f;
+  for (int k = 0; k < s; ++k, src += split_part_floats<C, TILE>()) {
+    sl += src[0];
+    s_a += src[NT];
+#pragma unroll
+    for (int c = 0; c < C; ++c) sc[c] += src[(2 + c) * NT];
+  }
+  const size_t pp = (size_t)L.pbase[l] + (size_t)yp * ta.W + xp;
+  slog[pp] = sl * kLn2;
+  sa[pp] = s_a;
+#pragma unroll
+  for (int c = 0; c < C; ++c) sac[pp * C + c] = sc[c];
 }
 
 // Exact path forward (render_triton.py:58-125): 64 pixels per workgroup in flat pixel order, pixel centres
@@ -550,10 +672,6 @@ __device__ __forceinline__ bool near_possible(float op, float lop, float gy, flo
   return op > kNearOpaqueBwd && d2 < smax * smax * (lop - kLog2NearOpaqueBwd + kNearMargin);
 }
 
-__device__ __forceinline__ float uniform_f(float x) {
-  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
-}
-
 // Geometry of one pair in the backward's lane-per-pair loops: the whitened offsets (u0, v0) of the tile's first
 // pixel centre and the rotation rows (A, B) and (Cc, D), so that at the pixel (yy, xx) of the tile
 // u = A ly[yy] + B lx[xx] + u0 and v = Cc ly[yy] + D lx[xx] + v0, where ly[yy] and lx[xx] are the pixel centre's
@@ -782,13 +900,15 @@ __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ re
 // covering a 1/L share of the tile's pixels (whole rows when that share is at least a row) and the L partial
 // sums are combined with xor shuffles. At 5 waves per SIMD (at most 96 VGPRs, no spills) there are enough waves
 // to cover the latency of the VALU, LDS and transcendental pipes.
-template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE, int S>
+// SPLIT (FIELDS only, S = 1): workgroup = a work item of the SplitTable, the item's chunk of its tile's pairs.
+template <int C, bool FIELDS, bool ODDS, bool UPS, int TILE, int S, bool SPLIT = false>
 __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) void k_bwd_cull(
     const float* __restrict__ rec, const int* __restrict__ gid, const int* __restrict__ starts, LevelTable L, int tb0,
     int ntiles, const float* __restrict__ bg, const float* __restrict__ Tin, const float* __restrict__ asum_in,
     const float* __restrict__ fg_in, const float* __restrict__ gout, float* __restrict__ dslog,
     float* __restrict__ dsa, float* __restrict__ dsac, const int* __restrict__ pair_q, float* __restrict__ psum,
-    float* __restrict__ bg_part) {
+    float* __restrict__ bg_part, SplitTable P) {
+  static_assert(!SPLIT || (FIELDS && S == 1), "split items: FIELDS backward, one wave per item");
   constexpr int NP = TILE * TILE;
   constexpr int RS = up_stride<TILE>();
   __shared__ float4 s_pa[TILE * RS];
@@ -797,7 +917,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   __shared__ float s_lyc[TILE];
   __shared__ int s_defer_w[S][128], s_mi_w[S][128];
   __shared__ float2 s_muv_w[S][128];
-  const TileAt ta = tile_at(L, tb0, ntiles);
+  int chunk = 0, nsplit = 1;
+  const TileAt ta = SPLIT ? split_item(L, P, xcd_swizzle(blockIdx.x, ntiles), &chunk, &nsplit) : tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
   const int t = ta.t;
   const int lane = threadIdx.x & 63;
@@ -856,6 +977,11 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   }
   __syncthreads();
   int g0 = starts[t], g1 = starts[t + 1];
+  if (SPLIT) {   // the item's chunk: whole passes of 64 pairs where the tile's list allows
+    const int len = (((g1 - g0 + nsplit - 1) / nsplit) + 63) & ~63;
+    g0 = min(g1, g0 + chunk * len);
+    g1 = min(g1, g0 + len);
+  }
   if (S > 1) {   // this wave's share of the tile's pairs
     const int chunk = (g1 - g0 + S - 1) / S;
     g0 = min(g1, g0 + wid * chunk);
@@ -1504,12 +1630,137 @@ int splat_render_bwd(const float* rec, const int* gid_sorted, const int* tile_st
         constexpr bool FL = decltype(fl)::value != 0, OD = decltype(od)::value != 0, UP = decltype(up)::value != 0;
         if (TT == 8 && (flags & kFlagWide))
           launch_tile_kernel(k_bwd_cull<CC, FL, OD, UP, TT, 16>, ntiles, 64 * 16, st, rec, gid_sorted, tile_starts, L,
-                             tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part);
+                             tb0, ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part,
+                             SplitTable{});
         else
           launch_tile_kernel(k_bwd_cull<CC, FL, OD, UP, TT, 1>, ntiles, 64, st, rec, gid_sorted, tile_starts, L, tb0,
-                             ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part);
+                             ntiles, bg, T, asum, fg, gout, dslog, dsa, dsac, pair_q, pair_sums, bg_part, SplitTable{});
         return check_launch("k_bwd_cull");
       });
+    });
+  });
+}
+
+// Host: the SplitTable of a split launch over the levels [lev_begin, lev_end) present in L.mask (levels outside
+// take no items); *nitems work items, *ncomb tiles to combine, *npart partial items.
+constexpr int kMaxSplit = 1024;
+static int make_split(const char* who, const LevelTable& L, int lev_begin, int lev_end, const int* splits,
+                      SplitTable* P, int* nitems, int* ncomb, long long* npart) {
+  if (!splits) return set_error(kInvalid, "%s: null splits", who);
+  SplitTable t{};
+  long long items = 0, comb = 0, part = 0;
+  for (int l = 0; l < L.n; ++l) {
+    t.ibase[l] = (int)items;
+    t.cbase[l] = (int)comb;
+    t.pibase[l] = (int)part;
+    const bool in = l >= lev_begin && l < lev_end && ((L.mask >> l) & 1);
+    const int s = in ? splits[l] : 0;
+    if (in && (s < 1 || s > kMaxSplit))
+      return set_error(kInvalid, "%s: splits[%d] = %d outside [1, %d]", who, l, s, kMaxSplit);
+    t.split[l] = s;
+    const long long nt = L.tbase[l + 1] - L.tbase[l];
+    items += nt * s;
+    if (s > 1) {
+      comb += nt;
+      part += nt * s;
+    }
+    if (items > 0x3fffffffLL) return set_error(kOverflow, "%s: %lld work items", who, items);
+  }
+  t.ibase[L.n] = (int)items;
+  t.cbase[L.n] = (int)comb;
+  *P = t;
+  *nitems = (int)items;
+  *ncomb = (int)comb;
+  *npart = part;
+  return kOk;
+}
+
+static size_t split_part_bytes(int C, int TILE, long long npart) {
+  return sizeof(float) * (size_t)(2 + C) * (size_t)tile_threads(TILE) * (size_t)npart;
+}
+
+size_t splat_fields_split_workspace_bytes(int C, int H, int W, int TILE, const splat_levels* lv, int lev_begin,
+                                          int lev_end, unsigned levmask, const int* splits) {
+  LevelTable L;
+  int tb0, ntiles, nitems, ncomb;
+  long long npart;
+  SplitTable P;
+  if (C < 1 || C > kMaxC || (TILE != 4 && TILE != 8 && TILE != 16) ||
+      launch_levels("splat_fields_split_workspace_bytes", H, W, TILE, lv, lev_begin, lev_end, levmask, kFlagFields,
+                    &L, &tb0, &ntiles) ||
+      make_split("splat_fields_split_workspace_bytes", L, lev_begin, lev_end, splits, &P, &nitems, &ncomb, &npart))
+    return 0;
+  return split_part_bytes(C, TILE, npart);
+}
+
+int splat_render_fields_split(const float* rec, const int* gid_sorted, const int* tile_starts, int C, int H, int W,
+                              int TILE, int flags, const splat_levels* lv, int lev_begin, int lev_end,
+                              unsigned levmask, const int* splits, float* slog, float* sa, float* sac, void* ws,
+                              size_t ws_bytes, void* stream) {
+  LevelTable L;
+  int tb0, ntiles, nitems, ncomb;
+  long long npart;
+  SplitTable P;
+  if (flags & ~kFlagOdds) return set_error(kInvalid, "splat_render_fields_split: flags=%d (only ODDS)", flags);
+  if (int e = launch_levels("splat_render_fields_split", H, W, TILE, lv, lev_begin, lev_end, levmask,
+                            flags | kFlagFields, &L, &tb0, &ntiles))
+    return e;
+  if (int e = make_split("splat_render_fields_split", L, lev_begin, lev_end, splits, &P, &nitems, &ncomb, &npart))
+    return e;
+  if (!rec || !gid_sorted || !tile_starts || !slog || !sa || !sac)
+    return set_error(kInvalid, "splat_render_fields_split: null pointer");
+  if (nitems == 0) return kOk;
+  if (ncomb && (!ws || ws_bytes < split_part_bytes(C, TILE, npart)))
+    return set_error(kWorkspace, "splat_render_fields_split: workspace of %zu bytes, %zu needed", ws_bytes,
+                     split_part_bytes(C, TILE, npart));
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)ws;
+  return with_c(C, [&](auto cc) {
+    return with_tile(TILE, [&](auto tt) {
+      constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
+      if (flags & kFlagOdds)
+        launch_tile_kernel(k_fwd_fields_split<CC, true, TT>, nitems, tile_threads(TT), st, rec, gid_sorted,
+                           tile_starts, L, P, nitems, slog, sa, sac, part);
+      else
+        launch_tile_kernel(k_fwd_fields_split<CC, false, TT>, nitems, tile_threads(TT), st, rec, gid_sorted,
+                           tile_starts, L, P, nitems, slog, sa, sac, part);
+      if (ncomb) k_fields_combine<CC, TT><<<ncomb, tile_threads(TT), 0, st>>>(L, P, part, slog, sa, sac);
+      return check_launch("k_fwd_fields_split");
+    });
+  });
+}
+
+int splat_render_fields_split_bwd(const float* rec, const int* gid_sorted, const int* tile_starts, const int* pair_q,
+                                  long long tot, int C, int H, int W, int TILE, int flags, const splat_levels* lv,
+                                  int lev_begin, int lev_end, unsigned levmask, const int* splits, float* dslog,
+                                  float* dsa, float* dsac, float* pair_sums, void* stream) {
+  LevelTable L;
+  int tb0, ntiles, nitems, ncomb;
+  long long npart;
+  SplitTable P;
+  if (flags & ~kFlagOdds) return set_error(kInvalid, "splat_render_fields_split_bwd: flags=%d (only ODDS)", flags);
+  if (int e = launch_levels("splat_render_fields_split_bwd", H, W, TILE, lv, lev_begin, lev_end, levmask,
+                            flags | kFlagFields, &L, &tb0, &ntiles))
+    return e;
+  if (int e = make_split("splat_render_fields_split_bwd", L, lev_begin, lev_end, splits, &P, &nitems, &ncomb, &npart))
+    return e;
+  if (tot < 0 || tot > 0x7fffffffLL - 64) return set_error(kInvalid, "splat_render_fields_split_bwd: tot=%lld", tot);
+  if (!rec || !gid_sorted || !tile_starts || !pair_sums || !dslog || !dsa || !dsac || (tot > 0 && !pair_q))
+    return set_error(kInvalid, "splat_render_fields_split_bwd: null pointer");
+  if (nitems == 0) return kOk;
+  hipStream_t st = (hipStream_t)stream;
+  return with_c(C, [&](auto cc) {
+    return with_tile(TILE, [&](auto tt) {
+      constexpr int CC = decltype(cc)::value, TT = decltype(tt)::value;
+      if (flags & kFlagOdds)
+        launch_tile_kernel(k_bwd_cull<CC, true, true, false, TT, 1, true>, nitems, 64, st, rec, gid_sorted,
+                           tile_starts, L, 0, nitems, nullptr, nullptr, nullptr, nullptr, nullptr, dslog, dsa, dsac,
+                           pair_q, pair_sums, nullptr, P);
+      else
+        launch_tile_kernel(k_bwd_cull<CC, true, false, false, TT, 1, true>, nitems, 64, st, rec, gid_sorted,
+                           tile_starts, L, 0, nitems, nullptr, nullptr, nullptr, nullptr, nullptr, dslog, dsa, dsac,
+                           pair_q, pair_sums, nullptr, P);
+      return check_launch("k_bwd_cull(split)");
     });
   });
 }

@@ -53,6 +53,11 @@ _SIGS = {
     "splat_pair_sums_bytes": (_SZ, [_LL]),
     "splat_render_bwd": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP,
                               _VP, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "splat_fields_split_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV, _I, _I, _U, _VP]),
+    "splat_render_fields_split": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP, _VP, _VP, _VP,
+                                       _SZ, _VP]),
+    "splat_render_fields_split_bwd": (_I, [_VP, _VP, _VP, _VP, _LL, _I, _I, _I, _I, _I, _LV, _I, _I, _U, _VP, _VP,
+                                           _VP, _VP, _VP, _VP]),
     "splat_upsample_adjoint_workspace_bytes": (_SZ, [_I, _I, _I, _I, _LV]),
     "splat_upsample_adjoint": (_I, [_I, _I, _I, _I, _LV, _U, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "splat_reduce_pairs": (_I, [_VP, _VP, _VP, _LL, _I, _I, _VP, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]),

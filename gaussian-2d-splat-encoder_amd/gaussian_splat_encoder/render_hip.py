@@ -440,18 +440,36 @@ def _wide(TILE, ntiles, pairs):
     return FLAG_WIDE if TILE == 8 and 0 < ntiles < 2048 and pairs >= 128 * ntiles else 0
 
 
-def _dense_levels(bins, lt, mask):
-    """Coarse levels (>= 1, present in `mask`) whose tiles hold long pair lists: each gets a forward and a backward
-    launch of its own with FLAG_WIDE; the other coarse levels share one launch."""
-    if bins.TILE != 8:
-        return []
+_SPLIT_PAIRS = 128   # pairs per workgroup the split launches of the coarse levels aim at
+_SPLIT_MAX = 64
+
+
+def _level_splits(bins, lt, mask):
+    """Chunks per tile of every level for the split FIELDS launches over the coarse levels (ctypes int array):
+    a level in `mask` gets about _SPLIT_PAIRS pairs per chunk on average over its tiles (1 to _SPLIT_MAX chunks),
+    so a dense coarse level's few tiles with long pair lists are spread over many workgroups; level 0 and levels
+    outside `mask` get 1 (unused)."""
     geom, L = bins.geom, bins.n_levels
-    dense = []
-    for l in range(1, L):
-        tiles = (geom[l + 1][3] if l + 1 < L else bins.nt) - geom[l][3]
-        if (mask >> l) & 1 and _wide(8, tiles, lt[l]):
-            dense.append(l)
-    return dense
+    sp = (_lib.ctypes.c_int * L)()
+    for l in range(L):
+        sp[l] = 1
+        if l and (mask >> l) & 1:
+            tiles = (geom[l + 1][3] if l + 1 < L else bins.nt) - geom[l][3]
+            if tiles:
+                sp[l] = max(1, min(_SPLIT_MAX, -(-int(lt[l]) // (_SPLIT_PAIRS * tiles))))
+    return sp
+
+
+def _fields_split_fwd(lib, bins, b, C, odd, lt, mask, fl, stream):
+    """FIELDS forward of the coarse levels in `mask` of image b into the packed fields fl, one split launch."""
+    L = bins.n_levels
+    lvr = _lib.ctypes.byref(bins.lv)
+    sp = _level_splits(bins, lt, mask)
+    nb = lib.splat_fields_split_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr, 1, L, mask, sp)
+    ws = _ws(nb, fl[0].device) if nb else None
+    check(lib.splat_render_fields_split(bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), C, bins.H, bins.W,
+                                        bins.TILE, odd, lvr, 1, L, mask, sp, *[ptr(t) for t in fl], ptr(ws), nb,
+                                        stream), "splat_render_fields_split")
 
 
 def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
@@ -539,18 +557,12 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     nt0 = bins.ntiles0
 
     def launch(b, lt, mask):
-        """The launches of image b for per-level pair totals lt (to pick the 16-wave launches) over the levels in
-        mask (a level in mask that holds no pair renders zeros)."""
+        """The launches of image b for per-level pair totals lt (they size the coarse levels' split and pick the
+        16-wave composite) over the levels in mask (a level in mask that holds no pair renders zeros)."""
         ev = kernel_timer.record("fwd")
         try:
             if mask & ~1:
-                dense = _dense_levels(bins, lt, mask)
-                light = mask & ~1 & ~sum(1 << l for l in dense)
-                if light:
-                    _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5, fl, stream)
-                for l in dense:
-                    _render_fwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5, fl,
-                                stream)
+                _fields_split_fwd(lib, bins, b, C, odd, lt, mask & ~1, fl, stream)
             _render_fwd(lib, bins, b, C, FLAG_UPS | odd | _wide(TILE, nt0, lt[0]), (0, 1), mask,
                         (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
         finally:
@@ -709,14 +721,11 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
             if mask & ~1:
                 check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
                                                  ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
-                dense = _dense_levels(bins, lt, mask)
-                light = mask & ~1 & ~sum(1 << l for l in dense)
-                if light:
-                    _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd, (1, L), light, (None,) * 5 + dS, sums, None,
-                                stream)
-                for l in dense:
-                    _render_bwd(lib, bins, b, C, FLAG_FIELDS | odd | FLAG_WIDE, (l, l + 1), 1 << l, (None,) * 5 + dS,
-                                sums, None, stream)
+                check(lib.splat_render_fields_split_bwd(bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"),
+                                                        bins.p(b, "pq"), bins.tot_b[b], C, bins.H, bins.W, bins.TILE,
+                                                        odd, lvr, 1, L, mask & ~1, _level_splits(bins, lt, mask & ~1),
+                                                        *[ptr(t) for t in dS], ptr(sums), stream),
+                      "splat_render_fields_split_bwd")
         finally:
             kernel_timer.close("bwd", ev)
         _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream, lsc)

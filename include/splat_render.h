@@ -195,6 +195,26 @@ int splat_render_bwd(const float *rec, const int *gid_sorted, const int *tile_st
                      const float *asum, const float *fg, const float *gout, float *dslog, float *dsa,
                      float *dsac, float *pair_sums, float *bg_part, void *stream);
 
+/* FIELDS forward and backward of the coarse levels [lev_begin, lev_end) of a multi-level render in one
+ * launch each, with every tile of level l split into splits[l] (1..1024) contiguous chunks of its pair list,
+ * one workgroup per chunk (levels not in levmask take none). Dense coarse levels (few tiles with long
+ * pair lists) then occupy every CU. The forward's chunks of a level with splits[l] > 1 write partial sums into
+ * the workspace (splat_fields_split_workspace_bytes; 0 when no level is split) and a second kernel adds them
+ * in chunk order: deterministic, the same fields as splat_render_fwd with FIELDS up to summation order. The
+ * backward's chunks write the per-pair sums as splat_render_bwd with FIELDS does. flags: SPLAT_FLAG_ODDS or 0.
+ * Replace the per-octave-group launches of _render_fwd_cull_kernel / _render_bwd_cull_kernel over the coarse
+ * groups, render_triton.py:962-978 (forward, per octave) and :768-810 (their backward). */
+size_t splat_fields_split_workspace_bytes(int C, int H, int W, int TILE, const splat_levels *lv, int lev_begin,
+                                          int lev_end, unsigned levmask, const int *splits);
+int splat_render_fields_split(const float *rec, const int *gid_sorted, const int *tile_starts, int C, int H, int W,
+                              int TILE, int flags, const splat_levels *lv, int lev_begin, int lev_end,
+                              unsigned levmask, const int *splits, float *slog, float *sa, float *sac, void *ws,
+                              size_t ws_bytes, void *stream);
+int splat_render_fields_split_bwd(const float *rec, const int *gid_sorted, const int *tile_starts, const int *pair_q,
+                                  long long tot, int C, int H, int W, int TILE, int flags, const splat_levels *lv,
+                                  int lev_begin, int lev_end, unsigned levmask, const int *splits, float *dslog,
+                                  float *dsa, float *dsac, float *pair_sums, void *stream);
+
 /* Backward of the upsample: the exact adjoint of the bilinear upsample of every masked coarse level,
  * from the level-0 upstream dslog/dsa/dsac[0, P) into the coarse levels' packed slots, deterministic
  * (two gather passes, no atomics). Replaces the autograd of F.interpolate at render_triton.py:864-876. */
