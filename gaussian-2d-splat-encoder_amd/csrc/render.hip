@@ -1396,48 +1396,74 @@ __device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo,
   *hi = b < out - 1 ? b : out - 1;
 }
 
-// Column slot of coarse level l: cbase(l) = sum of W[1..l-1].
-__device__ __forceinline__ int coarse_col_level(const LevelTable& L, int j, int* ix) {
-  int l = 1, base = 0;
-  while (l + 1 < L.n && j >= base + L.W[l]) {
-    base += L.W[l];
-    ++l;
-  }
-  *ix = j - base;
-  return l;
-}
+// Pass 1: workgroup = level-0 row y; tmp[k][y][j] = sum_x wx(x -> ix) dS_0[k][y, x] for the coarse column slots
+// j = cbase(l) + ix of every masked level l. STAGED: the row's 2 + C planes are first copied into LDS (coalesced;
+// rows of up to kAdjStageMax floats over all planes), so the window loops read LDS. The window of a texel of level l
+// spans about 2^(l+1) destinations (131 at the coarsest octave of a 2048-wide canvas) while the level has W0 / 2^l
+// texels, so every level is about 2 W0 window steps: the levels are taken one after another by the whole
+// workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at most 64), lane
+// s summing the destinations x0 + s, x0 + s + tpc, ... of the texel's window; the tpc partial sums are added by a
+// fixed xor tree (deterministic).
+constexpr int kAdjStageMax = 16384;   // floats of LDS per workgroup (64 KiB)
 
-// Pass 1: workgroup = level-0 row y; tmp[k][y][j] = sum_x wx(x -> ix) dS_0[k][y, x] for every coarse column
-// slot j = cbase(l) + ix of the masked levels (the row stays in cache across the slots).
-template <int C>
+template <int C, bool STAGED>
 __global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const float* __restrict__ dslog,
                                                   const float* __restrict__ dsa, const float* __restrict__ dsac,
                                                   float* __restrict__ tmp) {
+  extern __shared__ float s_row[];   // STAGED: [S_log W0][S_a W0][S_ac W0 x C]
   const int y = blockIdx.x, H0 = L.H[0], W0 = L.W[0];
   const size_t plane = (size_t)H0 * ncols;
-  for (int j = threadIdx.x; j < ncols; j += 256) {
-    int ix;
-    const int l = coarse_col_level(L, j, &ix);
+  const int t = threadIdx.x;
+  const float* rl = dslog + (size_t)y * W0;
+  const float* ra = dsa + (size_t)y * W0;
+  const float* rc = dsac + (size_t)y * W0 * C;
+  if (STAGED) {
+    for (int i = t; i < W0; i += 256) {
+      s_row[i] = rl[i];
+      s_row[W0 + i] = ra[i];
+    }
+    for (int i = t; i < W0 * C; i += 256) s_row[2 * W0 + i] = rc[i];
+    __syncthreads();
+    rl = s_row;
+    ra = s_row + W0;
+    rc = s_row + 2 * W0;
+  }
+  int cb = 0;
+  for (int l = 1; l < L.n; cb += L.W[l], ++l) {
     if (!((L.mask >> l) & 1)) continue;
     const int Wl = L.W[l];
     const float sx = (float)Wl / (float)W0;
-    int x0, x1;
-    ups_window(ix, W0, sx, &x0, &x1);
-    float al = 0.f, aa = 0.f, ac[kMaxC] = {0.f, 0.f, 0.f, 0.f};
-    for (int x = x0; x <= x1; ++x) {
-      const float w = ups_weight(x, ix, Wl, sx);
-      if (w == 0.f) continue;
-      const size_t p = (size_t)y * W0 + x;
-      al += w * dslog[p];
-      aa += w * dsa[p];
+    int tpc = 1;   // lanes per texel (block-uniform)
+    while (tpc < 64 && Wl * tpc * 2 <= 256) tpc *= 2;
+    const int sub = t & (tpc - 1);
+    for (int j0 = 0; j0 < Wl * tpc; j0 += 256) {   // block-uniform trip count (the xor tree needs every lane)
+      const int ix = (j0 + t) / tpc;
+      float al = 0.f, aa = 0.f, ac[kMaxC] = {0.f, 0.f, 0.f, 0.f};
+      if (ix < Wl) {
+        int x0, x1;
+        ups_window(ix, W0, sx, &x0, &x1);
+        for (int x = x0 + sub; x <= x1; x += tpc) {
+          const float w = ups_weight(x, ix, Wl, sx);
+          al += w * rl[x];
+          aa += w * ra[x];
 #pragma unroll
-      for (int c = 0; c < C; ++c) ac[c] += w * dsac[p * C + c];
+          for (int c = 0; c < C; ++c) ac[c] += w * rc[(size_t)x * C + c];
+        }
+      }
+      for (int d = 1; d < tpc; d <<= 1) {
+        al += __shfl_xor(al, d, 64);
+        aa += __shfl_xor(aa, d, 64);
+#pragma unroll
+        for (int c = 0; c < C; ++c) ac[c] += __shfl_xor(ac[c], d, 64);
+      }
+      if (ix < Wl && sub == 0) {
+        const size_t o = (size_t)y * ncols + cb + ix;
+        tmp[o] = al;
+        tmp[plane + o] = aa;
+#pragma unroll
+        for (int c = 0; c < C; ++c) tmp[(2 + c) * plane + o] = ac[c];
+      }
     }
-    const size_t o = (size_t)y * ncols + j;
-    tmp[o] = al;
-    tmp[plane + o] = aa;
-#pragma unroll
-    for (int c = 0; c < C; ++c) tmp[(2 + c) * plane + o] = ac[c];
   }
 }
 
@@ -1793,7 +1819,11 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels* lv
   float* tmp = (float*)ws;
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
-    k_adj_cols<CC><<<L.H[0], 256, 0, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+    const size_t stage = sizeof(float) * (size_t)(2 + CC) * (size_t)L.W[0];
+    if (stage <= sizeof(float) * kAdjStageMax)
+      k_adj_cols<CC, true><<<L.H[0], 256, stage, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+    else
+      k_adj_cols<CC, false><<<L.H[0], 256, 0, st>>>(L, ncols, dslog, dsa, dsac, tmp);
     k_adj_rows<CC><<<(ncoarse + 255) / 256, 256, 0, st>>>(L, ncols, tmp, dslog, dsa, dsac);
     return check_launch("splat_upsample_adjoint");
   });
