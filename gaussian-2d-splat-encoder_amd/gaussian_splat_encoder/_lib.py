@@ -114,8 +114,8 @@ def check(status: int, what: str) -> None:
 
 
 def ptr(t) -> int | None:
-    """Device pointer of a tensor (None stays NULL)."""
-    return None if t is None else t.data_ptr()
+    """Device pointer of a tensor (None stays NULL; an int is taken as a pointer already)."""
+    return t if t is None or type(t) is int else t.data_ptr()
 
 
 def stream_ptr(device=None) -> int:

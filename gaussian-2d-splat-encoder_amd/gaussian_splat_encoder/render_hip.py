@@ -41,11 +41,18 @@ def _dev_check(*ts):
 
 
 def _f32(t):
+    """t as contiguous fp32 (itself when it already is: the kernels only take its data pointer)."""
+    if t is None or (t.dtype is torch.float32 and t.is_contiguous()):
+        return t
+    return t.detach().contiguous().float()
+
+
+def _bptr(t, b):
+    """Device pointer of image b of a contiguous [B, ...] tensor (None stays NULL)."""
     if t is None:
         return None
-    if t.dtype is torch.float32 and t.is_contiguous():
-        return t.detach()
-    return t.detach().contiguous().float()
+    p = t.data_ptr()
+    return p if b == 0 else p + b * t.stride(0) * t.element_size()
 
 
 def _empty(shape, dev, dtype=torch.float32):
@@ -148,13 +155,18 @@ class TileBins:
         self.lv, self.geom, self.npix, self.level_tot_b = lv, geom, npix, level_tot_b
         self.pending = None   # a _Pending while the pair count of a deferred binning is unread
         self._views = {}
+        self._ptrs = {}
 
     def p(self, b, name):
         """Device pointer of buffer `name` of image b (None for maps that were not built)."""
-        which, i = self._SLOT[name]
-        if which == 1 and i >= 2 and not self.with_maps:
-            return None
-        return (self.blocks if which == 0 else self.pairs)[b].ptr(i)
+        key = (b, name)
+        v = self._ptrs.get(key, 0)
+        if v == 0:
+            which, i = self._SLOT[name]
+            v = None if (which == 1 and i >= 2 and not self.with_maps) else \
+                (self.blocks if which == 0 else self.pairs)[b].ptr(i)
+            self._ptrs[key] = v
+        return v
 
     def _list(self, name):
         v = self._views.get(name)
@@ -236,6 +248,7 @@ def _lv_key(lv):
 _GEOM = {}          # (H, W, TILE, levels) -> levels_geometry result
 _PAIRS_HW = {}      # binning configuration -> most pairs one image needed so far (sizes the next capacity)
 _LEVELS_SEEN = {}   # binning configuration -> per-level pair totals of its last binning (plans deferred launches)
+_WS1 = {}           # binning configuration -> count-phase workspace bytes
 _tls = threading.local()
 
 
@@ -314,9 +327,11 @@ class _Pending:
     __slots__ = ("lib", "info_p", "info_np", "blk", "cap", "budget", "key", "geo", "N", "L", "nt", "geom", "cutoff",
                  "max_pairs", "with_maps", "stream", "dev")
 
-    def __init__(self, **kw):
-        for k, v in kw.items():
-            setattr(self, k, v)
+    def __init__(self, lib, info_p, info_np, blk, cap, budget, key, geo, N, L, nt, geom, cutoff, max_pairs, with_maps,
+                 stream, dev):
+        self.lib, self.info_p, self.info_np, self.blk, self.cap, self.budget = lib, info_p, info_np, blk, cap, budget
+        self.key, self.geo, self.N, self.L, self.nt, self.geom = key, geo, N, L, nt, geom
+        self.cutoff, self.max_pairs, self.with_maps, self.stream, self.dev = cutoff, max_pairs, with_maps, stream, dev
 
 
 def _settle(p, rc, pb):
@@ -372,7 +387,9 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     info_t, info_np = _info_host()
     info_p = info_t.data_ptr()
     geo = (H, W, TILE, lvr)
-    ws1_bytes = lib.splat_bin_count_workspace_bytes(N, *geo)
+    ws1_bytes = _WS1.get(key)
+    if ws1_bytes is None:
+        ws1_bytes = _WS1[key] = lib.splat_bin_count_workspace_bytes(N, *geo)
     budget = -1 if max_pairs is None else int(max_pairs)
     defer = defer and B == 1 and cap > 0
     blocks, pairs, tots, level_tots = [], [], [], []
@@ -381,13 +398,12 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
         pb = _pair_buffers(lib, N, nt, cap, with_maps, dev, geo) if cap else None
         pp = (lambda i: None) if pb is None else pb.ptr
         info_np[0] = info_np[1] = 0
-        rc = lib.splat_bin(ptr(mu_[b]), ptr(sc_[b]), None if th_ is None else ptr(th_[b]), ptr(op_[b]), ptr(col_[b]),
+        rc = lib.splat_bin(_bptr(mu_, b), _bptr(sc_, b), _bptr(th_, b), _bptr(op_, b), _bptr(col_, b),
                            C, N, H, W, TILE, float(cutoff), lvr, sflags | (FLAG_DEFER if defer else 0), budget,
                            blk.ptr(0), blk.ptr(1), blk.ptr(2), blk.ptr(3), info_p, blk.ptr(4), ws1_bytes, cap, pp(0),
                            pp(1), None, pp(2) if with_maps else None, pp(3), 0 if pb is None else pb.nbytes(3), stream)
-        pend = _Pending(lib=lib, info_p=info_p, info_np=info_np, blk=blk, cap=cap, budget=budget, key=key, geo=geo, N=N,
-                        L=L, nt=nt, geom=geom, cutoff=cutoff, max_pairs=max_pairs, with_maps=with_maps, stream=stream,
-                        dev=dev)
+        pend = _Pending(lib, info_p, info_np, blk, cap, budget, key, geo, N, L, nt, geom, cutoff, max_pairs, with_maps,
+                        stream, dev)
         if defer:
             check(rc, "splat_bin")
             bins = TileBins(N, [None], H, W, TILE, ntx, nt, [blk], [pb], with_maps, lv, geom, npix, [None])
@@ -415,6 +431,7 @@ def _finish(bins):
     bins.tot_b[0] = tot
     bins.level_tot_b[0] = lt
     bins._views = {}
+    bins._ptrs = {}
     return redone
 
 
@@ -483,10 +500,9 @@ def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
 
 def _composite_buffers(B, P, C, dev):
     """out [B,P,C], T [B,P], asum [B,P], fg [B,P,C] as views of one allocation."""
-    buf = torch.empty(B * P * (2 * C + 2), device=dev)
     n = B * P
-    return (buf[:n * C].view(B, P, C), buf[n * C:n * (C + 1)].view(B, P), buf[n * (C + 1):n * (C + 2)].view(B, P),
-            buf[n * (C + 2):].view(B, P, C))
+    out, T, asum, fg = torch.empty(n * (2 * C + 2), device=dev).split_with_sizes((n * C, n, n, n * C))
+    return out.view(B, P, C), T.view(B, P), asum.view(B, P), fg.view(B, P, C)
 
 
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
@@ -507,7 +523,8 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
             ev = kernel_timer.record("fwd")
             try:
                 _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, tots[b]), (0, 1), 1,
-                            (bgf[b], out[b], T[b], asum[b], fg[b]), (None, None, None), stream)
+                            (_bptr(bgf, b), _bptr(out, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b)),
+                            (None, None, None), stream)
             finally:
                 kernel_timer.close("fwd", ev)
 
@@ -590,14 +607,10 @@ def _grads_bg_out(B, N, C, dev, has_th):
     """g_mu [B,N,2], g_scale [B,N,2], g_col [B,N,C], g_op [B,N], g_th [B,N] (or None) and g_bg [B,C]: views of one
     allocation (each a contiguous tensor of its own shape)."""
     n2, nc, n1 = B * N * 2, B * N * C, B * N
-    sizes = [n2, n2, nc, n1, n1 if has_th else 0, B * C]
-    buf = torch.empty(sum(sizes), device=dev)
-    out, o = [], 0
-    for k in sizes:
-        out.append(buf[o:o + k])
-        o += k
-    return (out[0].view(B, N, 2), out[1].view(B, N, 2), out[2].view(B, N, C), out[3].view(B, N),
-            out[4].view(B, N) if has_th else None, out[5].view(B, C))
+    sizes = (n2, n2, nc, n1, n1 if has_th else 0, B * C)
+    g_mu, g_sc, g_col, g_op, g_th, g_bg = torch.empty(sum(sizes), device=dev).split_with_sizes(sizes)
+    return (g_mu.view(B, N, 2), g_sc.view(B, N, 2), g_col.view(B, N, C), g_op.view(B, N),
+            g_th.view(B, N) if has_th else None, g_bg.view(B, C))
 
 
 def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stream):
@@ -616,7 +629,7 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
     tot = bins.tot_b[b]
     N = bins.N
     g_mu, g_scale, g_col, g_op, g_th = grads
-    sl = lambda t: None if (t is None or N == 0) else ptr(t[b])
+    sl = lambda t: None if N == 0 else _bptr(t, b)
     ev = kernel_timer.record("reduce")
     try:
         check(lib.splat_reduce_pairs(bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None,
@@ -630,9 +643,9 @@ def _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg, stream, lsc=None):
 def _bwd_buffers(lib, bins, b, C, with_bg, dev):
     """Per-pair sums and (optionally) the level-0 per-tile background partials, one allocation."""
     ns = (lib.splat_pair_sums_bytes(bins.tot_b[b]) // 4 + 3) & ~3   # partials start 16-byte aligned
-    nb = C * bins.ntiles0 if with_bg else 0
-    buf = torch.empty(ns + nb, device=dev)
-    return buf[:ns], (buf[ns:] if with_bg else None)
+    if not with_bg:
+        return torch.empty(ns, device=dev), None
+    return torch.empty(ns + C * bins.ntiles0, device=dev).split_with_sizes((ns, C * bins.ntiles0))
 
 
 def _backward_pairs(bins, b, flags, C, upstream, grads, g_bg, lib, stream, lsc=None):
@@ -668,8 +681,8 @@ def _backward_cull_raw(grad_out, bg, lsc, B, N, C, dev, has_th, T, asum, fg, bin
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
     flags = FLAG_ODDS if odds else 0
     for b in range(B):
-        up = (bgf[b], T[b], asum[b], fg[b], go[b], None, None, None)
-        _backward_pairs(bins, b, flags, C, up, grads, g_bg[b], lib, stream, lsc)
+        up = (_bptr(bgf, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b), _bptr(go, b), None, None, None)
+        _backward_pairs(bins, b, flags, C, up, grads, _bptr(g_bg, b), lib, stream, lsc)
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
