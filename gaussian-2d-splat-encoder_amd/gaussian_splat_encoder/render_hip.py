@@ -477,12 +477,25 @@ def _level_splits(bins, lt, mask):
     return sp
 
 
+def _fields_buffers(npix, C, dev):
+    """Packed level fields S_log [Pt], S_a [Pt], S_ac [Pt,C], views of one allocation."""
+    slog, sa, sac = torch.empty(npix * (2 + C), device=dev).split_with_sizes((npix, npix, npix * C))
+    return slog, sa, sac.view(npix, C)
+
+
+_SPLIT_WS = {}   # (C, H, W, TILE, levels, mask, splits) -> split-launch workspace bytes
+_ADJ_WS = {}     # (C, H, W, TILE, levels) -> upsample-adjoint workspace bytes
+
+
 def _fields_split_fwd(lib, bins, b, C, odd, lt, mask, fl, stream):
     """FIELDS forward of the coarse levels in `mask` of image b into the packed fields fl, one split launch."""
     L = bins.n_levels
     lvr = _lib.ctypes.byref(bins.lv)
     sp = _level_splits(bins, lt, mask)
-    nb = lib.splat_fields_split_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr, 1, L, mask, sp)
+    key = (C, bins.H, bins.W, bins.TILE, _lv_key(bins.lv), mask, tuple(sp))
+    nb = _SPLIT_WS.get(key)
+    if nb is None:
+        nb = _SPLIT_WS[key] = lib.splat_fields_split_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr, 1, L, mask, sp)
     ws = _ws(nb, fl[0].device) if nb else None
     check(lib.splat_render_fields_split(bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), C, bins.H, bins.W,
                                         bins.TILE, odd, lvr, 1, L, mask, sp, *[ptr(t) for t in fl], ptr(ws), nb,
@@ -566,8 +579,7 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     out, T, asum, fg = _composite_buffers(B, P, C, dev)
     L = bins.n_levels
     # packed fields, reused across the batch (stream order); slots [0, P) belong to level 0 and stay unused
-    fl = (_empty((bins.npix,), dev), _empty((bins.npix,), dev), _empty((bins.npix, C), dev)) if L > 1 else \
-        (None, None, None)
+    fl = _fields_buffers(bins.npix, C, dev) if L > 1 else (None, None, None)
     bgf = _f32(bg)
     odd = FLAG_ODDS if odds else 0
     lib, stream = _lib.load(), _lib.stream_ptr(dev)
@@ -581,7 +593,7 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
             if mask & ~1:
                 _fields_split_fwd(lib, bins, b, C, odd, lt, mask & ~1, fl, stream)
             _render_fwd(lib, bins, b, C, FLAG_UPS | odd | _wide(TILE, nt0, lt[0]), (0, 1), mask,
-                        (bgf[b], out[b], T[b], asum[b], fg[b]), fl, stream)
+                        (_bptr(bgf, b), _bptr(out, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b)), fl, stream)
         finally:
             kernel_timer.close("fwd", ev)
 
@@ -716,11 +728,15 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
     odd = FLAG_ODDS if odds else 0
     L = bins.n_levels
     npix = bins.npix if L > 1 else bins.H * bins.W
-    dsb = _empty((npix * (2 + C),), dev)   # the pixel upstream dS_log, dS_a, dS_ac, reused across the batch
-    dS = (dsb[:npix], dsb[npix:2 * npix], dsb[2 * npix:].view(npix, C))
+    dS = _fields_buffers(npix, C, dev)   # the pixel upstream dS_log, dS_a, dS_ac, reused across the batch
     lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
-    adj_ws = _ws(lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr), dev) if L > 1 \
-        else None
+    adj_ws = None
+    if L > 1:
+        key = (C, bins.H, bins.W, bins.TILE, _lv_key(bins.lv))
+        nb = _ADJ_WS.get(key)
+        if nb is None:
+            nb = _ADJ_WS[key] = lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr)
+        adj_ws = _ws(nb, dev)
     lsc = None if log_scale is None else _f32(log_scale)
     nt0 = bins.ntiles0
     for b in range(B):
@@ -730,7 +746,8 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
         ev = kernel_timer.record("bwd")
         try:
             _render_bwd(lib, bins, b, C, FLAG_UPS | odd | _wide(bins.TILE, nt0, lt[0]), (0, 1), mask,
-                        (bgf[b], T[b], asum[b], fg[b], go[b], *dS), sums, bg_part, stream)
+                        (_bptr(bgf, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b), _bptr(go, b), *dS), sums,
+                        bg_part, stream)
             if mask & ~1:
                 check(lib.splat_upsample_adjoint(C, bins.H, bins.W, bins.TILE, lvr, mask, *[ptr(t) for t in dS],
                                                  ptr(adj_ws), adj_ws.numel(), stream), "splat_upsample_adjoint")
@@ -741,7 +758,7 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
                       "splat_render_fields_split_bwd")
         finally:
             kernel_timer.close("bwd", ev)
-        _reduce(lib, bins, b, C, sums, bg_part, grads, g_bg[b], stream, lsc)
+        _reduce(lib, bins, b, C, sums, bg_part, grads, _bptr(g_bg, b), stream, lsc)
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
@@ -827,13 +844,15 @@ class _AlphaRenderLevels(torch.autograd.Function):
         ctx.odds = odds
         ctx.tiles = bins
         ctx.scale_is_log = scale_is_log
-        ctx.save_for_backward(color, bg, T, asum, fg, scale if scale_is_log else None)
+        ctx.fwd = (T, asum, fg)   # internal buffers, kept on ctx like the cull Function's
+        ctx.save_for_backward(color, bg, scale if scale_is_log else None)
         B, P, C = out.shape
         return out.view(B, H, W, C).permute(0, 3, 1, 2)
 
     @staticmethod
     def backward(ctx, grad_out):
-        color, bg, T, asum, fg, log_scale = ctx.saved_tensors
+        color, bg, log_scale = ctx.saved_tensors
+        T, asum, fg = ctx.fwd
         B, C, H, W = grad_out.shape
         go = grad_out.permute(0, 2, 3, 1).reshape(B, H * W, C)   # a view when the gradient has the image's layout
         g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(go, color, bg, ctx.has_theta, T, asum, fg,
