@@ -938,18 +938,32 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
   __shared__ int s_cnt[kWaves * kMaxRows];   // [wave][row - rmin]
   __shared__ int s_base[kMaxRows];            // [row]: where the block's next unit of the row goes
   __shared__ int s_w[kWaves];
-  const int tot = pair_count(info, cap);
-  if (tot == 0) return;   // no pairs, or a speculative launch past its capacity: no units to place
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int blk = blockIdx.x;
   const int t = threadIdx.x;
   const int g = blk * kBlock + t;
   const int nrows = L.rbase[L.n];
-  int h = 0, r0 = nrows, r1 = -1, q0 = 0, span = 0, w = 1;
+  // every global load of the block up front (one round trip): the splat's rect and offsets, and rows
+  // [4 t, 4 t + 4) of the row totals and of the block's column of the scanned row histogram
+  int4 rc = make_int4(0, 0, 0, 0);
+  int q0 = 0, q1 = 0;
   if (g < N) {
-    const int4 rc = rect[g];
+    rc = rect[g];
     q0 = offsets[g];
-    const int cnt = offsets[g + 1] - q0;
+    q1 = offsets[g + 1];
+  }
+  int rt[4], rh[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = 4 * t + k;
+    rt[k] = r < nrows ? rtot[r].x : 0;
+    rh[k] = r < nrows ? rowhist[(size_t)r * nb + blk].x : 0;
+  }
+  const int tot = pair_count(info, cap);
+  if (tot == 0) return;   // no pairs, or a speculative launch past its capacity: no units to place
+  int h = 0, r0 = nrows, r1 = -1, span = 0, w = 1;
+  if (g < N) {
+    const int cnt = q1 - q0;
     if (cnt > 0 && rc.z > 0) {
       w = rc.z;
       h = cnt / w;
@@ -973,20 +987,14 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
   s_span[t] = span;
   // first unit of every row: exclusive prefix of the row totals (rows [4 t, 4 t + 4) per thread)
   {
-    int v[4], sum = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int r = 4 * t + k;
-      v[k] = r < nrows ? rtot[r].x : 0;
-      sum += v[k];
-    }
+    const int sum = rt[0] + rt[1] + rt[2] + rt[3];
     int total;
     int run = block256_excl<false>(sum, s_w, total);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = 4 * t + k;
-      if (r >= rmin && r <= rmax) s_base[r] = run + rowhist[(size_t)r * nb + blk].x;
-      run += v[k];
+      if (r >= rmin && r <= rmax) s_base[r] = run + rh[k];
+      run += rt[k];
     }
   }
   int nbits = 0;
@@ -1062,19 +1070,24 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
 }
 
 // One workgroup of kRowThreads per tile row and chunk of at most kRowCols tile columns (blockIdx.y = global
-// row r, blockIdx.x = chunk of cw columns). The row's units are read kRowUnits at a time and those meeting the
-// chunk are kept, in order, in an LDS list; a difference array over their column ranges (LDS atomics) gives
-// the chunk's column counts, so its tile starts follow the row's pairs before the chunk (counted on the way).
-// Each wave then owns the columns j = wave, wave + 8, ...: it walks the list 64 units at a time and, per
-// column, the units covering it (one ballot) are that tile's next pairs in splat order, written by consecutive
-// lanes at the column's running position. A row of one round is read once; longer rows twice (counting, then
-// writing round by round, the running positions carried over).
+// row r, blockIdx.x = chunk of cw columns). Counting: the spans of the row's units (kRowUnits per round) give
+// the row's pairs before c0 and a difference array over the chunk's columns (LDS atomics), so the chunk's tile
+// starts follow. Writing: the units meeting the chunk are listed in LDS in unit order (their index and span),
+// their splat ids and splat-major indices gathered for the listed units only, then each wave owns the columns
+// j = wave, wave + 8, ...: it walks the list 64 units at a time and, per column, the units covering it (one
+// ballot) are that tile's next pairs in splat order, written by consecutive lanes at the column's running
+// position (kept in LDS). A row of at most kRowHold rounds has its spans read once, all rounds at a time, and
+// held in registers, and the lists of all its rounds are gathered together while they fit the list: three
+// dependent global round trips for the whole row (row totals, spans, gather). Longer rows read their spans
+// twice (counting, then writing round by round).
 constexpr int kRowThreads = 512;
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kRowItems = 4;                          // units per thread and round
 constexpr int kRowUnits = kRowThreads * kRowItems;   // 2048 units per round
 constexpr int kRowCols = 128;                         // columns per chunk, at most
-constexpr int kRowColsPerWave = kRowCols / kRowWaves;
+constexpr int kRowHold = 4;                           // rounds whose spans stay in registers
+constexpr int kRowList = 2048;                        // units meeting the chunk listed at once, at most
+static_assert(kRowList >= kRowUnits, "a round fits the list");
 
 __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const long long* __restrict__ info, int cap,
                                                             const int2* __restrict__ rtot, int cw,
@@ -1082,8 +1095,9 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
                                                             const int* __restrict__ uspan, int* __restrict__ gid_sorted,
                                                             int* __restrict__ tile_starts, int* __restrict__ pair_splat,
                                                             int* __restrict__ pair_q) {
-  __shared__ int s_cg[kRowUnits], s_cq[kRowUnits], s_cs[kRowUnits];   // the round's units meeting the chunk
-  __shared__ int s_diff[kRowCols + 1];   // difference array, then per column its first position
+  __shared__ int s_cu[kRowList], s_cs[kRowList];   // listed units: index (then splat id), span
+  __shared__ int s_cq[kRowList];                   // listed units: splat-major index of the first pair
+  __shared__ int s_diff[kRowCols + 1];   // difference array, then per column its running position
   __shared__ int s_kc[kRowItems][kRowWaves];
   __shared__ int s_red[3][kRowWaves];
   __shared__ int s_n;
@@ -1097,6 +1111,14 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
   const int c1 = min(c0 + cw, ntx), ncol = c1 - c0;
   const int tile0 = L.tbase[l] + (r - L.rbase[l]) * ntx + c0;
   const int nt = L.tbase[L.n];
+  // units and pairs of the rows before r and of row r (loaded before the pair count is known: one round trip)
+  int us = 0, pr = 0;
+  for (int i = t; i < r; i += kRowThreads) {
+    const int2 e = rtot[i];
+    us += e.x;
+    pr += e.y;
+  }
+  const int row_units = rtot[r].x;
   const int tot = pair_count(info, cap);
   if (tot == 0) {   // no pairs (or a speculative launch past its capacity): the empty list
     if (t < ncol) tile_starts[tile0 + t] = 0;
@@ -1107,13 +1129,6 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
     return;
   }
   if (r == 0 && c0 == 0 && t == 0) tile_starts[nt] = tot;
-  // units and pairs of the rows before r
-  int us = 0, pr = 0;
-  for (int i = t; i < r; i += kRowThreads) {
-    const int2 e = rtot[i];
-    us += e.x;
-    pr += e.y;
-  }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     us += __shfl_xor(us, m, 64);
@@ -1133,72 +1148,49 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
     pr += s_red[1][w];
   }
   // the row's units (at most one per pair: within the capacity the unit arrays are sized for)
-  const int ue = min(us + rtot[r].x, cap);
+  const int ue = min(us + row_units, cap);
   us = min(us, ue);
   const unsigned long long lt = (1ull << lane) - 1ull;
   const int nround = (ue - us + kRowUnits - 1) / kRowUnits;
-  // unit rb + 1024 k + t in slot k of thread t: (k, thread) order is unit order
-  int sp[kRowItems], gg[kRowItems], qq[kRowItems];
-  auto load = [&](int rb, bool all) {
+  const bool held = nround <= kRowHold;
+  // spans of round h in slot h (held rows) or of the current round in slot 0; unit rb + 512 k + t of a round
+  // sits in item k of thread t: (k, thread) order is unit order; w = 0 (no unit) meets no column
+  int sp[kRowHold][kRowItems];
+  auto load = [&](int h, int rb) {
 #pragma unroll
     for (int k = 0; k < kRowItems; ++k) {
       const int u = rb + kRowThreads * k + t;
-      const bool act = u < ue;
-      sp[k] = act ? uspan[u] : 0;   // w = 0: meets no column
-      if (all) {
-        gg[k] = act ? ug[u] : 0;
-        qq[k] = act ? uq[u] : 0;
-      }
+      sp[h][k] = u < ue ? uspan[u] : 0;
     }
   };
   auto meets = [&](int s1) {
     const int a = s1 & 0xffff, z = a + (s1 >> 16);
     return z > a && a < c1 && z > c0;
   };
-  // the round's units meeting the chunk into the list, in unit order; returns their number
-  auto compact = [&]() -> int {
-    unsigned long long mk[kRowItems];
-#pragma unroll
-    for (int k = 0; k < kRowItems; ++k) {
-      mk[k] = __ballot(meets(sp[k]));
-      if (lane == 0) s_kc[k][wv] = __popcll(mk[k]);
-    }
-    __syncthreads();
-    if (t == 0) {   // exclusive prefix in (k, wave) order
-      int run = 0;
-      for (int k = 0; k < kRowItems; ++k)
-        for (int w = 0; w < kRowWaves; ++w) {
-          const int c = s_kc[k][w];
-          s_kc[k][w] = run;
-          run += c;
-        }
-      s_n = run;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kRowItems; ++k)
-      if ((mk[k] >> lane) & 1) {
-        const int idx = s_kc[k][wv] + __popcll(mk[k] & lt);
-        s_cg[idx] = gg[k];
-        s_cq[idx] = qq[k];
-        s_cs[idx] = sp[k];
-      }
-    const int n = s_n;
-    __syncthreads();
-    return n;
-  };
   // counting: the row's pairs before c0 and, per column of the chunk, a difference array of the units meeting it
   int before = 0;
-  for (int rd = 0; rd < nround; ++rd) {
-    load(us + rd * kRowUnits, nround == 1);
+  auto count = [&](int h) {
 #pragma unroll
     for (int k = 0; k < kRowItems; ++k) {
-      const int a = sp[k] & 0xffff, z = a + (sp[k] >> 16);
+      const int a = sp[h][k] & 0xffff, z = a + (sp[h][k] >> 16);
       if (a < c0) before += min(z, c0) - a;
-      if (meets(sp[k])) {
+      if (meets(sp[h][k])) {
         atomicAdd(&s_diff[max(a, c0) - c0], 1);
         atomicAdd(&s_diff[min(z, c1) - c0], -1);
       }
+    }
+  };
+  if (held) {
+#pragma unroll
+    for (int h = 0; h < kRowHold; ++h)
+      if (h < nround) load(h, us + h * kRowUnits);
+#pragma unroll
+    for (int h = 0; h < kRowHold; ++h)
+      if (h < nround) count(h);
+  } else {
+    for (int rd = 0; rd < nround; ++rd) {
+      load(0, us + rd * kRowUnits);
+      count(0);
     }
   }
 #pragma unroll
@@ -1225,43 +1217,97 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
       run += __shfl(inc, 63, 64);
     }
   }
-  __syncthreads();
-  // writing: wave wv owns columns wv + 16 m; its running positions stay in registers across rounds
-  int pos[kRowColsPerWave];
+  // writing. The list holds n units. A round's units meeting the chunk (`mark`: their number, per (k, wave)
+  // their first list slot) go to the list in unit order (`place`) once it has room for them; flush() gathers the
+  // listed units' ids, writes their pairs and empties the list.
+  int n = 0;
+  unsigned long long mk[kRowItems];
+  auto mark = [&](int h) -> int {
 #pragma unroll
-  for (int m = 0; m < kRowColsPerWave; ++m) {
-    const int j = wv + kRowWaves * m;
-    pos[m] = j < ncol ? s_diff[j] : 0;
-  }
-  for (int rd = 0; rd < nround; ++rd) {
-    if (nround > 1) load(us + rd * kRowUnits, true);
-    const int n = compact();
+    for (int k = 0; k < kRowItems; ++k) {
+      mk[k] = __ballot(meets(sp[h][k]));
+      if (lane == 0) s_kc[k][wv] = __popcll(mk[k]);
+    }
+    __syncthreads();
+    if (t == 0) {   // exclusive prefix in (k, wave) order
+      int run = 0;
+      for (int k = 0; k < kRowItems; ++k)
+        for (int w = 0; w < kRowWaves; ++w) {
+          const int c = s_kc[k][w];
+          s_kc[k][w] = run;
+          run += c;
+        }
+      s_n = run;
+    }
+    __syncthreads();
+    return s_n;
+  };
+  auto place = [&](int h, int rb) {
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k)
+      if ((mk[k] >> lane) & 1) {
+        const int idx = n + s_kc[k][wv] + __popcll(mk[k] & lt);
+        s_cu[idx] = rb + kRowThreads * k + t;
+        s_cs[idx] = sp[h][k];
+      }
+  };
+  auto flush = [&]() {
+    __syncthreads();   // the list is complete
+    for (int i = t; i < n; i += kRowThreads) {   // gather: unit index -> splat id, splat-major index
+      const int u = s_cu[i];
+      s_cu[i] = ug[u];
+      s_cq[i] = uq[u];
+    }
+    __syncthreads();
     for (int b = 0; b < n; b += 64) {
       const int i = b + lane;
       const bool act = i < n;
       const int s1 = act ? s_cs[i] : 0;
-      const int g = act ? s_cg[i] : 0, q = act ? s_cq[i] : 0;
+      const int g = act ? s_cu[i] : 0, q = act ? s_cq[i] : 0;
       const int a = s1 & 0xffff, z = a + (s1 >> 16);
-#pragma unroll
-      for (int m = 0; m < kRowColsPerWave; ++m) {
-        const int c = c0 + wv + kRowWaves * m;
-        if (c >= c1) break;
+      for (int j = wv; j < ncol; j += kRowWaves) {   // the wave's columns; their positions only it touches
+        const int c = c0 + j;
         const bool cov = act && a <= c && c < z;
         const unsigned long long msk = __ballot(cov);
-        if (cov) {
-          const int p = pos[m] + __popcll(msk & lt);
-          const int qc = q + (c - a);
-          if ((unsigned)p < (unsigned)cap) {
-            gid_sorted[p] = g;
-            if (pair_q) pair_q[p] = qc;
+        if (msk) {
+          const int pos = s_diff[j];
+          if (cov) {
+            const int p = pos + __popcll(msk & lt);
+            const int qc = q + (c - a);
+            if ((unsigned)p < (unsigned)cap) {
+              gid_sorted[p] = g;
+              if (pair_q) pair_q[p] = qc;
+            }
+            if (pair_splat && (unsigned)qc < (unsigned)cap) pair_splat[qc] = g;
           }
-          if (pair_splat && (unsigned)qc < (unsigned)cap) pair_splat[qc] = g;
+          if (lane == 0) s_diff[j] = pos + __popcll(msk);
         }
-        pos[m] += __popcll(msk);
       }
     }
-    __syncthreads();   // before the next round's list
+    __syncthreads();   // before the list is refilled
+    n = 0;
+  };
+  // kRowList >= kRowUnits: a round always fits an empty list
+  if (held) {
+#pragma unroll
+    for (int h = 0; h < kRowHold; ++h) {
+      if (h < nround) {
+        const int m = mark(h);
+        if (n + m > kRowList) flush();
+        place(h, us + h * kRowUnits);
+        n += m;
+      }
+    }
+  } else {
+    for (int rd = 0; rd < nround; ++rd) {
+      load(0, us + rd * kRowUnits);
+      const int m = mark(0);
+      if (n + m > kRowList) flush();
+      place(0, us + rd * kRowUnits);
+      n += m;
+    }
   }
+  flush();
 }
 
 // ----------------------------------------------------------------------------------------------------
