@@ -82,8 +82,11 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   __shared__ long long s_part[kWaves];
   __shared__ int s_lev[kMaxLevels];
   __shared__ int s_du[kMaxRows + 1], s_dp[kMaxRows + 1];
+  __shared__ float4 s_rec[kBlock * 4];   // the block's records, written out coalesced
   const int g = blockIdx.x * kBlock + threadIdx.x;
   const int nrows = L.rbase[L.n];
+  // float4 k of splat t of the block sits at s_rec[4 t + (k ^ (t & 3))] (the xor spreads a wave's writes)
+  auto rec_slot = [](int t, int k) { return 4 * t + (k ^ (t & 3)); };
   if (do_bin) {
     for (int i = threadIdx.x; i < kMaxLevels; i += kBlock) s_lev[i] = 0;
     if (rowhist)
@@ -107,12 +110,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     if (C > 1) col.y = color[(size_t)g * C + 1];
     if (C > 2) col.z = color[(size_t)g * C + 2];
     if (C > 3) col.w = color[(size_t)g * C + 3];
-    float4* r = rec + (size_t)g * 4;
-    r[0] = make_float4(m.x, m.y, cs * ky, sn * ky);
+    const int t = threadIdx.x;
+    s_rec[rec_slot(t, 0)] = make_float4(m.x, m.y, cs * ky, sn * ky);
     const float op = opacity[g];
-    r[1] = make_float4(-sn * kx, cs * kx, op, log2f(op));
-    r[2] = col;
-    r[3] = make_float4(s.x, s.y, cs, sn);
+    s_rec[rec_slot(t, 1)] = make_float4(-sn * kx, cs * kx, op, log2f(op));
+    s_rec[rec_slot(t, 2)] = col;
+    s_rec[rec_slot(t, 3)] = make_float4(s.x, s.y, cs, sn);
     if (do_bin) {
       // level: render_triton.py:925-932 + 950-952 (octave), :904-913 (coarse/fine split)
       int lev = 0;
@@ -152,6 +155,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
         }
       }
     }
+  }
+  __syncthreads();
+  {   // the block's records: 16 consecutive bytes per thread and store
+    const int nrec = 4 * min(kBlock, N - (int)blockIdx.x * kBlock);
+    float4* dst = rec + (size_t)blockIdx.x * kBlock * 4;
+    for (int i = threadIdx.x; i < nrec; i += kBlock) dst[i] = s_rec[rec_slot(i >> 2, i & 3)];
   }
   if (!do_bin) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -337,14 +346,24 @@ __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offs
   const bool last = blk == nb - 1;
   if (threadIdx.x == 0) s_bad = 0;
   if (threadIdx.x < kMaxLevels) s_lev[threadIdx.x] = 0;
-  // prefix over predecessors (all blocks for the last one, to get the total and the error bits)
-  long long acc = 0;
+  // every global load up front (one round trip): the splat's count, and the prefix over predecessors (all
+  // blocks for the last one, to get the total, the error bits and the per-level totals)
+  const int g = blk * kBlock + threadIdx.x;
+  const int c = g < N ? offsets[g] : 0;
+  long long acc = 0, lev[kMaxLevels];
+#pragma unroll
+  for (int l = 0; l < kMaxLevels; ++l) lev[l] = 0;
   int bad = 0;
   const int upto = last ? nb : blk;
   for (int b = threadIdx.x; b < upto; b += kBlock) {
     const long long v = sums[(size_t)b * kSumCols];
     if (b < blk) acc += v & ~kBadBit;
     bad |= (v & kBadBit) ? 1 : 0;
+    if (last) {
+#pragma unroll
+      for (int l = 0; l < kMaxLevels; ++l)
+        if (l < nlev) lev[l] += sums[(size_t)b * kSumCols + 1 + l];
+    }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
@@ -354,8 +373,6 @@ __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offs
   long long pre_blk = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) pre_blk += s_r[w];
-  const int g = blk * kBlock + threadIdx.x;
-  const int c = g < N ? offsets[g] : 0;
   const int inc = wave_incl_scan(c, lane);
   if (lane == 63) s_w[wv] = inc;
   __syncthreads();
@@ -369,9 +386,10 @@ __global__ __launch_bounds__(kBlock) void k_offsets_fused(int* __restrict__ offs
   if (!last) return;
   const long long tot = pre_blk + btot;
   if (g == N - 1) offsets[N] = (int)tot;
-  for (int l = 0; l < nlev; ++l) {
-    long long x = 0;
-    for (int b = threadIdx.x; b < nb; b += kBlock) x += sums[(size_t)b * kSumCols + 1 + l];
+#pragma unroll
+  for (int l = 0; l < kMaxLevels; ++l) {
+    if (l >= nlev) break;
+    long long x = lev[l];
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
     if (lane == 0 && x) atomicAdd((unsigned long long*)&s_lev[l], (unsigned long long)x);
