@@ -1107,6 +1107,10 @@ constexpr int kRowHold = 4;                           // rounds whose spans stay
 constexpr int kRowList = 2048;                        // units meeting the chunk listed at once, at most
 static_assert(kRowList >= kRowUnits, "a round fits the list");
 
+// REG (chunks of at most kRowRegCols columns): each wave keeps its columns' running positions in registers;
+// otherwise in LDS (s_diff), read and advanced by the owning wave.
+constexpr int kRowRegCols = 2 * kRowWaves;
+template <bool REG>
 __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const long long* __restrict__ info, int cap,
                                                             const int2* __restrict__ rtot, int cw,
                                                             const int* __restrict__ ug, const int* __restrict__ uq,
@@ -1269,8 +1273,18 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
         s_cs[idx] = sp[h][k];
       }
   };
+  int rpos[REG ? kRowRegCols / kRowWaves : 1];   // REG: the wave's columns' running positions
+  bool have_pos = false;
   auto flush = [&]() {
-    __syncthreads();   // the list is complete
+    __syncthreads();   // the list is complete (and the column starts written)
+    if (REG && !have_pos) {
+#pragma unroll
+      for (int m = 0; m < (REG ? kRowRegCols / kRowWaves : 1); ++m) {
+        const int j = wv + kRowWaves * m;
+        rpos[m] = j < ncol ? s_diff[j] : 0;
+      }
+      have_pos = true;
+    }
     for (int i = t; i < n; i += kRowThreads) {   // gather: unit index -> splat id, splat-major index
       const int u = s_cu[i];
       s_cu[i] = ug[u];
@@ -1283,22 +1297,38 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
       const int s1 = act ? s_cs[i] : 0;
       const int g = act ? s_cu[i] : 0, q = act ? s_cq[i] : 0;
       const int a = s1 & 0xffff, z = a + (s1 >> 16);
-      for (int j = wv; j < ncol; j += kRowWaves) {   // the wave's columns; their positions only it touches
-        const int c = c0 + j;
-        const bool cov = act && a <= c && c < z;
-        const unsigned long long msk = __ballot(cov);
-        if (msk) {
-          const int pos = s_diff[j];
-          if (cov) {
-            const int p = pos + __popcll(msk & lt);
-            const int qc = q + (c - a);
-            if ((unsigned)p < (unsigned)cap) {
-              gid_sorted[p] = g;
-              if (pair_q) pair_q[p] = qc;
-            }
-            if (pair_splat && (unsigned)qc < (unsigned)cap) pair_splat[qc] = g;
+      // column j of the chunk: the units covering it are its next pairs, from its running position pos
+      auto column = [&](int j, int pos, unsigned long long msk, bool cov) {
+        if (cov) {
+          const int p = pos + __popcll(msk & lt);
+          const int qc = q + (c0 + j - a);
+          if ((unsigned)p < (unsigned)cap) {
+            gid_sorted[p] = g;
+            if (pair_q) pair_q[p] = qc;
           }
-          if (lane == 0) s_diff[j] = pos + __popcll(msk);
+          if (pair_splat && (unsigned)qc < (unsigned)cap) pair_splat[qc] = g;
+        }
+      };
+      // the wave's columns j = wv + 8 m, whose positions only it touches
+      if constexpr (REG) {
+#pragma unroll
+        for (int m = 0; m < kRowRegCols / kRowWaves; ++m) {
+          const int j = wv + kRowWaves * m;
+          if (j >= ncol) break;
+          const bool cov = act && a <= c0 + j && c0 + j < z;
+          const unsigned long long msk = __ballot(cov);
+          column(j, rpos[m], msk, cov);
+          rpos[m] += __popcll(msk);
+        }
+      } else {
+        for (int j = wv; j < ncol; j += kRowWaves) {
+          const bool cov = act && a <= c0 + j && c0 + j < z;
+          const unsigned long long msk = __ballot(cov);
+          if (msk) {
+            const int pos = s_diff[j];
+            column(j, pos, msk, cov);
+            if (lane == 0) s_diff[j] = pos + __popcll(msk);
+          }
         }
       }
     }
@@ -1520,8 +1550,12 @@ int bin_pairs_launch(const int* rect, const int* offsets, const void* ws_count, 
     // chunks of at most kRowCols columns, about 8 per row of the widest level (measured: 4 to 12 chunks, 256 to
     // 1024 threads, 2 to 8 units per thread; this is the fastest at 768 x 768 and 2048 x 2048)
     const int cw = min(kRowCols, max(8, div_up(mxtx, 8)));
-    k_expand_row<<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(L, dinfo, t, rtot, cw, ug, uq, uspan,
-                                                                            gid_sorted, tile_starts, pair_splat, pair_q);
+    if (cw <= kRowRegCols)
+      k_expand_row<true><<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(
+          L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts, pair_splat, pair_q);
+    else
+      k_expand_row<false><<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(
+          L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts, pair_splat, pair_q);
     return check_launch("k_expand_row");
   }
   const PairsPlan pl = plan_pairs(nt, t);
