@@ -1094,10 +1094,10 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
 // their splat ids and splat-major indices gathered for the listed units only, then each wave owns the columns
 // j = wave, wave + 8, ...: it walks the list 64 units at a time and, per column, the units covering it (one
 // ballot) are that tile's next pairs in splat order, written by consecutive lanes at the column's running
-// position (kept in LDS). A row of at most kRowHold rounds has its spans read once, all rounds at a time, and
-// held in registers, and the lists of all its rounds are gathered together while they fit the list: three
-// dependent global round trips for the whole row (row totals, spans, gather). Longer rows read their spans
-// twice (counting, then writing round by round).
+// position (in registers for chunks of up to kRowRegCols columns, else in LDS). Spans are read kRowHold rounds
+// at a time. A row of at most kRowHold rounds has its spans read once and held in registers, and the lists of
+// all its rounds are gathered together while they fit the list: three dependent global round trips for the
+// whole row (row totals, spans, gather). Longer rows read their spans twice (counting, then writing).
 constexpr int kRowThreads = 512;
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kRowItems = 4;                          // units per thread and round
@@ -1175,7 +1175,7 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
   const unsigned long long lt = (1ull << lane) - 1ull;
   const int nround = (ue - us + kRowUnits - 1) / kRowUnits;
   const bool held = nround <= kRowHold;
-  // spans of round h in slot h (held rows) or of the current round in slot 0; unit rb + 512 k + t of a round
+  // spans of round r0 + h of the current group of kRowHold rounds in slot h; unit rb + 512 k + t of a round
   // sits in item k of thread t: (k, thread) order is unit order; w = 0 (no unit) meets no column
   int sp[kRowHold][kRowItems];
   auto load = [&](int h, int rb) {
@@ -1202,18 +1202,17 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
       }
     }
   };
-  if (held) {
+  // rounds in groups of kRowHold, a group's spans loaded at once (a held row is one group)
+  auto load_group = [&](int r0) {
 #pragma unroll
     for (int h = 0; h < kRowHold; ++h)
-      if (h < nround) load(h, us + h * kRowUnits);
+      if (r0 + h < nround) load(h, us + (r0 + h) * kRowUnits);
+  };
+  for (int r0 = 0; r0 < nround; r0 += kRowHold) {
+    load_group(r0);
 #pragma unroll
     for (int h = 0; h < kRowHold; ++h)
-      if (h < nround) count(h);
-  } else {
-    for (int rd = 0; rd < nround; ++rd) {
-      load(0, us + rd * kRowUnits);
-      count(0);
-    }
+      if (r0 + h < nround) count(h);
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) before += __shfl_xor(before, m, 64);
@@ -1336,23 +1335,16 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
     n = 0;
   };
   // kRowList >= kRowUnits: a round always fits an empty list
-  if (held) {
+  for (int r0 = 0; r0 < nround; r0 += kRowHold) {
+    if (!held) load_group(r0);   // a held row's spans are still in registers
 #pragma unroll
     for (int h = 0; h < kRowHold; ++h) {
-      if (h < nround) {
+      if (r0 + h < nround) {
         const int m = mark(h);
         if (n + m > kRowList) flush();
-        place(h, us + h * kRowUnits);
+        place(h, us + (r0 + h) * kRowUnits);
         n += m;
       }
-    }
-  } else {
-    for (int rd = 0; rd < nround; ++rd) {
-      load(0, us + rd * kRowUnits);
-      const int m = mark(0);
-      if (n + m > kRowList) flush();
-      place(0, us + rd * kRowUnits);
-      n += m;
     }
   }
   flush();
