@@ -1094,7 +1094,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
 // their splat ids and splat-major indices gathered for the listed units only, then each wave owns the columns
 // j = wave, wave + 8, ...: it walks the list 64 units at a time and, per column, the units covering it (one
 // ballot) are that tile's next pairs in splat order, written by consecutive lanes at the column's running
-// position (in registers for chunks of up to kRowRegCols columns, else in LDS). Spans are read kRowHold rounds
+// position (in registers for chunks of up to 32 columns, else in LDS). Spans are read kRowHold rounds
 // at a time. A row of at most kRowHold rounds has its spans read once and held in registers, and the lists of
 // all its rounds are gathered together while they fit the list: three dependent global round trips for the
 // whole row (row totals, spans, gather). Longer rows read their spans twice (counting, then writing).
@@ -1107,10 +1107,9 @@ constexpr int kRowHold = 4;                           // rounds whose spans stay
 constexpr int kRowList = 2048;                        // units meeting the chunk listed at once, at most
 static_assert(kRowList >= kRowUnits, "a round fits the list");
 
-// REG (chunks of at most kRowRegCols columns): each wave keeps its columns' running positions in registers;
-// otherwise in LDS (s_diff), read and advanced by the owning wave.
-constexpr int kRowRegCols = 2 * kRowWaves;
-template <bool REG>
+// CPW > 0 (chunks of at most CPW columns per wave): each wave keeps its columns' running positions in
+// registers; CPW = 0: in LDS (s_diff), read and advanced by the owning wave.
+template <int CPW>
 __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const long long* __restrict__ info, int cap,
                                                             const int2* __restrict__ rtot, int cw,
                                                             const int* __restrict__ ug, const int* __restrict__ uq,
@@ -1272,13 +1271,14 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
         s_cs[idx] = sp[h][k];
       }
   };
-  int rpos[REG ? kRowRegCols / kRowWaves : 1];   // REG: the wave's columns' running positions
+  constexpr bool REG = CPW > 0;
+  int rpos[REG ? CPW : 1];   // REG: the wave's columns' running positions
   bool have_pos = false;
   auto flush = [&]() {
     __syncthreads();   // the list is complete (and the column starts written)
     if (REG && !have_pos) {
 #pragma unroll
-      for (int m = 0; m < (REG ? kRowRegCols / kRowWaves : 1); ++m) {
+      for (int m = 0; m < (REG ? CPW : 1); ++m) {
         const int j = wv + kRowWaves * m;
         rpos[m] = j < ncol ? s_diff[j] : 0;
       }
@@ -1311,7 +1311,7 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
       // the wave's columns j = wv + 8 m, whose positions only it touches
       if constexpr (REG) {
 #pragma unroll
-        for (int m = 0; m < kRowRegCols / kRowWaves; ++m) {
+        for (int m = 0; m < CPW; ++m) {
           const int j = wv + kRowWaves * m;
           if (j >= ncol) break;
           const bool cov = act && a <= c0 + j && c0 + j < z;
@@ -1542,12 +1542,16 @@ int bin_pairs_launch(const int* rect, const int* offsets, const void* ws_count, 
     // chunks of at most kRowCols columns, about 8 per row of the widest level (measured: 4 to 12 chunks, 256 to
     // 1024 threads, 2 to 8 units per thread; this is the fastest at 768 x 768 and 2048 x 2048)
     const int cw = min(kRowCols, max(8, div_up(mxtx, 8)));
-    if (cw <= kRowRegCols)
-      k_expand_row<true><<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(
-          L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts, pair_splat, pair_q);
+    const dim3 grid(div_up(mxtx, cw), cp.nrows);
+    if (cw <= 2 * kRowWaves)
+      k_expand_row<2><<<grid, kRowThreads, 0, st>>>(L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts,
+                                                     pair_splat, pair_q);
+    else if (cw <= 4 * kRowWaves)
+      k_expand_row<4><<<grid, kRowThreads, 0, st>>>(L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts,
+                                                     pair_splat, pair_q);
     else
-      k_expand_row<false><<<dim3(div_up(mxtx, cw), cp.nrows), kRowThreads, 0, st>>>(
-          L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts, pair_splat, pair_q);
+      k_expand_row<0><<<grid, kRowThreads, 0, st>>>(L, dinfo, t, rtot, cw, ug, uq, uspan, gid_sorted, tile_starts,
+                                                     pair_splat, pair_q);
     return check_launch("k_expand_row");
   }
   const PairsPlan pl = plan_pairs(nt, t);
