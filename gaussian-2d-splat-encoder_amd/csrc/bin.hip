@@ -990,15 +990,40 @@ __global__ __launch_bounds__(kBlock) void k_scatter_units(const int4* __restrict
       span = rc.x | (w << 16);
     }
   }
-  // the block's row range [rmin, rmax] (block-uniform; maxima of values >= -1, the max-scan's identity)
-  int rmax, rmin;
-  block256_excl<true>(r1, s_w, rmax);
-  block256_excl<true>(nrows - r0, s_w, rmin);
-  rmin = nrows - rmin;
+  // one barrier for: the block's row range [rmin, rmax] (block-uniform; a splat without units has r0 = nrows,
+  // r1 = -1) and the first unit u0 of splat t within the block (exclusive prefix of h; nu = the block's total)
+  int inc = h, mx = r1, mn = r0;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    mx = max(mx, __shfl_xor(mx, m, 64));
+    mn = min(mn, __shfl_xor(mn, m, 64));
+  }
+  __shared__ int s_w3[3][kWaves];
+  if (lane == 63) s_w3[0][wv] = inc;
+  if (lane == 0) {
+    s_w3[1][wv] = mx;
+    s_w3[2][wv] = mn;
+  }
+  __syncthreads();
+  int pre = 0, nu = 0, rmax = -1, rmin = nrows;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int x = s_w3[0][w];
+    if (w < wv) pre += x;
+    nu += x;
+    rmax = max(rmax, s_w3[1][w]);
+    rmin = min(rmin, s_w3[2][w]);
+  }
+  int ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = 0;
+  const int u0 = pre + ex;
   if (rmax < rmin) return;   // the block holds no units
   const int nr = rmax - rmin + 1;
-  int nu;
-  const int u0 = block256_excl<false>(h, s_w, nu);   // first unit of splat t within the block; nu = block total
   s_u0[t] = u0;
   s_r0[t] = r0;
   s_q0[t] = q0;
