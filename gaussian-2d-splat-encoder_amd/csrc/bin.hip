@@ -177,8 +177,11 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   }
   if (threadIdx.x < kMaxLevels) block_sums[(size_t)blockIdx.x * kSumCols + 1 + threadIdx.x] = s_lev[threadIdx.x];
   if (!rowhist) return;
-  // inclusive scan of the difference arrays over the rows: thread t takes rows [4 t, 4 t + 4)
+  // inclusive scan of the difference arrays over the rows: thread t takes rows [4 t, 4 t + 4); up to 256 rows
+  // wave 0 alone (no barrier)
   static_assert(kMaxRows <= 4 * kBlock, "rows per thread");
+  const bool one_wave = nrows <= 256;
+  if (one_wave && wv != 0) return;
   __shared__ int s_w[kWaves];
   int du[4], dp[4], su = 0, sp = 0;
 #pragma unroll
@@ -189,9 +192,15 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     su += du[k];
     sp += dp[k];
   }
-  int t_u, t_p;
-  int pu = block256_excl<false>(su, s_w, t_u);
-  int pp = block256_excl<false>(sp, s_w, t_p);
+  int pu, pp;
+  if (one_wave) {
+    pu = wave_incl_scan<int>(su, lane) - su;
+    pp = wave_incl_scan<int>(sp, lane) - sp;
+  } else {
+    int t_u, t_p;
+    pu = block256_excl<false>(su, s_w, t_u);
+    pp = block256_excl<false>(sp, s_w, t_p);
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int r = 4 * (int)threadIdx.x + k;
