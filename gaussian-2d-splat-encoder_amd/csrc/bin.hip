@@ -1741,23 +1741,40 @@ int splat_bin_pairs(const int* rect, const int* offsets, const void* ws_count, i
 
 namespace {
 
-// The one read of a binning's totals (info_host[0, 2 + nlev)): waits for the read-back event recorded behind the
-// count phase, takes a copy when the count kernel's stores into pinned memory were not seen, and applies the
-// checks of splat_bin: error bits, the per-level budget, the capacity.
+// Whether every entry of a pinned totals buffer has been written by the count kernel.
+bool totals_seen(const long long* info_host, int ninfo) {
+  const volatile long long* ih = info_host;
+  for (int i = 0; i < ninfo; ++i)
+    if (ih[i] == kUnsetInfo) return false;
+  return true;
+}
+
+// The one read of a binning's totals (info_host[0, 2 + nlev)) and the checks of splat_bin: error bits, the
+// per-level budget, the capacity. Pinned totals (the count kernel stores them into host memory itself, every
+// entry preset to kUnsetInfo) are polled until every entry is written, without an event: recording one costs the
+// host several microseconds per render. Between polls the stream is queried now and then; once it is idle the
+// count kernel has run, and totals still unseen are copied from the device. Pageable totals wait for the
+// read-back event recorded behind their copy.
 int read_totals(const char* who, long long* info_host, const long long* info, int nlev, long long max_pairs,
                 long long pair_cap, hipStream_t st) {
   const int ninfo = 2 + nlev;
-  hipEvent_t ev = readback_event();
-  if (!ev || hipEventSynchronize(ev) != hipSuccess) return set_error(kHipError, "%s: reading the pair totals failed", who);
   if (host_mirror(info_host)) {
-    volatile long long* ih = info_host;
-    bool seen = true;
-    for (int i = 0; i < ninfo; ++i) seen = seen && ih[i] != kUnsetInfo;
-    if (!seen) {   // the kernel's stores did not reach the host: this call copies them (the next tries again)
-      if (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
-          hipStreamSynchronize(st) != hipSuccess)
+    for (unsigned it = 1; !totals_seen(info_host, ninfo); ++it) {
+      __builtin_ia32_pause();
+      if ((it & 1023) != 0) continue;
+      const hipError_t q = hipStreamQuery(st);
+      if (q == hipErrorNotReady) continue;
+      if (q != hipSuccess) return set_error(kHipError, "%s: reading the pair totals failed", who);
+      if (!totals_seen(info_host, ninfo) &&   // the kernel's stores did not reach the host: copy them
+          (hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
+           hipStreamSynchronize(st) != hipSuccess))
         return set_error(kHipError, "%s: reading the pair totals failed", who);
+      break;
     }
+  } else {
+    hipEvent_t ev = readback_event();
+    if (!ev || hipEventSynchronize(ev) != hipSuccess)
+      return set_error(kHipError, "%s: reading the pair totals failed", who);
   }
   const long long tot = info_host[0];
   if (info_host[1] & 1) return set_error(kInvalid, "%s: a splat has an empty tile rect (negative cutoff or scale)", who);
@@ -1808,11 +1825,12 @@ int splat_bin(const float* mu, const float* scale, const float* theta, const flo
   int rc = bin_count_launch(mu, scale, theta, opacity, color, C, N, L, R, TILE, cutoff, flags, rec, rect, offsets,
                             info, mirror, ws_count, st);
   if (rc) return rc;
-  hipEvent_t ev = readback_event();
-  if (!ev ||
-      (!mirror && hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess) ||
-      hipEventRecord(ev, st) != hipSuccess)
-    return set_error(kHipError, "splat_bin: queueing the read of the pair totals failed");
+  if (!mirror) {   // pageable totals: a copy and the event read_totals waits for
+    hipEvent_t ev = readback_event();
+    if (!ev || hipMemcpyAsync(info_host, info, sizeof(long long) * ninfo, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipEventRecord(ev, st) != hipSuccess)
+      return set_error(kHipError, "splat_bin: queueing the read of the pair totals failed");
+  }
   if (spec) {
     rc = bin_pairs_launch(rect, offsets, ws_count, N, L, (int)pair_cap, info, gid_sorted, tile_starts, pair_splat, pair_q,
                           ws_pairs, st);

@@ -132,7 +132,8 @@ int splat_bin(const float *mu, const float *scale, const float *theta, const flo
  * render_triton.py:391, which splat_bin does inside): waits for the totals to land in info_host[0, 2 + nlev) and
  * returns splat_bin's status for them (0, 6 past pair_cap, 7 over max_pairs, 1 / 4 error bits), with the same
  * info, info_host, max_pairs and pair_cap as that call. Call it on the thread (and current device) that queued the binning,
- * before that thread's next splat_bin: the wait is on a read-back event per thread and device. Launches queued in between on the
+ * before the next splat_bin into the same info_host: pinned totals are polled (splat_bin presets every entry), pageable
+ * ones wait on a read-back event per thread and device. Launches queued in between on the
  * speculative pair list have run on the right list when it returns 0; on status 6 they read an empty list and
  * must be repeated after splat_bin_pairs. */
 int splat_bin_finish(long long *info_host, const long long *info, int nlev, long long max_pairs, long long pair_cap,
@@ -147,7 +148,7 @@ int splat_bin_finish(long long *info_host, const long long *info, int nlev, long
  * fit the scratch: 12 bytes per pair plus 8 bytes per tile row and 256 splats for level tables of at most
  * 1,024 tile rows (pair_cap up to ~5M at 768 x 768), about 25 bytes per pair past that; a larger request
  * returns status 5 before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device (per
- * thread) looks up the scratch address and creates the read-back event. Statuses as splat_bin. Every call
+ * thread) looks up the scratch address and, for a pageable info_host, creates the read-back event. Statuses as splat_bin. Every call
  * on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams or threads before the
  * previous call's kernels have finished) race; calls in one stream do not. Nothing in the scratch needs to
  * start at zero: every region is written before it is read within a call. */
