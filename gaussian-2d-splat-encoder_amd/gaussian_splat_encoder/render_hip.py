@@ -265,16 +265,26 @@ def _align(n):
     return (n + 255) & ~255
 
 
+_CARVE_OFF = {}   # tuple of sizes -> sub-buffer offsets (the renders of one configuration repeat their sizes)
+
+
 class _Carve:
     """Sub-buffers of one uint8 device allocation (256-byte aligned)."""
 
     def __init__(self, sizes, dev, zero=False):
-        self.off, o = [], 0
-        for n in sizes:
-            self.off.append(o)
-            o += _align(max(int(n), 1))
-        self.off.append(o)
-        self.buf = (torch.zeros if zero else torch.empty)(o, dtype=torch.uint8, device=dev)
+        key = tuple(sizes)
+        off = _CARVE_OFF.get(key)
+        if off is None:
+            off, o = [], 0
+            for n in sizes:
+                off.append(o)
+                o += _align(max(int(n), 1))
+            off.append(o)
+            if len(_CARVE_OFF) > 4096:
+                _CARVE_OFF.clear()
+            _CARVE_OFF[key] = off
+        self.off = off
+        self.buf = (torch.zeros if zero else torch.empty)(off[-1], dtype=torch.uint8, device=dev)
         self.base = self.buf.data_ptr()
 
     def ptr(self, i):
