@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
 }
 
 // One entry of the count phase's totals, into `info` and, when the caller gave one, into its mirror in pinned
-// host memory (a system-scope store: the host reads it after waiting for an event recorded behind the kernel).
+// host memory (a system-scope store: the host polls the mirror until every entry it preset has been written).
 __device__ __forceinline__ void put_info(long long* info, long long* mirror, int i, long long v) {
   info[i] = v;
   if (mirror) __hip_atomic_store(mirror + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
