@@ -222,3 +222,17 @@ def test_kernel_timer_brackets(dev):
     for k, v in ms.items():
         assert len(v) == 3 and all(0.0 < x < 1e3 for x in v), (k, v)
     assert RH._lib.load().splat_time_next_launch(None, None) == 0
+
+
+@pytest.mark.parametrize("TILE,cutoff", [(4, 3.0), (16, 3.0), (8, 2.0), (8, 4.5)])
+@pytest.mark.parametrize("odds", [False, True])
+def test_cull_entry_point_tiles_and_cutoffs(dev, TILE, cutoff, odds):
+    """The culled entry point at the other tile sizes and cull radii the reference's probes use
+    (render_triton.py:1037, :1170), through autograd, on a ragged canvas."""
+    H, W = 50, 38
+    scene = random_scene(400, H, W, seed=90 + TILE, dev=dev, op_max=0.95, margin=0.1)
+    gout = gout_for(H, W, dev, 9)
+    out, g = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=True, TILE=TILE, cutoff=cutoff,
+                        odds=odds)
+    ref, rg = oracle_run("cull", scene, gout, H, W, TILE=TILE, cutoff=cutoff, odds=odds)
+    compare(out, g, ref, rg)
