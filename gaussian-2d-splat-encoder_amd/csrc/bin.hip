@@ -85,8 +85,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
   __shared__ float4 s_rec[kBlock * 4];   // the block's records, written out coalesced
   const int g = blockIdx.x * kBlock + threadIdx.x;
   const int nrows = L.rbase[L.n];
-  // float4 k of splat t of the block sits at s_rec[4 t + (k ^ (t & 3))] (the xor spreads a wave's writes)
-  auto rec_slot = [](int t, int k) { return 4 * t + (k ^ (t & 3)); };
+  // float4 k of splat t of the block sits at s_rec[4 t + (k ^ ((t >> 2) & 3))]: 16 consecutive lanes then write
+  // 16 different 16-byte bank groups (slot mod 16) and read back 16 consecutive slots
+  auto rec_slot = [](int t, int k) { return 4 * t + (k ^ ((t >> 2) & 3)); };
   if (do_bin) {
     for (int i = threadIdx.x; i < kMaxLevels; i += kBlock) s_lev[i] = 0;
     if (rowhist)
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
       }
     __syncthreads();
   }
-  int cnt = 0;
+  int cnt = 0, lev = 0;
   bool bad = false;
   if (g < N) {
     const float2 m = reinterpret_cast<const float2*>(mu)[g];      // (y, x)
@@ -118,7 +119,6 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     s_rec[rec_slot(t, 3)] = make_float4(s.x, s.y, cs, sn);
     if (do_bin) {
       // level: render_triton.py:925-932 + 950-952 (octave), :904-913 (coarse/fine split)
-      int lev = 0;
       if (R.mode == 1) {
         const float px = fmaxf(s.x, s.y) * R.rep;
         const float o = ceilf(log2f(fmaxf(px * R.inv_base, 1e-6f)));
@@ -145,7 +145,6 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
       rect[g] = make_int4(tx0, ty0, w, lev);   // the rect height is not needed past this point
       counts[g] = cnt;
       if (cnt) {
-        atomicAdd(&s_lev[lev], cnt);
         if (rowhist) {   // rows [r0, r0 + h) each get one unit of w pairs
           const int r0 = L.rbase[lev] + ty0;
           atomicAdd(&s_du[r0], 1);
@@ -154,6 +153,16 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
           atomicAdd(&s_dp[r0 + h], -w);
         }
       }
+    }
+  }
+  if (do_bin) {   // per-level pair sums: one LDS atomic per level present in the wave (lanes of a level summed)
+    const int lane = threadIdx.x & 63;
+    for (unsigned long long rem = __ballot(cnt != 0); rem;) {
+      const int l0 = __shfl(lev, __ffsll((long long)rem) - 1, 64);
+      const unsigned long long m = __ballot(cnt != 0 && lev == l0);
+      const int sum = wave_sum_i(((m >> lane) & 1ull) ? cnt : 0);
+      if (lane == 0) atomicAdd(&s_lev[l0], sum);
+      rem &= ~m;
     }
   }
   __syncthreads();
