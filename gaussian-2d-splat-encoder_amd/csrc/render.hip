@@ -1397,8 +1397,8 @@ __device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo,
 }
 
 // Pass 1: workgroup = level-0 row y; tmp[k][y][j] = sum_x wx(x -> ix) dS_0[k][y, x] for the coarse column slots
-// j = cbase(l) + ix of every masked level l. STAGED: the row's 2 + C planes are first copied into LDS (coalesced;
-// rows of up to kAdjStageMax floats over all planes), so the window loops read LDS. The window of a texel of level l
+// j = cbase(l) + ix of every masked level l. Staged modes: the row's 2 + C planes are first copied into LDS (coalesced
+// loads; rows whose padded planes fit in kAdjStageMax floats), so the window loops read LDS. The window of a texel of level l
 // spans about 2^(l+1) destinations (131 at the coarsest octave of a 2048-wide canvas) while the level has W0 / 2^l
 // texels, so every level is about 2 W0 window steps: the levels are taken one after another by the whole
 // workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at most 64), lane
@@ -1406,28 +1406,83 @@ __device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo,
 // fixed xor tree (deterministic).
 constexpr int kAdjStageMax = 16384;   // floats of LDS per workgroup (64 KiB)
 
-template <int C, bool STAGED>
+// Where the window loops read the row. kAdjGlobal: from global memory (rows too wide for LDS). kAdjSource: the
+// row staged in LDS as it lies in memory, [S_log W0][S_a W0][S_ac W0 x C]. kAdjRotated: plane p (0: S_log, 1: S_a,
+// 2 + c: S_ac[c], de-interleaved) at s_row[p * adj_plane(W0) + adj_slot(x)], each 64-word row r = x / 64 of a
+// plane rotated by 9 r words, so the lanes of a wave that read destinations 2^l apart (a texel each, or a few
+// lanes per texel) mostly fall on different banks: 1.8 lanes per bank on average over the levels of 384- to
+// 2048-wide rows, against 3.5 to 5.1 unrotated (a simulation of this kernel's reads). The rotated layout costs an
+// LDS read per colour channel instead of one per two or three, which pays on wide rows only (measured: 2048
+// wide, 114 -> 81 us per launch; 768 wide, 11.5 -> 13.2 us), so rows from kAdjRotateMin pixels take it.
+enum AdjMode { kAdjGlobal = 0, kAdjSource = 1, kAdjRotated = 2 };
+constexpr int kAdjRotateMin = 1024;
+__device__ __forceinline__ int adj_slot(int x) { return (x & ~63) | ((x + 9 * (x >> 6)) & 63); }
+__host__ __device__ constexpr int adj_plane(int W0) { return (W0 + 63) & ~63; }
+
+template <int C, int MODE>
 __global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const float* __restrict__ dslog,
                                                   const float* __restrict__ dsa, const float* __restrict__ dsac,
                                                   float* __restrict__ tmp) {
-  extern __shared__ float s_row[];   // STAGED: [S_log W0][S_a W0][S_ac W0 x C]
+  extern __shared__ float s_row[];   // kAdjSource: (2 + C) W0 floats; kAdjRotated: 2 + C planes of adj_plane(W0)
   const int y = blockIdx.x, H0 = L.H[0], W0 = L.W[0];
+  const int P = adj_plane(W0);
   const size_t plane = (size_t)H0 * ncols;
   const int t = threadIdx.x;
   const float* rl = dslog + (size_t)y * W0;
   const float* ra = dsa + (size_t)y * W0;
   const float* rc = dsac + (size_t)y * W0 * C;
-  if (STAGED) {
-    for (int i = t; i < W0; i += 256) {
-      s_row[i] = rl[i];
-      s_row[W0 + i] = ra[i];
+  if (MODE != kAdjGlobal) {   // the row's (2 + C) W0 floats in source order, 16 loads per thread in flight
+    constexpr int kU = 16;
+    const int n = (2 + C) * W0;
+    for (int i0 = t; i0 < n; i0 += 256 * kU) {
+      float v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int k = i0 + u * 256;
+        v[u] = k < W0 ? rl[k] : k < 2 * W0 ? ra[k - W0] : k < n ? rc[k - 2 * W0] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int k = i0 + u * 256;
+        if (k >= n) continue;
+        if (MODE == kAdjSource) {
+          s_row[k] = v[u];
+          continue;
+        }
+        int pl, x;
+        if (k < 2 * W0) {
+          pl = k < W0 ? 0 : 1;
+          x = k - pl * W0;
+        } else {
+          const int j = k - 2 * W0;
+          x = j / C;
+          pl = 2 + (j - x * C);
+        }
+        s_row[pl * P + adj_slot(x)] = v[u];
+      }
     }
-    for (int i = t; i < W0 * C; i += 256) s_row[2 * W0 + i] = rc[i];
     __syncthreads();
-    rl = s_row;
-    ra = s_row + W0;
-    rc = s_row + 2 * W0;
   }
+  // the 2 + C values of destination x
+  auto fetch = [&](int x, float& vl, float& va, float* vc) {
+    if (MODE == kAdjSource) {
+      vl = s_row[x];
+      va = s_row[W0 + x];
+#pragma unroll
+      for (int c = 0; c < C; ++c) vc[c] = s_row[2 * W0 + x * C + c];
+    } else if (MODE == kAdjRotated) {
+      const int sl = adj_slot(x);
+      vl = s_row[sl];
+      va = s_row[P + sl];
+#pragma unroll
+      for (int c = 0; c < C; ++c) vc[c] = s_row[(2 + c) * P + sl];
+    } else {
+      vl = rl[x];
+      va = ra[x];
+#pragma unroll
+      for (int c = 0; c < C; ++c) vc[c] = rc[(size_t)x * C + c];
+    }
+  };
   int cb = 0;
   for (int l = 1; l < L.n; cb += L.W[l], ++l) {
     if (!((L.mask >> l) & 1)) continue;
@@ -1442,12 +1497,31 @@ __global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const
       if (ix < Wl) {
         int x0, x1;
         ups_window(ix, W0, sx, &x0, &x1);
-        for (int x = x0 + sub; x <= x1; x += tpc) {
-          const float w = ups_weight(x, ix, Wl, sx);
-          al += w * rl[x];
-          aa += w * ra[x];
+        int x = x0 + sub;
+        // four destinations per step, their loads issued before any is added (the additions keep the order of x)
+        for (; x + 3 * tpc <= x1; x += 4 * tpc) {
+          float w[4], vl[4], va[4], vc[4][kMaxC];
 #pragma unroll
-          for (int c = 0; c < C; ++c) ac[c] += w * rc[(size_t)x * C + c];
+          for (int u = 0; u < 4; ++u) {
+            w[u] = ups_weight(x + u * tpc, ix, Wl, sx);
+            fetch(x + u * tpc, vl[u], va[u], vc[u]);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            al += w[u] * vl[u];
+            aa += w[u] * va[u];
+#pragma unroll
+            for (int c = 0; c < C; ++c) ac[c] += w[u] * vc[u][c];
+          }
+        }
+        for (; x <= x1; x += tpc) {
+          const float w = ups_weight(x, ix, Wl, sx);
+          float vl, va, vc[kMaxC];
+          fetch(x, vl, va, vc);
+          al += w * vl;
+          aa += w * va;
+#pragma unroll
+          for (int c = 0; c < C; ++c) ac[c] += w * vc[c];
         }
       }
       for (int d = 1; d < tpc; d <<= 1) {
@@ -1487,7 +1561,29 @@ __global__ __launch_bounds__(256) void k_adj_rows(LevelTable L, int ncols, const
   int y0, y1;
   ups_window(iy, H0, sy, &y0, &y1);
   float al = 0.f, aa = 0.f, ac[kMaxC] = {0.f, 0.f, 0.f, 0.f};
-  for (int y = y0; y <= y1; ++y) {
+  int y = y0;
+  // four source rows per step, their loads issued before any is added (rows of weight 0 add nothing, as below)
+  for (; y + 3 <= y1; y += 4) {
+    float w[4], vl[4], va[4], vc[4][kMaxC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      w[u] = ups_weight(y + u, iy, Hl, sy);
+      const size_t o = (size_t)(y + u) * ncols + cb + ix;
+      vl[u] = tmp[o];
+      va[u] = tmp[plane + o];
+#pragma unroll
+      for (int c = 0; c < C; ++c) vc[u][c] = tmp[(2 + c) * plane + o];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (w[u] == 0.f) continue;
+      al += w[u] * vl[u];
+      aa += w[u] * va[u];
+#pragma unroll
+      for (int c = 0; c < C; ++c) ac[c] += w[u] * vc[u][c];
+    }
+  }
+  for (; y <= y1; ++y) {
     const float w = ups_weight(y, iy, Hl, sy);
     if (w == 0.f) continue;
     const size_t o = (size_t)y * ncols + cb + ix;
@@ -1819,11 +1915,15 @@ int splat_upsample_adjoint(int C, int H, int W, int TILE, const splat_levels* lv
   float* tmp = (float*)ws;
   return with_c(C, [&](auto cc) {
     constexpr int CC = decltype(cc)::value;
-    const size_t stage = sizeof(float) * (size_t)(2 + CC) * (size_t)L.W[0];
-    if (stage <= sizeof(float) * kAdjStageMax)
-      k_adj_cols<CC, true><<<L.H[0], 256, stage, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+    const int W0 = L.W[0];
+    const size_t src = sizeof(float) * (size_t)(2 + CC) * (size_t)W0;
+    const size_t rot = sizeof(float) * (size_t)(2 + CC) * (size_t)adj_plane(W0);
+    if (W0 >= kAdjRotateMin && rot <= sizeof(float) * kAdjStageMax)
+      k_adj_cols<CC, kAdjRotated><<<L.H[0], 256, rot, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+    else if (src <= sizeof(float) * kAdjStageMax)
+      k_adj_cols<CC, kAdjSource><<<L.H[0], 256, src, st>>>(L, ncols, dslog, dsa, dsac, tmp);
     else
-      k_adj_cols<CC, false><<<L.H[0], 256, 0, st>>>(L, ncols, dslog, dsa, dsac, tmp);
+      k_adj_cols<CC, kAdjGlobal><<<L.H[0], 256, 0, st>>>(L, ncols, dslog, dsa, dsac, tmp);
     k_adj_rows<CC><<<(ncoarse + 255) / 256, 256, 0, st>>>(L, ncols, tmp, dslog, dsa, dsac);
     return check_launch("splat_upsample_adjoint");
   });
