@@ -1498,12 +1498,24 @@ __global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const
         int x0, x1;
         ups_window(ix, W0, sx, &x0, &x1);
         int x = x0 + sub;
+        // The weight of texel ix for destination x at source position r = max(sx (x + 0.5) - 0.5, 0) (x + 0.5
+        // carried as a float: exact): max(0, 1 - |r - ix|), what ups_weight gives (1 - (r - i) on texel
+        // i = floor(r), r - i on texel i + 1), except that the last texel also takes its missing right
+        // neighbour's share, (1 - d) + d for d = r - ix > 0.
+        const float fix = (float)ix;
+        const bool last = ix == Wl - 1;
+        float xf = (float)x + 0.5f;
+        auto weight = [&](float xh) {
+          const float d = fmaxf(fmaf(sx, xh, -0.5f), 0.f) - fix;
+          return (last && d > 0.f) ? (1.f - d) + d : fmaxf(1.f - fabsf(d), 0.f);
+        };
+        const float step = (float)tpc;
         // four destinations per step, their loads issued before any is added (the additions keep the order of x)
-        for (; x + 3 * tpc <= x1; x += 4 * tpc) {
+        for (; x + 3 * tpc <= x1; x += 4 * tpc, xf += 4.f * step) {
           float w[4], vl[4], va[4], vc[4][kMaxC];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            w[u] = ups_weight(x + u * tpc, ix, Wl, sx);
+            w[u] = weight(xf + (float)u * step);
             fetch(x + u * tpc, vl[u], va[u], vc[u]);
           }
 #pragma unroll
@@ -1514,8 +1526,8 @@ __global__ __launch_bounds__(256) void k_adj_cols(LevelTable L, int ncols, const
             for (int c = 0; c < C; ++c) ac[c] += w[u] * vc[u][c];
           }
         }
-        for (; x <= x1; x += tpc) {
-          const float w = ups_weight(x, ix, Wl, sx);
+        for (; x <= x1; x += tpc, xf += step) {
+          const float w = weight(xf);
           float vl, va, vc[kMaxC];
           fetch(x, vl, va, vc);
           al += w * vl;
