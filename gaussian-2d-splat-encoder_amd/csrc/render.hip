@@ -1581,10 +1581,15 @@ __global__ __launch_bounds__(256) void k_adj_rows(LevelTable L, int ncols, const
     for (int u = 0; u < 4; ++u) {
       w[u] = ups_weight(y + u, iy, Hl, sy);
       const size_t o = (size_t)(y + u) * ncols + cb + ix;
-      vl[u] = tmp[o];
-      va[u] = tmp[plane + o];
+      vl[u] = va[u] = 0.f;
 #pragma unroll
-      for (int c = 0; c < C; ++c) vc[u][c] = tmp[(2 + c) * plane + o];
+      for (int c = 0; c < C; ++c) vc[u][c] = 0.f;
+      if (w[u] != 0.f) {   // rows of the widened window outside the texel's support are not fetched
+        vl[u] = tmp[o];
+        va[u] = tmp[plane + o];
+#pragma unroll
+        for (int c = 0; c < C; ++c) vc[u][c] = tmp[(2 + c) * plane + o];
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
