@@ -1397,11 +1397,11 @@ __device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo,
 }
 
 // Pass 1: workgroup = level-0 row y; tmp[k][y][j] = sum_x wx(x -> ix) dS_0[k][y, x] for the coarse column slots
-// j = cbase(l) + ix of every masked level l. Staged modes: the row's 2 + C planes are first copied into LDS (coalesced
-// loads; rows whose padded planes fit in kAdjStageMax floats), so the window loops read LDS. The window of a texel of level l
-// spans about 2^(l+1) destinations (131 at the coarsest octave of a 2048-wide canvas) while the level has W0 / 2^l
-// texels, so every level is about 2 W0 window steps: the levels are taken one after another by the whole
-// workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at most 64), lane
+// j = cbase(l) + ix of every masked level l. Staged modes: the row's 2 + C planes are first copied into LDS
+// (coalesced loads; rows whose planes fit in kAdjStageMax floats), so the window loops read LDS. The window of a
+// texel of level l spans about 2^(l+1) destinations (131 at the coarsest octave of a 2048-wide canvas) while the
+// level has W0 / 2^l texels, so every level is about 2 W0 window steps: the levels are taken one after another by
+// the whole workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at most 64), lane
 // s summing the destinations x0 + s, x0 + s + tpc, ... of the texel's window; the tpc partial sums are added by a
 // fixed xor tree (deterministic).
 constexpr int kAdjStageMax = 16384;   // floats of LDS per workgroup (64 KiB)
@@ -1412,8 +1412,9 @@ constexpr int kAdjStageMax = 16384;   // floats of LDS per workgroup (64 KiB)
 // plane rotated by 9 r words, so the lanes of a wave that read destinations 2^l apart (a texel each, or a few
 // lanes per texel) mostly fall on different banks: 1.8 lanes per bank on average over the levels of 384- to
 // 2048-wide rows, against 3.5 to 5.1 unrotated (a simulation of this kernel's reads). The rotated layout costs an
-// LDS read per colour channel instead of one per two or three, which pays on wide rows only (measured: 2048
-// wide, 114 -> 81 us per launch; 768 wide, 11.5 -> 13.2 us), so rows from kAdjRotateMin pixels take it.
+// LDS read per colour channel instead of one per two or three, which pays on wide rows only (measured against the
+// source layout with the same loops: 2048 wide, 98 -> 81 us per launch; 768 wide, about 10.8 -> 13.2 us), so rows
+// from kAdjRotateMin pixels take it.
 enum AdjMode { kAdjGlobal = 0, kAdjSource = 1, kAdjRotated = 2 };
 constexpr int kAdjRotateMin = 1024;
 __device__ __forceinline__ int adj_slot(int x) { return (x & ~63) | ((x + 9 * (x >> 6)) & 63); }
