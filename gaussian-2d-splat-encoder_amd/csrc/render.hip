@@ -1401,9 +1401,9 @@ __device__ __forceinline__ void ups_window(int i, int out, float scale, int* lo,
 // (coalesced loads; rows whose planes fit in kAdjStageMax floats), so the window loops read LDS. The window of a
 // texel of level l spans about 2^(l+1) destinations (131 at the coarsest octave of a 2048-wide canvas) while the
 // level has W0 / 2^l texels, so every level is about 2 W0 window steps: the levels are taken one after another by
-// the whole workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at most 64), lane
-// s summing the destinations x0 + s, x0 + s + tpc, ... of the texel's window; the tpc partial sums are added by a
-// fixed xor tree (deterministic).
+// the whole workgroup, and a level narrower than the workgroup gives each texel tpc lanes (a power of two, at
+// most 64), lane s summing the destinations x0 + s, x0 + s + tpc, ... of the texel's window; the tpc partial sums
+// are added by a fixed xor tree (deterministic).
 constexpr int kAdjStageMax = 16384;   // floats of LDS per workgroup (64 KiB)
 
 // Where the window loops read the row. kAdjGlobal: from global memory (rows too wide for LDS). kAdjSource: the
