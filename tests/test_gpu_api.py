@@ -236,3 +236,46 @@ def test_cull_entry_point_tiles_and_cutoffs(dev, TILE, cutoff, odds):
                         odds=odds)
     ref, rg = oracle_run("cull", scene, gout, H, W, TILE=TILE, cutoff=cutoff, odds=odds)
     compare(out, g, ref, rg)
+
+
+def octave_scene(n, seed, dev):
+    """Splats whose sizes span several octaves (log-uniform sigma 0.006-0.31 of the image), as in
+    test_octave_multi_level."""
+    g = torch.Generator().manual_seed(seed)
+    sig = torch.exp(torch.rand(1, n, generator=g) * (np.log(0.31) - np.log(0.006)) + np.log(0.006))
+    ls = torch.log(torch.exp(sig).clamp_min(1 + 1e-6) - 1.0).unsqueeze(-1).expand(1, n, 2).contiguous()
+    mu = torch.rand(1, n, 2, generator=g)
+    col = torch.rand(1, n, 3, generator=g)
+    op = torch.rand(1, n, generator=g) * 0.4
+    th = torch.rand(1, n, generator=g) * 3.14159
+    bg = torch.rand(1, 3, generator=g)
+    return [t.to(dev) for t in (mu, ls, col, op, bg, th)]
+
+
+@pytest.mark.parametrize("TILE,base,mo", [(4, 8.0, 6), (16, 8.0, 6), (8, 4.0, 3), (8, 16.0, 2)])
+def test_octave_entry_point_options(dev, TILE, base, mo):
+    """render_alpha_octave's TILE, base_texels and max_octaves (render_triton.py:935-980) through autograd on a
+    ragged canvas, against the oracle's octave glue with the same options (routing and per-level binning)."""
+    H, W = 96, 80
+    scene = octave_scene(300, 70 + TILE + mo, dev)
+    gout = gout_for(H, W, dev, 7)
+    kw = dict(TILE=TILE, base_texels=base, max_octaves=mo, odds=True)
+    out, gd = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, **kw)
+    ref, rg = oracle_run("octave", scene, gout, H, W, **kw)
+    compare(out, gd, ref, rg)
+
+
+@pytest.mark.parametrize("TILE,cf", [(4, 4), (16, 8), (8, 2)])
+def test_multires_entry_point_options(dev, TILE, cf):
+    """render_alpha_multires's TILE and coarse_factor (render_triton.py:879-922) through autograd, against the
+    oracle's coarse/fine glue with the same options."""
+    H, W = 96, 80
+    scene = list(random_scene(400, H, W, seed=80 + TILE + cf, dev=dev))
+    ls = scene[1].clone()
+    ls[:, :80] = float(np.log(np.exp(0.1) - 1.0))
+    scene[1] = ls
+    gout = gout_for(H, W, dev, 8)
+    kw = dict(n_coarse=80, coarse_factor=cf, TILE=TILE, odds=True)
+    out, gd = device_run(RH.render_alpha_multires, scene, gout, H=H, W=W, **kw)
+    ref, rg = oracle_run("multires", scene, gout, H, W, **kw)
+    compare(out, gd, ref, rg)
