@@ -158,17 +158,28 @@ def test_errors(dev):
         RH.render_alpha_full_triton(*scene[:5], 32, 32, theta=scene[5], cull=True, TILE=5)
 
 
-def test_batch_of_three(dev):
+BATCH_ENTRIES = {
+    "cull": (lambda *a, **k: RH.render_alpha_full_triton(*a, cull=True, **k), {}),
+    "octave": (RH.render_alpha_octave, {}),
+    "multires": (RH.render_alpha_multires, {"n_coarse": 60, "coarse_factor": 4}),
+}
+
+
+@pytest.mark.parametrize("entry", ["cull", "octave", "multires"])
+def test_batch_of_three(dev, entry):
+    """B = 3 through each entry point: every batch element's image and gradients (background included) equal
+    those of the element rendered alone."""
     H = W = 40
+    fn, kw = BATCH_ENTRIES[entry]
     scene = random_scene(300, H, W, seed=31, dev=dev, B=3)
     g = torch.Generator().manual_seed(8)
     gout = torch.randn(3, 3, H, W, generator=g).to(dev)
-    out, gd = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, odds=True)
+    out, gd = device_run(fn, scene, gout, H=H, W=W, odds=True, **kw)
     for b in range(3):
         one = [None if t is None else t[b:b + 1] for t in scene]
-        o1, g1 = device_run(RH.render_alpha_octave, one, gout[b:b + 1], H=H, W=W, odds=True)
+        o1, g1 = device_run(fn, one, gout[b:b + 1], H=H, W=W, odds=True, **kw)
         assert (o1[0] - out[b]).abs().max().item() <= 1e-6
-        for n in ["mu", "ls", "col", "op", "th"]:
+        for n in ["mu", "ls", "col", "op", "bg", "th"]:
             assert rel_err(np_(g1[n][0]), np_(gd[n][b])) <= 1e-5, n
 
 
