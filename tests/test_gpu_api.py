@@ -290,3 +290,44 @@ def test_multires_entry_point_options(dev, TILE, cf):
     out, gd = device_run(RH.render_alpha_multires, scene, gout, H=H, W=W, **kw)
     ref, rg = oracle_run("multires", scene, gout, H, W, **kw)
     compare(out, gd, ref, rg)
+
+
+@pytest.mark.parametrize("entry", ["cull", "octave"])
+def test_noncontiguous_parameters(dev, entry):
+    """Parameters passed as strided views (transposed, every other element) give the image and gradients of the
+    same values passed contiguous, bit for bit; each base tensor's gradient is the view's gradient in the viewed
+    elements and zero elsewhere."""
+    H = W = 48
+    fn, kw = BATCH_ENTRIES[entry]
+    mu, ls, col, op, bg, th = random_scene(400, H, W, seed=33, dev=dev)
+    N = mu.shape[1]
+    z = lambda t: torch.zeros_like(t)
+    bases = {
+        "mu": mu.transpose(1, 2).contiguous(),                              # [1, 2, N]
+        "ls": torch.stack([ls, z(ls)], -1).reshape(1, N, 4).contiguous(),    # values at [..., ::2]
+        "col": col.transpose(1, 2).contiguous(),                            # [1, 3, N]
+        "op": torch.stack([op, z(op)], -1).reshape(1, 2 * N).contiguous(),  # values at [:, ::2]
+        "bg": torch.stack([bg, z(bg)], -1).reshape(1, 6).contiguous(),      # values at [:, ::2]
+        "th": torch.stack([th, z(th)], -1).contiguous(),                    # values at [..., 0]
+    }
+    views = {
+        "mu": lambda b: b.transpose(1, 2), "ls": lambda b: b[..., ::2], "col": lambda b: b.transpose(1, 2),
+        "op": lambda b: b[:, ::2], "bg": lambda b: b[:, ::2], "th": lambda b: b[..., 0],
+    }
+    names = ["mu", "ls", "col", "op", "bg", "th"]
+    leaves = {n: bases[n].clone().requires_grad_(True) for n in names}
+    args = [views[n](leaves[n]) for n in names]
+    assert not any(a.is_contiguous() for a in args[:4])
+    gout = gout_for(H, W, dev, 9)
+    out = fn(*args[:5], H, W, theta=args[5], odds=True, **kw)
+    (out * gout).sum().backward()
+    ref = [views[n](bases[n]).contiguous().requires_grad_(True) for n in names]
+    out_c = fn(*ref[:5], H, W, theta=ref[5], odds=True, **kw)
+    (out_c * gout).sum().backward()
+    assert torch.equal(out, out_c)
+    for n, r in zip(names, ref):
+        g = leaves[n].grad
+        assert torch.equal(views[n](g), r.grad), n
+        rest = g.clone()
+        views[n](rest).zero_()
+        assert not rest.any(), f"{n}: gradient outside the viewed elements"
