@@ -331,3 +331,28 @@ def test_noncontiguous_parameters(dev, entry):
         rest = g.clone()
         views[n](rest).zero_()
         assert not rest.any(), f"{n}: gradient outside the viewed elements"
+
+
+@pytest.mark.parametrize("entry", ["cull", "octave", "multires"])
+def test_grad_modes(dev, entry):
+    """The image does not depend on whether autograd records the render (no_grad, inference_mode: the binning
+    then builds no backward maps), and a render where only the colours and opacities need gradients returns
+    exactly those gradients of the full backward, the others None."""
+    H = W = 40
+    fn, kw = BATCH_ENTRIES[entry]
+    scene = random_scene(300, H, W, seed=41, dev=dev)
+    gout = gout_for(H, W, dev, 10)
+    out, gd = device_run(fn, scene, gout, H=H, W=W, odds=True, **kw)
+    with torch.no_grad():
+        o_ng = fn(*scene[:5], H, W, theta=scene[5], odds=True, **kw)
+    with torch.inference_mode():
+        o_im = fn(*scene[:5], H, W, theta=scene[5], odds=True, **kw)
+    assert torch.equal(o_ng, out) and torch.equal(o_im, out)
+    L = [t.detach().clone() for t in scene]
+    L[2].requires_grad_(True)
+    L[3].requires_grad_(True)
+    o_p = fn(*L[:5], H, W, theta=L[5], odds=True, **kw)
+    (o_p * gout).sum().backward()
+    assert torch.equal(o_p.detach(), out)
+    assert torch.equal(L[2].grad, gd["col"]) and torch.equal(L[3].grad, gd["op"])
+    assert all(L[i].grad is None for i in (0, 1, 4, 5))
