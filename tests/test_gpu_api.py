@@ -356,3 +356,43 @@ def test_grad_modes(dev, entry):
     assert torch.equal(o_p.detach(), out)
     assert torch.equal(L[2].grad, gd["col"]) and torch.equal(L[3].grad, gd["op"])
     assert all(L[i].grad is None for i in (0, 1, 4, 5))
+
+
+@pytest.mark.parametrize("entry", ["cull", "octave"])
+def test_threads_on_own_streams(dev, entry):
+    """Two threads, each on a stream of its own (default priority), rendering and differentiating different scenes
+    at the same time five times over, get the images and gradients of the same renders run one after another (the
+    count's landing buffer and the error state are per thread, the workspaces per call)."""
+    import threading
+    H = W = 48
+    fn, kw = BATCH_ENTRIES[entry]
+    scenes = [random_scene(300, H, W, seed=50 + i, dev=dev) for i in range(2)]
+    gouts = [gout_for(H, W, dev, 20 + i) for i in range(2)]
+    seq = [device_run(fn, s, g, H=H, W=W, odds=True, **kw) for s, g in zip(scenes, gouts)]
+    results, errors = [[], []], []
+    main = torch.cuda.current_stream(dev)
+
+    def work(i):
+        try:
+            st = torch.cuda.Stream(device=dev)
+            st.wait_stream(main)
+            with torch.cuda.stream(st):
+                for _ in range(5):
+                    results[i].append(device_run(fn, scenes[i], gouts[i], H=H, W=W, odds=True, **kw))
+            st.synchronize()
+        except Exception as e:   # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "a render thread did not finish"
+    assert not errors, errors
+    for i in range(2):
+        assert len(results[i]) == 5
+        for out, g in results[i]:
+            assert torch.equal(out, seq[i][0])
+            for n in NAMES:
+                assert torch.equal(g[n], seq[i][1][n]), n
