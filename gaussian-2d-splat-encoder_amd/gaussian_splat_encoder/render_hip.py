@@ -1031,7 +1031,14 @@ def render_alpha_octave(mu, log_scale, color, opacity, bg, H, W, theta=None, cut
     number of tiles; octave fields are upsampled to (H, W), summed and composited once. Fused: the routing
     happens in the binning pass, every octave shares one pair list, and the level-0 composite kernel
     upsamples the coarse octaves' fields in its epilogue (octaves whose canvas is clamped to 8x8 share one
-    level, which sums the same fields)."""
+    level, which sums the same fields).
+
+    H and W must be at least 8: the reference renders octave 0 on a max(8, H) x max(8, W) canvas and adds it to
+    the H x W field (render_triton.py:958-962), a shape error as soon as a splat routes to octave 0 on a
+    smaller canvas; here such a canvas is refused up front (RuntimeError) whatever the routing."""
     B, N, C = color.shape
+    if H < 8 or W < 8:
+        raise RuntimeError(f"render_alpha_octave: H={H} W={W}; the octave render needs H, W >= 8 (its octave 0 "
+                           f"renders on a max(8, H) x max(8, W) canvas)")
     lv = _octave_levels(H, W, base_texels, max_octaves)
     return _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv)

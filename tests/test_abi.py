@@ -138,3 +138,18 @@ def test_deferred_read_needs_pair_buffers():
     for nlev, cap in ((0, 1), (_lib.MAX_LEVELS + 1, 1), (1, -1)):
         assert lib.splat_bin_finish(fake, fake, nlev, -1, cap, None) == 1
         assert b"splat_bin_finish" in lib.splat_last_error()
+
+
+@pytest.mark.parametrize("H,W", [(1, 1), (7, 64), (64, 3)])
+def test_octave_render_refuses_canvases_below_8(H, W):
+    """render_alpha_octave refuses a canvas under 8 pixels a side before any device work (the reference's octave 0
+    renders on a max(8, H) x max(8, W) canvas and fails adding it to the H x W field)."""
+    import torch
+    from gaussian_splat_encoder import render_hip as RH
+    n = 4
+    args = (torch.rand(1, n, 2), torch.zeros(1, n, 2), torch.rand(1, n, 3), torch.rand(1, n), torch.rand(1, 3))
+    with pytest.raises(RuntimeError, match="H, W >= 8"):
+        RH.render_alpha_octave(*args, H, W)
+    # the level table itself is refused by the library too
+    lv = _lib.SplatLevels(1, 6, 8.0, 0, 0, 0)
+    assert _lib.load().splat_levels_geometry(H, W, 8, ctypes.byref(lv), None, 0) < 0

@@ -396,3 +396,26 @@ def test_threads_on_own_streams(dev, entry):
             assert torch.equal(out, seq[i][0])
             for n in NAMES:
                 assert torch.equal(g[n], seq[i][1][n]), n
+
+
+@pytest.mark.parametrize("H,W", [(1, 1), (3, 200), (200, 3), (7, 9)])
+def test_tiny_and_thin_canvases(dev, H, W):
+    """Canvases of a single pixel, a few pixel rows or columns, and less than a tile: the culled and the
+    coarse/fine renders over partial tiles against the oracle. The octave render refuses them with a RuntimeError, as the reference's
+    fails with one (its octave 0 renders on a max(8, H) x max(8, W) canvas that it adds to the H x W field,
+    render_triton.py:958-962; the oracle's restatement fails the same way)."""
+    scene = random_scene(150, H, W, seed=H * 1000 + W, dev=dev, ls_mean_px=3.0, margin=0.2)
+    gout = gout_for(H, W, dev, 11)
+    out, gd = device_run(RH.render_alpha_full_triton, scene, gout, H=H, W=W, cull=True, odds=True)
+    assert out.shape == (1, 3, H, W)
+    ref, rg = oracle_run("cull", scene, gout, H, W, odds=True)
+    compare(out, gd, ref, rg)
+    kw = dict(n_coarse=50, coarse_factor=8, odds=True)   # the coarse group at max(1, H // cf), cf from min(H, W)
+    out, gd = device_run(RH.render_alpha_multires, scene, gout, H=H, W=W, **kw)
+    ref, rg = oracle_run("multires", scene, gout, H, W, **kw)
+    compare(out, gd, ref, rg)
+    with pytest.raises(RuntimeError, match="H, W >= 8"):
+        RH.render_alpha_octave(*scene[:5], H, W, theta=scene[5], odds=True)
+    if min(H, W) > 1:   # a splat at octave 0 (the whole scene routed there with a large base)
+        with pytest.raises(RuntimeError):
+            oracle_run("octave", scene, gout, H, W, odds=True, base_texels=1e6)
