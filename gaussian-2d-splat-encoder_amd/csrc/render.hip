@@ -1180,9 +1180,12 @@ __device__ __forceinline__ void zero_grads(int g, float* __restrict__ g_mu, floa
 // xor tree), so one heavy splat does not serialise its wave. The order of every addition is fixed:
 // deterministic. Splats with no pair (none for valid rects) get zeros. With g_bg set, the grid's first
 // workgroup sums the per-tile background partials instead.
-constexpr int kSumLanes = 4;
+// Measured at C2 (about 20 records per splat) and C4: 8 lanes per splat 17.2 us and 261 us per launch, against 18.1
+// and 265 with 4 lanes, 20.9 and 278 with 2, 19.9 and 270 with 16; with 8 lanes, 2 loads in flight instead of 4
+// 18.1 and 284 us.
+constexpr int kSumLanes = 8;
 constexpr int kLightPairs = 64;
-constexpr int kSumUnroll = 4;   // 4 measured 2% faster than 8 at C2 (about 20 records per splat, 4 lanes)
+constexpr int kSumUnroll = 4;
 
 // s += records q, q + step, ... below qe, in that order. The records of kSumUnroll steps are loaded before
 // any is added (clamped to the last valid one), so each lane keeps kSumUnroll loads in flight.
