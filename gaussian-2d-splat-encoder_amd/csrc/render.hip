@@ -1182,9 +1182,10 @@ __device__ __forceinline__ void zero_grads(int g, float* __restrict__ g_mu, floa
 // workgroup sums the per-tile background partials instead.
 // Measured at C2 (about 20 records per splat) and C4: 8 lanes per splat 17.2 us and 261 us per launch, against 18.1
 // and 265 with 4 lanes, 20.9 and 278 with 2, 19.9 and 270 with 16; with 8 lanes, 2 loads in flight instead of 4
-// 18.1 and 284 us.
+// 18.1 and 284 us. Splats of more than 128 pairs go to the whole-wave path: 16.3 us at C2 against 17.2 with 64
+// and 256 (C4 unchanged, 262 us).
 constexpr int kSumLanes = 8;
-constexpr int kLightPairs = 64;
+constexpr int kLightPairs = 128;
 constexpr int kSumUnroll = 4;
 
 // s += records q, q + step, ... below qe, in that order. The records of kSumUnroll steps are loaded before
