@@ -1,4 +1,4 @@
-"""The reference's own self-tests of the render (render_triton.py:983-1042, :1256-1298, :1370-1402) on the device
+"""The reference's own self-tests of the render (render_triton.py:983-1042, :1256-1298, :1370-1428) on the device
 path, with their shapes and tolerances. Their inputs came from the CUDA RNG and cannot be regenerated, so the
 scenes are drawn here from seeded CPU generators with the same distributions:
 * the culled render converges to the exact one as the cutoff grows (forward within 5e-3 at some cutoff of 3, 4, 5
@@ -6,6 +6,8 @@ scenes are drawn here from seeded CPU generators with the same distributions:
 * the coarse/fine and octave renders approximate the exact full-resolution render (mean relative difference
   below 0.03), and their backward agrees with a central finite difference of the loss in one splat's position
   (relative 5e-2): a coarse splat for the split, the largest splat (deepest octave) for the octave render.
+* the octave render at 1024, 1536 and 2048 pixels a side with 4 (H/8)^2 splats stays within the pair budget
+  (render_triton.py:1405-1428), its pair total within 36 N.
 The finite differences sum the loss in float64 so that only the float32 render's own rounding enters them."""
 
 import math
@@ -127,3 +129,30 @@ def test_octave_split_approximates_exact(dev):
     mm[0, j, 0] -= eps
     fd = (loss64(oc(mp), g) - loss64(oc(mm), g)) / (2 * eps)
     assert abs(ana - fd) / (abs(fd) + 1e-6) < 5e-2, (ana, fd)
+
+
+@pytest.mark.parametrize("H", [1024, 1536, 2048])
+def test_octave_probe_budget(dev, H):
+    """render_triton.py:1405-1428: at H x H with 4 (H/8)^2 splats, half large (sigma 0.20) and half small (sigma
+    0.018), the octave render's forward and backward stay within the 48M pair budget (no PairBudgetExceeded), its
+    pair total within the 36 N the routing bounds it by, and its image and gradients finite."""
+    W = H
+    grid = (H // 8) * (W // 8)
+    n = 4 * grid
+    g = torch.Generator().manual_seed(0)
+    mu = torch.rand(1, n, 2, generator=g).to(dev)
+    ls = torch.empty(1, n, 2, device=dev)
+    ls[:, :n // 2] = math.log(math.exp(0.20) - 1.0)
+    ls[:, n // 2:] = math.log(math.exp(0.018) - 1.0)
+    col = torch.rand(1, n, 3, generator=g).to(dev)
+    op = torch.rand(1, n, generator=g).to(dev)
+    bg = torch.rand(1, 3, generator=g).to(dev)
+    L = [t.clone().requires_grad_(True) for t in (mu, ls, col, op, bg)]
+    out = RH.render_alpha_octave(*L, H, W, max_pairs=48_000_000)
+    out.float().pow(2).mean().backward()
+    assert torch.isfinite(out).all()
+    assert all(torch.isfinite(t.grad).all() for t in L)
+    lv = RH._octave_levels(H, W, 8.0, 6)
+    _, _, bins = RH._forward_levels(mu, ls, col, op, bg, None, H, W, 8, 3.0, 48_000_000, False, lv,
+                                    with_maps=False, scale_is_log=True)
+    assert 0 < bins.tot_b[0] <= 36 * n, (bins.tot_b[0], 36 * n)
