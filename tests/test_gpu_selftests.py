@@ -1,4 +1,4 @@
-"""The reference's own self-tests of the render (render_triton.py:983-1042, :1256-1298, :1370-1428) on the device
+"""The reference's own self-tests of the render (render_triton.py:983-1042, :1256-1428) on the device
 path, with their shapes and tolerances. Their inputs came from the CUDA RNG and cannot be regenerated, so the
 scenes are drawn here from seeded CPU generators with the same distributions:
 * the culled render converges to the exact one as the cutoff grows (forward within 5e-3 at some cutoff of 3, 4, 5
@@ -7,7 +7,8 @@ scenes are drawn here from seeded CPU generators with the same distributions:
   below 0.03), and their backward agrees with a central finite difference of the loss in one splat's position
   (relative 5e-2): a coarse splat for the split, the largest splat (deepest octave) for the octave render.
 * the octave render at 1024, 1536 and 2048 pixels a side with 4 (H/8)^2 splats stays within the pair budget
-  (render_triton.py:1405-1428), its pair total within 36 N.
+  (render_triton.py:1405-1428), its pair total within 36 N; the coarse/fine render of the same kind of scene at
+  1024 pixels a side stays below 20 GB of device memory (render_triton.py:1301-1331).
 The finite differences sum the loss in float64 so that only the float32 render's own rounding enters them."""
 
 import math
@@ -156,3 +157,31 @@ def test_octave_probe_budget(dev, H):
     _, _, bins = RH._forward_levels(mu, ls, col, op, bg, None, H, W, 8, 3.0, 48_000_000, False, lv,
                                     with_maps=False, scale_is_log=True)
     assert 0 < bins.tot_b[0] <= 36 * n, (bins.tot_b[0], 36 * n)
+
+
+def test_multires_probe_memory(dev):
+    """render_triton.py:1301-1331: the coarse/fine render at 1024 x 1024 with 4 (H/8)^2 splats, the coarse half at
+    sigma 0.20 (the initial scale whose full-resolution binning would need about 400M pairs), forward and backward
+    with a peak of device memory below 20 GB (torch's allocator statistics), image and gradients finite."""
+    H = W = 1024
+    grid = (H // 8) * (W // 8)
+    nc = nf = 2 * grid
+    n = nc + nf
+    g = torch.Generator().manual_seed(0)
+    mu = torch.rand(1, n, 2, generator=g).to(dev)
+    ls = torch.empty(1, n, 2, device=dev)
+    ls[:, :nc] = math.log(math.exp(0.20) - 1.0)
+    ls[:, nc:] = math.log(math.exp(0.018) - 1.0)
+    col = torch.rand(1, n, 3, generator=g).to(dev)
+    op = torch.rand(1, n, generator=g).to(dev)
+    bg = torch.rand(1, 3, generator=g).to(dev)
+    L = [t.clone().requires_grad_(True) for t in (mu, ls, col, op, bg)]
+    torch.cuda.synchronize(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    out = RH.render_alpha_multires(*L, H, W, n_coarse=nc, coarse_factor=8)
+    out.float().pow(2).mean().backward()
+    torch.cuda.synchronize(dev)
+    peak = (torch.cuda.max_memory_allocated(dev) - base) / 1e9
+    assert peak < 20.0, peak
+    assert torch.isfinite(out).all() and all(torch.isfinite(t.grad).all() for t in L)
