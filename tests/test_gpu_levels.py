@@ -94,15 +94,17 @@ def test_split_bit_exact(dev):
     check_level_bins(mu, activate_scale(ls), H, W, 8, split_lv(H, W, 700))
 
 
+@pytest.mark.parametrize("C", [1, 2, 3, 4])
 @pytest.mark.parametrize("H,W", [(100, 60), (16, 1536), (8, 3584)])
-def test_upsample_adjoint_matches_torch(dev, H, W):
+def test_upsample_adjoint_matches_torch(dev, H, W, C):
     """dS_l = (d upsample_l / d field_l)^T dS_0 for every coarse level, against torch's bilinear backward. The
     widths take each way the column pass reads a level-0 row: staged in LDS as it lies in memory (60), staged as
     de-interleaved planes with rotated 64-word rows (1536, rows of 1024 pixels and more), and from global memory
-    (3584: five planes of 3584 floats exceed the 64 KiB of LDS a workgroup stages). The wide rows' level widths
+    (3584 with C >= 3: 2 + C planes of 3584 floats exceed the 64 KiB of LDS a workgroup stages; with C = 1 or
+    2 that width is staged rotated). The wide rows' level widths
     are the row's width over powers of two, so the float32 source positions of the kernels carry no rounding
-    that the float64 reference would not (at 1500 wide, 187 texels per row put them about 1e-7 x 1500 apart)."""
-    C = 3
+    that the float64 reference would not (at 1500 wide, 187 texels per row put them about 1e-7 x 1500 apart).
+    Colour channel counts 1 to 4 (the rotated layout keeps one plane per channel)."""
     lv = octave_lv(6)
     geom, nt, npix = RH.levels_geometry(H, W, 8, lv)
     g = torch.Generator().manual_seed(4)
