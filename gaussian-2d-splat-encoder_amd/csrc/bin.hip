@@ -22,6 +22,8 @@
 #include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 
 #include "splat_common.h"
@@ -1696,13 +1698,42 @@ void* noalloc_scratch() {
   return g_scratch_dev[dev];
 }
 
+// Ordering of splat_bin_noalloc calls on one device: every call's kernels use the device's one scratch, so each
+// call's stream first waits for the event that the previous call recorded behind its last scratch user. The
+// mutex makes (wait, launches, record) one step across threads, so the calls run one after another on the GPU
+// in the order they took the mutex, whatever streams they are queued on. The event is created on the device's
+// first call and kept until the process ends.
+struct ScratchOrder {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+};
+ScratchOrder g_scratch_order[kMaxDevices];
+
+// Per-thread read-back events of splat_bin (one per device), destroyed when a thread other than the process's
+// first one exits. The first thread's events are left to the end of the process: its thread-local objects are
+// destroyed during exit, when the HIP runtime may already be shutting down.
+struct ReadbackEvents {
+  hipEvent_t ev[kMaxDevices] = {};
+  ~ReadbackEvents() {
+    if ((pid_t)syscall(SYS_gettid) == getpid()) return;
+    for (int d = 0; d < kMaxDevices; ++d)
+      if (ev[d]) {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != d) (void)hipSetDevice(d);
+        (void)hipEventDestroy(ev[d]);
+        if (cur >= 0 && cur != d) (void)hipSetDevice(cur);
+      }
+  }
+};
+
 // One event per thread and device, recorded after the read-back of the pair count (splat_bin).
 hipEvent_t readback_event() {
-  static thread_local hipEvent_t ev[64] = {};
+  static thread_local ReadbackEvents tls;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  if (!ev[dev] && hipEventCreateWithFlags(&ev[dev], hipEventDisableTiming) != hipSuccess) ev[dev] = nullptr;
-  return ev[dev];
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  hipEvent_t& ev = tls.ev[dev];
+  if (!ev && hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) ev = nullptr;
+  return ev;
 }
 
 }  // namespace
@@ -1884,9 +1915,25 @@ int splat_bin_noalloc(const float* mu, const float* scale, const float* theta, c
                      N, pair_cap, cbytes + pbytes, kNoAllocScratchBytes, kMaxRows);
   char* ws = (char*)noalloc_scratch();
   if (!ws) return kHipError;
-  return splat_bin(mu, scale, theta, opacity, color, C, N, H, W, TILE, cutoff, lv, flags, max_pairs, rec, rect,
-                   offsets, info, info_host, ws, cbytes, pair_cap, gid_sorted, tile_starts, pair_splat, pair_q,
-                   ws + cbytes, pbytes, stream);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(kHipError, "splat_bin_noalloc: no current device");
+  ScratchOrder& order = g_scratch_order[dev];
+  hipStream_t st = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lock(order.mu);
+  if (!order.done && hipEventCreateWithFlags(&order.done, hipEventDisableTiming) != hipSuccess) {
+    order.done = nullptr;
+    return set_error(kHipError, "splat_bin_noalloc: creating the scratch-order event on device %d failed", dev);
+  }
+  if (hipStreamWaitEvent(st, order.done, 0) != hipSuccess)
+    return set_error(kHipError, "splat_bin_noalloc: ordering after the previous scratch user failed");
+  const int rc = splat_bin(mu, scale, theta, opacity, color, C, N, H, W, TILE, cutoff, lv, flags, max_pairs, rec, rect,
+                           offsets, info, info_host, ws, cbytes, pair_cap, gid_sorted, tile_starts, pair_splat, pair_q,
+                           ws + cbytes, pbytes, stream);
+  // behind every kernel the call queued (a status after launches still leaves them on the stream)
+  if (hipEventRecord(order.done, st) != hipSuccess && rc == kOk)
+    return set_error(kHipError, "splat_bin_noalloc: recording the scratch-order event failed");
+  return rc;
 }
 
 }  // extern "C"

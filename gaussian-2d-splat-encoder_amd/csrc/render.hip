@@ -672,25 +672,29 @@ __device__ __forceinline__ bool near_possible(float op, float lop, float gy, flo
   return op > kNearOpaqueBwd && d2 < smax * smax * (lop - kLog2NearOpaqueBwd + kNearMargin);
 }
 
-// Geometry of one pair in the backward's lane-per-pair loops: the whitened offsets (u0, v0) of the tile's first
-// pixel centre and the rotation rows (A, B) and (Cc, D), so that at the pixel (yy, xx) of the tile
-// u = A ly[yy] + B lx[xx] + u0 and v = Cc ly[yy] + D lx[xx] + v0, where ly[yy] and lx[xx] are the pixel centre's
-// offsets from the tile's first pixel centre (differences of the float centres, exact).
+// Geometry of one pair in the backward's lane-per-pair loops: the splat centre (gy, gx) and the rotation rows
+// (A, B) and (Cc, D), so that at the pixel centre (py, px) u = A (py - gy) + B (px - gx) and
+// v = Cc (py - gy) + D (px - gx). The offsets py - gy and px - gx are float32 differences of absolute
+// coordinates, exact where the pixel lies near the splat (Sterbenz), so u and v carry a rounding error relative
+// to their own terms there. Offsets taken from any other reference point (the tile's first pixel centre, its
+// centre) would carry that point's rounding times the whitening factor, about 2,000 per unit of the canvas for
+// a splat of a third of a pixel: 1e-4 of u^2 at the few pixels of such a splat.
 struct PairGeo {
-  float u0, v0, A, B, Cc, D;
+  float gy, gx, A, B, Cc, D;
 };
 
-__device__ __forceinline__ PairGeo pair_geo(const float4& r0, const float4& r1, float py0, float px0) {
-  const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
-  return {uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
+__device__ __forceinline__ PairGeo pair_geo(const float4& r0, const float4& r1) {
+  return {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y};
 }
 
-// A lane whose pair was taken out: u = 1e30 at every pixel, so u^2 overflows, the falloff is 0, 1 - a = 1 and
-// every sum of the lane stays 0.
+// A lane whose pair was taken out: a centre at 1e30 with u = -(py - gy) = 1e30 at every pixel, so u^2
+// overflows, the falloff is 0, 1 - a = 1 and every sum of the lane stays 0 (no product of 0 and infinity:
+// u stays finite).
 __device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
   if (mute) {
-    g.u0 = 1e30f;
-    g.A = g.B = g.Cc = g.D = 0.f;
+    g.gy = 1e30f;
+    g.A = 1.f;
+    g.B = g.Cc = g.D = 0.f;
   }
 }
 
@@ -699,24 +703,38 @@ __device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
 template <int TILE>
 __host__ __device__ constexpr int up_stride() { return TILE + 1; }
 
-// Offsets of the tile's pixel centres from the tile centre (cy, cx from the first pixel centre: half the
-// offsets of the last row / column), which lies at (ty, tx): rows in LDS, columns as wave-uniform values.
+// The tile's pixel centres (render_triton.py:455-456): the first and last row and column (py0, py1, px0, px1),
+// the half extents cy = (py1 - py0) / 2, cx = (px1 - px0) / 2, and every column's centre as a wave-uniform
+// value; the rows' centres are in LDS.
 template <int TILE>
-struct CentredOffsets {
-  float cy, cx, ty, tx;
-  float lx[TILE];
+struct TileCentres {
+  float py0, py1, px0, px1, cy, cx;
+  float pxa[TILE];
 };
 
-// Pairs whose falloff stays below 2^-kCullLog2 (about 1e-9) at every pixel centre of the tile add nothing the
-// backward keeps: their sums would change a splat's gradients by about 1e-9 of their size (the splat's own
-// tiles near its centre carry falloffs near 1). They get a zero record and no lanes of the row loops. The test
-// is on the falloff alone, not on op * falloff: the opacity gradient sum da * falloff (render_triton.py:698)
-// carries no opacity factor, so a near-transparent splat's far tiles weigh as much in it as an opaque one's.
-// At the 768 x 768 benchmark about a tenth of the pairs qualify, mostly elongated splats' tiles across their
-// narrow axis. The test is a lower bound of m = u^2 + v^2 over the box of the tile's pixel centres: u and v are
-// linear in the pixel offsets, so over the box each lies in an interval given by the corners, and
-// m >= dist(0, u-interval)^2 + dist(0, v-interval)^2.
+// Pairs whose falloff stays below 2^-kCullLog2 (about 1e-9) of the splat's own falloff at the pixel centre
+// nearest its centre, at every pixel centre of the tile, add nothing the backward keeps: their sums would change
+// the splat's gradients by about 1e-9 of their size. They get a zero record and no lanes of the row loops. The
+// bound is relative to the splat's own pixel: a splat far smaller than a pixel whose centre lies between pixel
+// centres may reach only 2^-20 at its best pixel, and an absolute cut at 2^-30 would drop tiles worth 1e-3 of
+// its scale gradient (sum q u^2 weighs its far pixels by u^2). The test is on the falloff alone, not on
+// op * falloff: the opacity gradient sum da * falloff (render_triton.py:698) carries no opacity factor, so a
+// near-transparent splat's far tiles weigh as much in it as an opaque one's. At the 768 x 768 benchmark about a
+// tenth of the pairs qualify, mostly elongated splats' tiles across their narrow axis. The test is a lower bound
+// of m = u^2 + v^2 over the box of the tile's pixel centres: u and v are linear in the pixel offsets, so over
+// the box each lies in an interval given by the corners, and m >= dist(0, u-interval)^2 + dist(0, v-interval)^2.
 constexpr float kCullLog2 = 30.f;
+
+// m = u^2 + v^2 of a splat at the centre of the canvas pixel that holds its centre (clamped to the canvas of H x W
+// pixels, rH = 1 / H, rW = 1 / W): an upper bound of the splat's smallest m over the canvas' pixel centres (the
+// centre position need not be the exact float32 pixel centre for a cut).
+__device__ __forceinline__ float near_pixel_m(float gy, float gx, float A, float B, float Cc, float D, float fH,
+                                              float fW, float rH, float rW) {
+  const float ny = fmaf(fminf(fmaxf(floorf(gy * fH), 0.f), fH - 1.f) + 0.5f, rH, -gy);
+  const float nx = fmaf(fminf(fmaxf(floorf(gx * fW), 0.f), fW - 1.f) + 0.5f, rW, -gx);
+  const float u = fmaf(A, ny, B * nx), v = fmaf(Cc, ny, D * nx);
+  return fmaf(u, u, v * v);
+}
 
 // Lower bound of u^2 + v^2 over ly in [0, Ly], lx in [0, Lx] with u = u0 + A ly + B lx, v = v0 + Cc ly + D lx.
 __device__ __forceinline__ float box_min_m(float u0, float v0, float A, float B, float Cc, float D, float Ly,
@@ -728,77 +746,119 @@ __device__ __forceinline__ float box_min_m(float u0, float v0, float A, float B,
   return fmaf(du, du, dv * dv);
 }
 
-// Two forms of the per-pair sums over whole rows of the tile (lane = pair). Offsets are taken from the tile
-// centre: u = uc + A ly + B lx and v = vc + Cc ly + D lx with (ly, lx) the centred offsets.
-//  * direct: per pixel u and v (one fma each from the row terms) and the five moments of q in (u, v),
-//    eight operations;
-//  * moments: offsets (ly', lx') from the pair's own centre (the splat centre clamped to the tile); per pixel
-//    m = u^2 + v^2 as a quadratic in lx' with per-row coefficients (no u or v) and three row sums
-//    (q, q lx', q lx'^2); each row folds its sums into the six moments of q in (ly', lx'), which map onto
-//    sum q u, ..., sum q u v once per pair since u, v are linear in (ly', lx'). Four fewer operations per
-//    pixel.
+// Two forms of the per-pair sums over whole rows of the tile (lane = pair):
+//  * direct: per pixel u and v from the offsets to the splat centre (one fma each from the row terms) and the
+//    five moments of q in (u, v), eight operations;
+//  * moments: offsets (ly', lx') from the pair's own centre, the splat centre clamped into the box of the
+//    tile's pixel centres (both exact float32 differences of absolute coordinates); per pixel m = u^2 + v^2
+//    as a quadratic in lx' with per-row coefficients (no u or v) and three row sums (q, q lx', q lx'^2); each
+//    row folds its sums into the six moments of q in (ly', lx'), which map onto sum q u, ..., sum q u v once
+//    per pair since u, v are linear in (ly', lx'). Four fewer operations per pixel.
 // The moment form evaluates sum q u^2 as up^2 sum q + 2 up sum q du + sum q du^2 (up = u at the pair's
 // centre, du = u - up): the terms cancel where q sits away from that centre, and the rounding error grows
-// with the pair's whitened span over the tile, max |du|. Centred on the splat, the error relative to the
-// splat's own sums stays below 1e-5 up to a span of 8 in float32 experiments (4x4 to 16x16 tiles), and
-// reaches 1e-4 and more for splats far smaller than a pixel (spans of 20 to 60). Pairs with a span above
-// kMomentSpan take the direct form.
+// with the pair's whitened span over the tile, max |du|. In a float32 emulation of the form (random pair
+// geometries, spans up to 8, 8x8 tiles, signed upstream) each sum's error stays below 1.2e-5 of the sum of its
+// terms' magnitudes, also for elongated rotated splats whose du^2 = (A ly' + B lx')^2 cancels along their long
+// axis; the GPU tests hold every splat's gradients to 1e-4 of their own term magnitudes across this limit.
+// Pairs with a span above kMomentSpan take the direct form.
 constexpr float kMomentSpan = 8.f;
 
 template <int TILE>
-__device__ __forceinline__ bool moment_span_ok(const PairGeo& g, const CentredOffsets<TILE>& co) {
-  return fmaxf(fmaf(fabsf(g.A), co.cy, fabsf(g.B) * co.cx), fmaf(fabsf(g.Cc), co.cy, fabsf(g.D) * co.cx)) <=
+__device__ __forceinline__ bool moment_span_ok(const PairGeo& g, const TileCentres<TILE>& tc) {
+  return fmaxf(fmaf(fabsf(g.A), tc.cy, fabsf(g.B) * tc.cx), fmaf(fabsf(g.Cc), tc.cy, fabsf(g.D) * tc.cx)) <=
          kMomentSpan;
+}
+
+// Geometry of one pair in the direct form: the splat centre, the rotation (cs, sn) and the whitening factors
+// ky = k / sy, kx = k / sx (the decode pass's own values), so that u = ky (cs dy + sn dx) and
+// v = kx (cs dx - sn dy). The rotated offsets are formed before the scaling, each as one rounding of the exact
+// sum (the row's product and its rounding error, by fma): an elongated rotated splat's narrow-axis offset is a
+// small difference of two large products along its long axis, and the whitened rows (A, B), (Cc, D) of the
+// moment form would add their own roundings to it (at an aspect ratio of 100, 1e-4 of its rotation gradient).
+// This is the order in which the reference rotates (render_triton.py:476-480), with fewer roundings.
+struct DirectGeo {
+  float gy, gx, cs, sn, ky, kx;
+};
+
+__device__ __forceinline__ DirectGeo direct_geo(const float4& r0, const float4& r3) {
+  return {r0.x, r0.y, r3.z, r3.w, kWhiten / r3.x, kWhiten / r3.y};
+}
+
+// A lane whose pair was taken out of the direct form (see mute_pair).
+__device__ __forceinline__ void mute_direct(bool mute, DirectGeo& g) {
+  if (mute) {
+    g.gy = 1e30f;
+    g.cs = g.ky = 1.f;
+    g.sn = g.kx = 0.f;
+  }
+}
+
+// The row terms of u and v at a row offset dy: cs dy and -sn dy with their rounding errors.
+struct RowTerms {
+  float au, eu, av, ev;
+};
+__device__ __forceinline__ RowTerms row_terms(const DirectGeo& g, float dy) {
+  RowTerms t;
+  t.au = g.cs * dy;
+  t.eu = fmaf(g.cs, dy, -t.au);
+  t.av = -g.sn * dy;
+  t.ev = fmaf(-g.sn, dy, -t.av);
+  return t;
+}
+
+// Whitened offsets (u, v) at column offset dx of a row.
+__device__ __forceinline__ float2 direct_uv(const DirectGeo& g, const RowTerms& t, float dx) {
+  return make_float2(g.ky * (fmaf(g.sn, dx, t.au) + t.eu), g.kx * (fmaf(g.cs, dx, t.av) + t.ev));
 }
 
 // Direct form over rows [row0, row0 + nrows), with 1 - a = 1 - op f by one fma: the caller has taken every
 // pair that may be near-opaque in the tile (near_possible) out of the wave's lanes.
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ void pair_rows_direct(const PairGeo& g, float op, const float4& col, int row0, int nrows,
-                                                 const float* s_lyc, const CentredOffsets<TILE>& co,
+__device__ __forceinline__ void pair_rows_direct(const DirectGeo& g, float op, const float4& col, int row0, int nrows,
+                                                 const float* s_pya, const TileCentres<TILE>& tc,
                                                  const float4* s_pa, const float4* s_pb, PairSums<C>& s) {
-  const float uc = fmaf(g.B, co.cx, fmaf(g.A, co.cy, g.u0));
-  const float vc = fmaf(g.D, co.cx, fmaf(g.Cc, co.cy, g.v0));
+  float dx[TILE];   // the columns' offsets from the splat centre, once per pair
+#pragma unroll
+  for (int xx = 0; xx < TILE; ++xx) dx[xx] = tc.pxa[xx] - g.gx;
 #pragma nounroll
   for (int yy = row0; yy < row0 + nrows; ++yy) {
-    const float ly = s_lyc[yy];
-    const float uy = fmaf(g.A, ly, uc), vy = fmaf(g.Cc, ly, vc);
+    const RowTerms rt = row_terms(g, s_pya[yy] - g.gy);
     const float4* pa_row = s_pa + yy * up_stride<TILE>();
     const float4* pb_row = s_pb + yy * up_stride<TILE>();
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
       const float4 pa = pa_row[xx];
       const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float u = fmaf(g.B, co.lx[xx], uy), v = fmaf(g.D, co.lx[xx], vy);
+      const float2 uv = direct_uv(g, rt, dx[xx]);
+      const float u = uv.x, v = uv.y;
       const float f = hw_exp2(-fmaf(u, u, v * v));
       bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, pa, pb, s);
     }
   }
 }
 
-// Moment form over rows [row0, row0 + nrows) for pairs with moment_span_ok (and not near-opaque); (gy, gx) is
-// the splat centre.
+// Moment form over rows [row0, row0 + nrows) for pairs with moment_span_ok (and not near-opaque).
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, float gx, float op, const float4& col,
-                                                  int row0, int nrows, const float* s_lyc,
-                                                  const CentredOffsets<TILE>& co, const float4* s_pa,
+__device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float op, const float4& col, int row0, int nrows,
+                                                  const float* s_pya, const TileCentres<TILE>& tc, const float4* s_pa,
                                                   const float4* s_pb, PairSums<C>& s) {
-  // the pair's centre (ey, ex), in centred offsets, and u, v there
-  const float ey = fminf(fmaxf(gy - co.ty, -co.cy), co.cy), ex = fminf(fmaxf(gx - co.tx, -co.cx), co.cx);
-  const float up = fmaf(g.B, co.cx + ex, fmaf(g.A, co.cy + ey, g.u0));
-  const float vp = fmaf(g.D, co.cx + ex, fmaf(g.Cc, co.cy + ey, g.v0));
+  // the pair's centre (ey, ex): the splat centre clamped into the box of the tile's pixel centres; u, v there
+  const float ey = fminf(fmaxf(g.gy, tc.py0), tc.py1), ex = fminf(fmaxf(g.gx, tc.px0), tc.px1);
+  const float eyg = ey - g.gy, exg = ex - g.gx;
+  const float up = fmaf(g.A, eyg, g.B * exg);
+  const float vp = fmaf(g.Cc, eyg, g.D * exg);
   // along a row, u = uy + B lx' and v = vy + D lx', so m = (uy^2 + vy^2) + 2 (uy B + vy D) lx' + (B^2 + D^2) lx'^2
   const float a2 = fmaf(g.B, g.B, g.D * g.D), b2 = 2.f * g.B, d2 = 2.f * g.D;
   float lxp[TILE];   // the column offsets lx', once per pair
 #pragma unroll
-  for (int xx = 0; xx < TILE; ++xx) lxp[xx] = co.lx[xx] - ex;
+  for (int xx = 0; xx < TILE; ++xx) lxp[xx] = tc.pxa[xx] - ex;
   // sum q {1, ly', ly'^2, lx' ly'} by rows; sum q {lx', lx'^2} from the column sums cq of q after the rows
   float m0 = 0.f, my = 0.f, myy = 0.f, mxy = 0.f, cq[TILE];
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) cq[xx] = 0.f;
 #pragma nounroll
   for (int yy = row0; yy < row0 + nrows; ++yy) {
-    const float ly = s_lyc[yy] - ey;
+    const float ly = s_pya[yy] - ey;
     const float uy = fmaf(g.A, ly, up), vy = fmaf(g.Cc, ly, vp);
     const float a0 = fmaf(uy, uy, vy * vy), a1 = fmaf(uy, b2, vy * d2);
     const float4* pa_row = s_pa + yy * up_stride<TILE>();
@@ -844,18 +904,17 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float gy, fl
 // Per-pair sums over the pixels [j0, j0 + npx) of one row of the tile (lane = pair, lane-varying j0): the
 // remainder chunks that give a pair fewer pixels than a row.
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ void pair_row_part(const PairGeo& g, float op, const float4& col, int j0, int npx,
-                                              const float* s_ly, const float* s_lx, const float4* s_pa,
+__device__ __forceinline__ void pair_row_part(const DirectGeo& g, float op, const float4& col, int j0, int npx,
+                                              const float* s_pya, const float* s_pxa, const float4* s_pa,
                                               const float4* s_pb, PairSums<C>& s) {
   const int yy = j0 / TILE;
-  const float ly = s_ly[yy];
-  const float uy = fmaf(g.A, ly, g.u0), vy = fmaf(g.Cc, ly, g.v0);
+  const RowTerms rt = row_terms(g, s_pya[yy] - g.gy);
   for (int l = j0; l < j0 + npx; ++l) {
     const int xx = l - yy * TILE;
-    const float lx = s_lx[xx];
     const int k = yy * up_stride<TILE>() + xx;
     const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float u = fmaf(g.B, lx, uy), v = fmaf(g.D, lx, vy);
+    const float2 uv = direct_uv(g, rt, s_pxa[xx] - g.gx);
+    const float u = uv.x, v = uv.y;
     const float f = hw_exp2(-fmaf(u, u, v * v));
     bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, s_pa[k], pb, s);
   }
@@ -866,19 +925,19 @@ __device__ __forceinline__ void pair_row_part(const PairGeo& g, float op, const 
 // of the lane-per-pair loops (a few near-opaque splats around their centre tile, and splats far smaller than
 // the tile).
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, float py0, float px0,
-                                                    const float* s_ly, const float* s_lx, const float4* s_pa,
-                                                    const float4* s_pb, int lane, float& op) {
+__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, const float* s_pya,
+                                                    const float* s_pxa, const float4* s_pa, const float4* s_pb, int lane,
+                                                    float& op) {
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
   const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
-  const PairGeo pg = pair_geo(r0, r1, py0, px0);
+  const DirectGeo dg = direct_geo(r0, r4[3]);
   const PairOp po = pair_op(r1.z);
   op = r1.z;
   PairSums<C> s;
   for (int l = lane; l < TILE * TILE; l += 64) {
     const int yy = l / TILE, xx = l % TILE;
-    const float ly = s_ly[yy], lx = s_lx[xx];
-    const float u = fmaf(pg.A, ly, fmaf(pg.B, lx, pg.u0)), v = fmaf(pg.Cc, ly, fmaf(pg.D, lx, pg.v0));
+    const float2 uv = direct_uv(dg, row_terms(dg, s_pya[yy] - dg.gy), s_pxa[xx] - dg.gx);
+    const float u = uv.x, v = uv.y;
     const float m = fmaf(u, u, v * v);
     const int k = yy * up_stride<TILE>() + xx;
     const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -913,10 +972,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   constexpr int RS = up_stride<TILE>();
   __shared__ float4 s_pa[TILE * RS];
   __shared__ float4 s_pb[TILE * RS];
-  __shared__ float s_ly[TILE], s_lx[TILE];
-  __shared__ float s_lyc[TILE];
+  __shared__ float s_pya[TILE], s_pxa[TILE];
   __shared__ int s_defer_w[S][128], s_mi_w[S][128];
-  __shared__ float2 s_muv_w[S][128];
   int chunk = 0, nsplit = 1;
   const TileAt ta = SPLIT ? split_item(L, P, xcd_swizzle(blockIdx.x, ntiles), &chunk, &nsplit) : tile_at(L, tb0, ntiles);
   if (!((L.mask >> ta.l) & 1)) return;
@@ -925,7 +982,6 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   const int wid = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;   // wave-uniform
   int* s_defer = s_defer_w[wid];
   int* s_mi = s_mi_w[wid];
-  float2* s_muv = s_muv_w[wid];
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int l = (int)threadIdx.x; l < NP; l += 64 * S) {
     const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
@@ -953,29 +1009,24 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
       bg_part[(size_t)threadIdx.x * ntiles + (t - tb0)] = v;
     }
   }
-  // the tile's first and last pixel centres (render_triton.py:455-456) and the per-row / per-column offsets
+  // the tile's pixel centres (render_triton.py:455-456): rows and columns in LDS, columns also wave-uniform
   const float fH = (float)ta.H, fW = (float)ta.W;
-  const float py0 = uniform_f(((float)(ta.ty * TILE) + 0.5f) / fH);
-  const float px0 = uniform_f(((float)(ta.tx * TILE) + 0.5f) / fW);
-  const float py1 = uniform_f(((float)(ta.ty * TILE + TILE - 1) + 0.5f) / fH);
-  const float px1 = uniform_f(((float)(ta.tx * TILE + TILE - 1) + 0.5f) / fW);
   if (threadIdx.x < TILE) {
-    s_ly[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / fH - py0;
-    s_lx[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW - px0;
+    s_pya[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / fH;
+    s_pxa[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW;
   }
   __syncthreads();
-  CentredOffsets<TILE> co;
-  co.cy = 0.5f * (py1 - py0);
-  co.cx = 0.5f * (px1 - px0);
-  co.ty = py0 + co.cy;
-  co.tx = px0 + co.cx;
+  TileCentres<TILE> tc;
+  tc.py0 = uniform_f(s_pya[0]);
+  tc.py1 = uniform_f(s_pya[TILE - 1]);
+  tc.px0 = uniform_f(s_pxa[0]);
+  tc.px1 = uniform_f(s_pxa[TILE - 1]);
+  tc.cy = 0.5f * (tc.py1 - tc.py0);
+  tc.cx = 0.5f * (tc.px1 - tc.px0);
 #pragma unroll
-  for (int xx = 0; xx < TILE; ++xx) co.lx[xx] = uniform_f(s_lx[xx] - co.cx);
-  if (threadIdx.x < TILE) {
-    const float ly = s_ly[lane] - co.cy;
-    s_lyc[lane] = ly;
-  }
-  __syncthreads();
+  for (int xx = 0; xx < TILE; ++xx) tc.pxa[xx] = uniform_f(s_pxa[xx]);
+  const float py0 = tc.py0, px0 = tc.px0, py1 = tc.py1, px1 = tc.px1;
+  const float rH = uniform_f(1.f / fH), rW = uniform_f(1.f / fW);
   int g0 = starts[t], g1 = starts[t + 1];
   if (SPLIT) {   // the item's chunk: whole passes of 64 pairs where the tile's list allows
     const int len = (((g1 - g0 + nsplit - 1) / nsplit) + 63) & ~63;
@@ -988,10 +1039,12 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     g1 = min(g1, g0 + chunk);
   }
   const unsigned long long below = (1ull << lane) - 1ull;
-  // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (falloff below
-  // 2^-kCullLog2 at every pixel centre: a zero record), near-opaque (summed by careful_pair at once), small
-  // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi / s_muv with
-  // their offsets at the tile origin, for a moment pass). Only queued pairs occupy lanes of the row loops.
+  // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (falloff below 2^-kCullLog2
+  // of the splat's falloff at its nearest pixel centre, at every pixel centre: a zero record), near-opaque
+  // (summed by careful_pair at once), small
+  // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi for a moment
+  // pass). Only queued pairs occupy lanes of the row loops. The classification bounds u and v over the tile from
+  // their values at the tile's first pixel centre (float64 offsets, rounded once).
   int nmain = 0, ndefer = 0;
   auto classify = [&](int c0) {
     const int i = c0 + lane;
@@ -1001,34 +1054,31 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     const float4 r0 = r4[0], r1 = r4[1];
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
     const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
-    const PairGeo pg{uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
-    const bool negl = act && box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) > kCullLog2;
+    const PairGeo pg = pair_geo(r0, r1);
+    const bool negl = act && box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) >
+                                 kCullLog2 + near_pixel_m(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, fH, fW, rH, rW);
     const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
-    const bool defer = act && !negl && !near && !moment_span_ok<TILE>(pg, co);
+    const bool defer = act && !negl && !near && !moment_span_ok<TILE>(pg, tc);
     const bool mom = act && !negl && !near && !defer;
     const int q = (negl || near) ? pair_q[i] : 0;
     if (negl) store_pair<C>(psum + (size_t)q * pair_rec<C>(), PairSums<C>(), 1.f);
     for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
       const int j = __builtin_ctzll(nm);
       float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), py0, px0, s_ly, s_lx,
-                                                          s_pa, s_pb, lane, opj);
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_pya, s_pxa, s_pa,
+                                                          s_pb, lane, opj);
       if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
     }
     const unsigned long long dm = __ballot(defer), mm = __ballot(mom);
     if (defer) s_defer[ndefer + __popcll(dm & below)] = i;
-    if (mom) {
-      const int k = nmain + __popcll(mm & below);
-      s_mi[k] = i;
-      s_muv[k] = uv;
-    }
+    if (mom) s_mi[nmain + __popcll(mm & below)] = i;
     ndefer += __popcll(dm);
     nmain += __popcll(mm);
   };
   // One pass over np <= 64 queued pairs: Lp lanes per pair (the largest power of two with np Lp <= 64, at most
   // NP), lane = (pair pr = lane / Lp, share sub = lane % Lp of the tile's pixels: whole rows when that share is
-  // at least a row); the Lp partial sums are combined with xor shuffles. MOM: the moment form over s_mi / s_muv,
-  // else the direct form over s_defer.
+  // at least a row); the Lp partial sums are combined with xor shuffles. MOM: the moment form over s_mi, else the
+  // direct form over s_defer.
   auto pass = [&](int np, auto mom) {
     constexpr bool MOM = decltype(mom)::value != 0;
     int lg = 0;   // Lp = 2^lg (shifts, not divisions: Lp is a runtime value)
@@ -1042,28 +1092,18 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
     const float op = r1.z;
-    PairGeo pg;
-    if (MOM) {
-      const float2 uv = s_muv[act ? pr : 0];
-      pg = {uv.x, uv.y, r0.z, r0.w, r1.x, r1.y};
-    } else {
-      pg = pair_geo(r0, r1, py0, px0);
-    }
-    mute_pair(!act, pg);
     PairSums<C> s;
-    if (Lp == 1) {   // every row (uniform branch; the loops' bounds are wave-uniform)
-      if (MOM)
-        pair_rows_moments<C, ODDS, TILE>(pg, r0.x, r0.y, op, col, 0, TILE, s_lyc, co, s_pa, s_pb, s);
-      else
-        pair_rows_direct<C, ODDS, TILE>(pg, op, col, 0, TILE, s_lyc, co, s_pa, s_pb, s);
-    } else if (npx >= TILE) {   // whole rows
-      if (MOM)
-        pair_rows_moments<C, ODDS, TILE>(pg, r0.x, r0.y, op, col, sub * (npx / TILE), npx / TILE, s_lyc, co, s_pa,
-                                         s_pb, s);
-      else
-        pair_rows_direct<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_lyc, co, s_pa, s_pb, s);
+    if (MOM && npx >= TILE) {   // whole rows (uniform branch; the loops' bounds are wave-uniform)
+      PairGeo pg = pair_geo(r0, r1);
+      mute_pair(!act, pg);
+      pair_rows_moments<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_pya, tc, s_pa, s_pb, s);
     } else {
-      pair_row_part<C, ODDS, TILE>(pg, op, col, sub * npx, npx, s_ly, s_lx, s_pa, s_pb, s);
+      DirectGeo dg = direct_geo(r0, r4[3]);
+      mute_direct(!act, dg);
+      if (npx >= TILE)
+        pair_rows_direct<C, ODDS, TILE>(dg, op, col, sub * (npx / TILE), npx / TILE, s_pya, tc, s_pa, s_pb, s);
+      else
+        pair_row_part<C, ODDS, TILE>(dg, op, col, sub * npx, npx, s_pya, s_pxa, s_pa, s_pb, s);
     }
     for (int d = 1; d < Lp; d <<= 1) xor_reduce<C>(s, d);
     if (act && sub == 0) store_pair<C>(psum + (size_t)pair_q[i] * pair_rec<C>(), s, op);
@@ -1087,12 +1127,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
       pass(np, IC<1>{});
       const int rest = nmain - np;
       const int mi = lane < rest ? s_mi[np + lane] : 0;
-      const float2 muv = lane < rest ? s_muv[np + lane] : make_float2(0.f, 0.f);
       wave_lds_sync();
-      if (lane < rest) {
-        s_mi[lane] = mi;
-        s_muv[lane] = muv;
-      }
+      if (lane < rest) s_mi[lane] = mi;
       nmain = rest;
     } else if (done < g1) {
       classify(done);

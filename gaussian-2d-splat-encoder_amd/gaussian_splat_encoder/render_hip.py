@@ -40,6 +40,24 @@ def _dev_check(*ts):
             raise RuntimeError("the HIP splat renderer needs device tensors (got a CPU tensor)")
 
 
+def _batch_args(mu, log_scale, color, opacity, bg, theta):
+    """Checks the parameter shapes against color [B,N,C] and returns bg as [B,C]. The per-image launches take
+    image b's data at b times each tensor's batch stride, so every tensor must hold B images. A bg of shape
+    [1,C] is broadcast over the batch (the composite of render_triton.py:921, :980 broadcasts it; autograd sums
+    its gradient back to [1,C])."""
+    if color.dim() != 3:
+        raise ValueError(f"color must be [B,N,C], got {tuple(color.shape)}")
+    B, N, C = color.shape
+    want = {"mu": (mu, (B, N, 2)), "log_scale": (log_scale, (B, N, 2)), "opacity": (opacity, (B, N)),
+            "theta": (theta, (B, N))}
+    for name, (t, shape) in want.items():
+        if t is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be {list(shape)} for color {list(color.shape)}, got {list(t.shape)}")
+    if bg.dim() != 2 or bg.shape[1] != C or bg.shape[0] not in (1, B):
+        raise ValueError(f"bg must be [{B},{C}] or [1,{C}] for color {list(color.shape)}, got {list(bg.shape)}")
+    return bg.expand(B, C) if bg.shape[0] != B else bg
+
+
 def _f32(t):
     """t as contiguous fp32 (itself when it already is: the kernels only take its data pointer)."""
     if t is None or (t.dtype is torch.float32 and t.is_contiguous()):
@@ -946,6 +964,7 @@ def _scale_arg(log_scale):
 
 
 def _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
+    bg = _batch_args(mu, log_scale, color, opacity, bg, theta)
     scale, is_log = _scale_arg(log_scale)
     return _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
                                     is_log)
@@ -956,6 +975,7 @@ def render_alpha_full_triton(mu, log_scale, color, opacity, bg, H, W, theta=None
     """render_triton.py:326-347. cull=False: exact (every pixel sums every splat); cull=True: tile-binned
     at `cutoff` sigma. Returns [B,C,H,W]. The name is kept for drop-in compatibility; no Triton is used."""
     B, N, C = color.shape
+    bg = _batch_args(mu, log_scale, color, opacity, bg, theta)
     if cull:
         scale, is_log = _scale_arg(log_scale)
         return _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds, is_log)

@@ -31,9 +31,10 @@ extern "C" {
 #define SPLAT_FLAG_ODDS 2   /* colour weight a/(1-a) instead of a */
 #define SPLAT_FLAG_UPS 4    /* composite adds the coarse levels' upsampled fields; clamp_min gradient of S_a */
 #define SPLAT_FLAG_WIDE 8   /* TILE 8: 16 waves share each tile's pair list, instead of 4 in the forward and 1 in
-                               the backward (a performance hint for launches of few tiles with long lists; forward
-                               results are identical up to the order the partial sums are added in, backward
-                               results are identical) */
+                               the backward (a performance hint for launches of few tiles with long lists; results
+                               are identical up to summation order: the forward adds the waves' partial sums in
+                               another grouping, and the backward's per-pair sums of the pairs that end a wave's
+                               share in a partial pass are split over lanes and combined by xor shuffles) */
 #define SPLAT_FLAG_LOG_SCALE 16 /* binning (splat_bin, splat_bin_count): `scale` holds the raw log-scales [N,2]; the
                                    decode pass activates them, softplus(x) + 1e-4 with the bits torch's fp32
                                    F.softplus(x) + 1e-4 gives (params.py:18-28), so callers need no activation
@@ -147,11 +148,14 @@ int splat_bin_finish(long long *info_host, const long long *info, int nlev, long
  * of N splats and pair_cap pairs (splat_bin_count_workspace_bytes + splat_bin_pairs_workspace_bytes) must
  * fit the scratch: 12 bytes per pair plus 8 bytes per tile row and 256 splats for level tables of at most
  * 1,024 tile rows (pair_cap up to ~5M at 768 x 768), about 25 bytes per pair past that; a larger request
- * returns status 5 before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device (per
- * thread) looks up the scratch address and, for a pageable info_host, creates the read-back event. Statuses as splat_bin. Every call
- * on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams or threads before the
- * previous call's kernels have finished) race; calls in one stream do not. Nothing in the scratch needs to
- * start at zero: every region is written before it is read within a call. */
+ * returns status 5 before any launch. No hipMalloc, hipFree or allocating library call; the first call on a device
+ * looks up the scratch address and creates the device's scratch-order event, and the first call of a thread with a
+ * pageable info_host creates its read-back event. Statuses as splat_bin. Every call on a GPU shares that GPU's
+ * scratch, so calls are serialised on the device: each call's stream waits for the event recorded behind the
+ * previous call's last kernel (on whatever stream or thread it was queued), under a per-device mutex. Calls on
+ * other streams or threads therefore never overlap on the GPU, and a caller's stream may wait for another
+ * caller's binning. Nothing in the scratch needs to start at zero: every region is written before it is read
+ * within a call. */
 int splat_bin_noalloc(const float *mu, const float *scale, const float *theta, const float *opacity,
                       const float *color, int C, int N, int H, int W, int TILE, float cutoff, const splat_levels *lv,
                       int flags, long long max_pairs, float *rec, int *rect, int *offsets, long long *info,

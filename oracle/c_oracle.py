@@ -84,8 +84,9 @@ def fwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=F
 def bwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=False, fields=False, bg=None,
              T=None, asum=None, fg=None, gout=None, dslog=None, dsa=None, dsac=None):
     """float64 cull backward of one batch -> dict of per-splat grads (+ 'bg' in composite mode), plus
-    'op_scale': per splat, the summed magnitudes of the terms of its opacity gradient (the scale of a
-    per-splat relative check of g_op)."""
+    'mag': per splat, for every gradient by name (mu, scale, theta, op, col; same shapes as the gradients) the
+    summed magnitudes of the terms of that gradient component, the scale of a per-splat relative check (see
+    orc_bwd_cull); 'op_scale' is mag['op']."""
     mu, scale, theta, opacity, color = map(_f32, (mu, scale, theta, opacity, color))
     n, C = color.shape
     d64 = lambda x: None if x is None else np.ascontiguousarray(x, np.float64).reshape(-1)
@@ -94,17 +95,21 @@ def bwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=F
     g_th = np.zeros(n) if theta is not None else None
     g_op, g_col = np.zeros(n), np.zeros(n * C)
     g_bg = None if fields else np.zeros(C)
-    g_ops = np.zeros(n)
+    KG = 6 + C
+    g_mag = np.zeros(n * KG)
     lib().orc_bwd_cull(_p(mu), _p(scale), _p(theta), _p(opacity), _p(color), ctypes.c_int(C), ctypes.c_int(n),
                        _p(np.ascontiguousarray(gid, np.int32)), _p(np.ascontiguousarray(starts, np.int32)),
                        ctypes.c_int(H), ctypes.c_int(W), ctypes.c_int(TILE), ctypes.c_int(int(odds)),
                        ctypes.c_int(int(fields)), _p(bg), _p(d64(T)), _p(d64(asum)), _p(d64(fg)), _p(d64(gout)),
                        _p(d64(dslog)), _p(d64(dsa)), _p(d64(dsac)), _p(g_mu), _p(g_sc), _p(g_th), _p(g_op),
-                       _p(g_col), _p(g_bg), _p(g_ops))
+                       _p(g_col), _p(g_bg), _p(g_mag))
+    m = g_mag.reshape(n, KG)
+    mag = {"mu": m[:, 0:2].copy(), "scale": m[:, 2:4].copy(), "op": m[:, 5].copy(), "col": m[:, 6:].copy()}
     out = {"mu": g_mu.reshape(n, 2), "scale": g_sc.reshape(n, 2), "op": g_op, "col": g_col.reshape(n, C),
-           "op_scale": g_ops}
+           "op_scale": mag["op"], "mag": mag}
     if g_th is not None:
         out["theta"] = g_th
+        mag["theta"] = m[:, 4].copy()
     if g_bg is not None:
         out["bg"] = g_bg
     return out

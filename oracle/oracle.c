@@ -162,22 +162,26 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
 
 /* Backward over one batch. fields != 0: upstream dS_log[P], dS_a[P], dS_ac[P*C]; else upstream gout[P*C]
  * with the saved T, asum, fg and bg. Per-splat outputs are zeroed here and summed over pairs.
- * g_op_scale (optional, [N]): the sum over the splat's pixel-pairs of the magnitudes of every term that
- * enters its opacity gradient, f * (|dS_log u| + (|dS_a| + sum_c |dS_ac[c] col[c]|) u^k) with k = 2 for odds
- * and 0 for alpha: the scale against which a per-splat relative error of g_op is meaningful.
+ * g_mag (optional, [N, 6 + C]): per splat and gradient component (mu_y, mu_x, s_y, s_x, theta, opacity,
+ * colour[C]) the sum over the splat's pixel-pairs of the magnitudes of every term that enters that component:
+ * the scale against which a per-splat relative error of the component is meaningful. Each pixel-pair's term is
+ * the reference's product of factors (render_triton.py:688-710) with every sum in it replaced by the sum of its
+ * terms' magnitudes: da by m_da = |dS_log u| + (|dS_a| + sum_c |dS_ac[c] col[c]|) u^k (k = 2 for odds, 0 for
+ * alpha), and the two summands of each of g_mu and g_theta taken apart (|gry c| + |grx s|, |gry rx| + |grx ry|).
  * Tiles run in parallel (OpenMP), each thread into accumulators of its own, summed in thread order. */
-enum { ACC_MU = 0, ACC_SC = 2, ACC_TH = 4, ACC_OP = 5, ACC_OPS = 6, ACC_COL = 7 };
+enum { ACC_MU = 0, ACC_SC = 2, ACC_TH = 4, ACC_OP = 5, ACC_COL = 6 };
 
 void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const float* opacity,
                   const float* color, int C, int N, const int* gid_sorted, const int* tile_starts, int H,
                   int W, int TILE, int odds, int fields, const float* bg, const double* T,
                   const double* asum, const double* fg, const double* gout, const double* dslog_in,
                   const double* dsa_in, const double* dsac_in, double* g_mu, double* g_scale,
-                  double* g_theta, double* g_op, double* g_col, double* g_bg, double* g_op_scale) {
+                  double* g_theta, double* g_op, double* g_col, double* g_bg, double* g_mag) {
     orc_splats s = {mu, scale, theta, opacity, color, NULL, NULL};
     trig_tables(&s, N);
     const int ntx = (W + TILE - 1) / TILE, nty = (H + TILE - 1) / TILE;
-    const int K = ACC_COL + C;
+    const int KG = ACC_COL + C;   /* gradient components; their magnitude sums follow at KG + k */
+    const int K = 2 * KG;
     int nth = 1;
 #ifdef _OPENMP
     nth = omp_get_max_threads();
@@ -239,31 +243,44 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
                             da = -dS_log * u + dS_a + col_term; cw = a;
                             mag = fabs(dS_log * u) + fabs(dS_a) + col_abs;
                         }
-                        for (int c = 0; c < C; ++c) a_g[ACC_COL + c] += cw * dS_ac[c];
+                        double* m_g = a_g + KG;
+                        for (int c = 0; c < C; ++c) {
+                            a_g[ACC_COL + c] += cw * dS_ac[c];
+                            m_g[ACC_COL + c] += fabs(cw * dS_ac[c]);
+                        }
                         const double da_fo = fo < ORC_CLAMP ? da : 0.0;
+                        const double mag_fo = fo < ORC_CLAMP ? mag : 0.0;
                         const double op = (double)opacity[g];
                         const double sy = (double)scale[2 * g], sx = (double)scale[2 * g + 1];
                         a_g[ACC_OP] += da_fo * f;
-                        if (fo < ORC_CLAMP) a_g[ACC_OPS] += mag * f;
-                        const double gm = (da_fo * op) * (-0.5 * f);
+                        m_g[ACC_OP] += mag_fo * f;
+                        const double gm = (da_fo * op) * (-0.5 * f), gmm = (mag_fo * op) * (0.5 * f);
                         a_g[ACC_SC + 0] += gm * (-2.0 * ry * ry) / (sy * sy * sy);
                         a_g[ACC_SC + 1] += gm * (-2.0 * rx * rx) / (sx * sx * sx);
+                        m_g[ACC_SC + 0] += gmm * (2.0 * ry * ry) / (sy * sy * sy);
+                        m_g[ACC_SC + 1] += gmm * (2.0 * rx * rx) / (sx * sx * sx);
                         const double gry = gm * 2.0 * ry / (sy * sy), grx = gm * 2.0 * rx / (sx * sx);
+                        const double grym = gmm * 2.0 * fabs(ry) / (sy * sy), grxm = gmm * 2.0 * fabs(rx) / (sx * sx);
                         if (theta) {
                             const double cth = s.cs[g], sth = s.sn[g];
                             a_g[ACC_TH] += gry * rx - grx * ry;
                             a_g[ACC_MU + 0] += -(gry * cth - grx * sth);
                             a_g[ACC_MU + 1] += -(gry * sth + grx * cth);
+                            m_g[ACC_TH] += grym * fabs(rx) + grxm * fabs(ry);
+                            m_g[ACC_MU + 0] += grym * fabs(cth) + grxm * fabs(sth);
+                            m_g[ACC_MU + 1] += grym * fabs(sth) + grxm * fabs(cth);
                         } else {
                             a_g[ACC_MU + 0] += -gry;
                             a_g[ACC_MU + 1] += -grx;
+                            m_g[ACC_MU + 0] += grym;
+                            m_g[ACC_MU + 1] += grxm;
                         }
                     }
                 }
         }
     }
     for (int g = 0; g < N; ++g) {
-        double v[ACC_COL + 16];
+        double v[2 * (ACC_COL + 16)];
         for (int k = 0; k < K; ++k) v[k] = 0.0;
         for (int th = 0; th < nth; ++th) {
             const double* a_g = acc + ((size_t)th * (size_t)N + (size_t)g) * K;
@@ -273,7 +290,8 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
         g_scale[2 * g] = v[ACC_SC]; g_scale[2 * g + 1] = v[ACC_SC + 1];
         if (g_theta) g_theta[g] = v[ACC_TH];
         g_op[g] = v[ACC_OP];
-        if (g_op_scale) g_op_scale[g] = v[ACC_OPS];
+        if (g_mag)
+            for (int k = 0; k < KG; ++k) g_mag[(size_t)g * KG + k] = v[KG + k];
         for (int c = 0; c < C; ++c) g_col[g * C + c] = v[ACC_COL + c];
     }
     if (g_bg)

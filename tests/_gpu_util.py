@@ -10,6 +10,9 @@ from gaussian_splat_encoder.params import activate_scale
 # reference magnitude of each tensor (the reference self-tests' definition of "rel").
 IMG_TOL = 1e-5
 GRAD_REL_TOL = 1e-4
+# Per-splat bar: every gradient component of every splat within 1e-4 of that splat's own scale for the component
+# (the oracle's 'mag': the summed magnitudes of the terms entering it), floored at 1e-7 of the largest scale.
+PER_SPLAT_TOL = 1e-4
 
 
 def np_(t):
@@ -37,9 +40,22 @@ def random_scene(n, H, W, seed, dev, ls_mean_px=2.5, ls_std=0.6, op_max=1.0, the
     return mv(mu), mv(ls), mv(col), mv(op), mv(bg), mv(th)
 
 
+def check_per_splat(got, gref, tol=PER_SPLAT_TOL):
+    """Every gradient the oracle gives a per-splat scale for (mu, scale, col, op, theta), per splat and component.
+    `got` maps names to device tensors with a batch dimension of 1 (None for an absent theta). Returns the
+    errors by name."""
+    from _scenes import per_splat_errors
+    errs = per_splat_errors({k: None if v is None else np_(v[0]) for k, v in got.items()}, gref)
+    worst = {k: f"{e:.2e} at splat {i // max(1, np.asarray(gref[k]).reshape(len(gref[k]), -1).shape[1])}"
+             for k, (e, i) in errs.items() if e > tol}
+    assert not worst, f"per-splat gradient errors above {tol:g} of the splat's scale: {worst}"
+    return {k: e for k, (e, _) in errs.items()}
+
+
 def device_bins(mu, scale, H, W, TILE=8, cutoff=3.0):
     gid_b, st_b, ntx, nt = RH._build_tiles(mu, scale, H, W, TILE, cutoff)
     return [g.cpu().numpy() for g in gid_b], [s.cpu().numpy() for s in st_b]
 
 
-__all__ = ["IMG_TOL", "GRAD_REL_TOL", "np_", "rel_err", "random_scene", "device_bins", "activate_scale", "RH"]
+__all__ = ["IMG_TOL", "GRAD_REL_TOL", "PER_SPLAT_TOL", "np_", "rel_err", "random_scene", "device_bins",
+           "check_per_splat", "activate_scale", "RH"]

@@ -183,6 +183,37 @@ def test_batch_of_three(dev, entry):
             assert rel_err(np_(g1[n][0]), np_(gd[n][b])) <= 1e-5, n
 
 
+@pytest.mark.parametrize("entry", ["cull", "octave", "multires"])
+def test_background_broadcast_over_batch(dev, entry):
+    """A [1, C] background with B = 2 is broadcast over the batch, as the reference's torch composite broadcasts
+    it (render_triton.py:921, :980): each image equals the image rendered alone with that background, and the
+    background's gradient is the sum of the per-image ones. Shapes that do not match the batch are refused."""
+    H = W = 40
+    fn, kw = BATCH_ENTRIES[entry]
+    mu, ls, col, op, bg, th = random_scene(300, H, W, seed=35, dev=dev, B=2)
+    bg1 = bg[:1].clone()
+    gout = torch.randn(2, 3, H, W, generator=torch.Generator().manual_seed(9)).to(dev)
+    leaves = [t.clone().requires_grad_(True) for t in (mu, ls, col, op, bg1, th)]
+    out = fn(*leaves[:5], H, W, theta=leaves[5], odds=True, **kw)
+    (out * gout).sum().backward()
+    g_bg = torch.zeros_like(bg1)
+    for b in range(2):
+        one = [t[b:b + 1].clone().requires_grad_(True) for t in (mu, ls, col, op)] + [bg1.clone().requires_grad_(True),
+                                                                                     th[b:b + 1].clone()]
+        o1 = fn(*one[:5], H, W, theta=one[5], odds=True, **kw)
+        (o1 * gout[b:b + 1]).sum().backward()
+        assert (o1[0] - out[b]).abs().max().item() <= 1e-6
+        g_bg += one[4].grad
+        assert rel_err(np_(one[2].grad[0]), np_(leaves[2].grad[b])) <= 1e-5
+    assert leaves[4].grad.shape == (1, 3)
+    assert rel_err(np_(leaves[4].grad), np_(g_bg)) <= 1e-5
+    for bad_bg in (bg[:, :2], torch.rand(3, 3, device=dev)):
+        with pytest.raises(ValueError, match="bg must be"):
+            fn(mu, ls, col, op, bad_bg, H, W, theta=th, **kw)
+    with pytest.raises(ValueError, match="opacity must be"):
+        fn(mu, ls, col, op[:1], bg, H, W, theta=th, **kw)
+
+
 @pytest.mark.parametrize("kind", ["cull", "octave", "multires"])
 def test_scale_activation_in_decode_matches_torch_bits(dev, monkeypatch, kind):
     """fp32 log-scales are activated inside the binning's decode pass and the log-scale gradient is chained in

@@ -12,7 +12,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, np_, random_scene, rel_err
+from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, check_per_splat, np_, random_scene, rel_err
 from gaussian_splat_encoder import _lib, synth
 from oracle import c_oracle
 from oracle import render_ref as R
@@ -158,20 +158,25 @@ def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=
     out = R.composite(*S, bg64, straight_through=False)[0]
     (out * torch.from_numpy(np_(gout)).double()).sum().backward()
     grads = {"mu": np.zeros((N, 2)), "scale": np.zeros((N, 2)), "col": np.zeros((N, C)), "op": np.zeros(N),
-             "theta": np.zeros(N) if th is not None else None, "bg": bg64.grad.numpy(), "op_scale": np.zeros(N)}
+             "theta": np.zeros(N) if th is not None else None, "bg": bg64.grad.numpy()}
+    mag = {k: np.zeros_like(v) for k, v in grads.items() if v is not None and k != "bg"}
     for (l, idx, args, gid, st, Hl, Wl), f in zip(per_level, leaves):
         d = [x.grad.numpy() if x.grad is not None else np.zeros(x.shape) for x in f]
         gl = c_oracle.bwd_cull(*args, gid, st, Hl, Wl, TILE, odds=odds, fields=True, dslog=d[0], dsa=d[1], dsac=d[2])
-        for k in ("mu", "scale", "col", "op", "theta", "op_scale"):
+        for k in ("mu", "scale", "col", "op", "theta"):
             if grads[k] is not None:
                 grads[k][idx] = gl[k]
+                mag[k][idx] = gl["mag"][k]
+    grads["mag"] = mag
+    grads["op_scale"] = mag["op"]
     return out.detach().numpy(), grads
 
 
 def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL,
-               want_grads=False):
-    """Fused level render of one batch against composed_oracle. Returns the bins, and with want_grads also the
-    device gradients by name and the oracle's."""
+               want_grads=False, per_splat=True):
+    """Fused level render of one batch against composed_oracle: the image, every gradient tensor and, with
+    per_splat, every gradient component of every splat against that splat's own scale (check_per_splat).
+    Returns the bins, and with want_grads also the device gradients by name and the oracle's."""
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
     out, (T, asum, fg), bins = RH._forward_levels(mu, sc, col, op, bg, th, H, W, TILE, 3.0, None, odds, lv)
@@ -187,6 +192,8 @@ def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_
             continue
         e = rel_err(np_(got[0]), gref[name])
         assert e <= grad_tol, f"grad {name}: rel {e:.2e}"
+    if per_splat:
+        check_per_splat({"mu": g_mu, "scale": g_sc, "col": g_col, "op": g_op, "theta": g_th}, gref)
     if want_grads:
         return bins, {"mu": g_mu, "scale": g_sc, "col": g_col, "op": g_op, "bg": g_bg, "theta": g_th}, gref
     return bins

@@ -1,0 +1,74 @@
+"""Per-splat parity of every backward gradient where the per-tile backward takes its numerical shortcut.
+
+The backward sums each pair's moments around the pair's own centre (the splat centre clamped to the tile) and
+maps them onto sum q u, ..., sum q u v once per pair; sum q u^2 then comes out as up^2 sum q + 2 up sum q du +
+sum q du^2, whose terms cancel where q sits away from that centre, more so the larger the pair's whitened span
+over the tile. Pairs whose span exceeds the kernel's limit (8) take the direct form instead. Every component of
+every splat is held to 1e-4 of that splat's own scale for the component (the float64 C oracle's summed term
+magnitudes, render_triton.py:688-710), beside the tensor-wide bar, on scenes built around that limit:
+* splats whose smaller axis puts their spans over an 8 x 8 tile at 5 to 11 (sigma about 0.3 to 0.7 px);
+* splats far smaller than a pixel (direct form);
+* the benchmark frame through the octave render (alpha and odds).
+Every run_case / run_levels call of the other GPU tests applies the same per-splat check.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import RH, activate_scale, np_
+from _scenes import span_scene, spans
+from gaussian_splat_encoder import _lib, synth
+from test_gpu_levels import run_levels
+from test_gpu_render import run_case
+
+pytestmark = pytest.mark.gpu
+
+MOMENT_SPAN = 8.0
+
+
+def on(dev, scene):
+    return [t.to(dev) for t in scene]
+
+
+@pytest.mark.parametrize("odds,fields", [(False, False), (True, False), (True, True)])
+def test_moment_span_boundary(dev, odds, fields):
+    H = W = 256
+    scene = span_scene(6000, H, W, seed=71)
+    sp = spans(np_(scene[0][0]), np_(activate_scale(scene[1])[0]), np_(scene[5][0]), H, W)
+    # the scene straddles the limit: many splats on either side of it within the window
+    assert np.mean((sp > 6) & (sp <= MOMENT_SPAN)) > 0.15 and np.mean((sp > MOMENT_SPAN) & (sp < 10)) > 0.15
+    run_case(*on(dev, scene), H, W, 8, odds, fields, seed=72)
+
+
+@pytest.mark.parametrize("odds", [False, True])
+def test_moment_span_boundary_octave(dev, odds):
+    H = W = 256
+    scene = span_scene(6000, H, W, seed=73)
+    lv = _lib.SplatLevels(1, 6, 8.0, 0, 0, 0)
+    run_levels(*on(dev, scene), H, W, 8, lv, odds, seed=74)
+
+
+@pytest.mark.parametrize("odds,fields", [(False, False), (True, True)])
+def test_subpixel_splats(dev, odds, fields):
+    """Splats of 0.05 to 0.35 px (spans of 8.5 to 80 over a tile: the direct form), mixed with ordinary ones."""
+    H = W = 128
+    scene = span_scene(3000, H, W, seed=75, lo=8.5, hi=80.0, frac=0.7)
+    run_case(*on(dev, scene), H, W, 8, odds, fields, seed=76)
+
+
+@pytest.mark.parametrize("TILE", [4, 16])
+def test_moment_span_other_tiles(dev, TILE):
+    """The span limit over 4 x 4 and 16 x 16 tiles (the same scenes give other spans there)."""
+    H = W = 256
+    scene = span_scene(5000, H, W, seed=77 + TILE, lo=5.0 * 7 / (TILE - 1), hi=11.0 * 7 / (TILE - 1))
+    run_case(*on(dev, scene), H, W, TILE, False, False, seed=78)
+    run_case(*on(dev, scene), H, W, TILE, True, True, seed=79)
+
+
+@pytest.mark.parametrize("odds", [False, True])
+def test_c2_octave_per_splat(dev, odds):
+    """The benchmark frame (768 x 768, 92,160 splats) through the octave render, every splat's gradients."""
+    s = synth.config("c2").to(dev)
+    run_levels(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.theta, s.H, s.W, 8, _lib.SplatLevels(1, 6, 8.0, 0, 0, 0),
+               odds, seed=80)

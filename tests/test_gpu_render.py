@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, np_, random_scene, rel_err
+from _gpu_util import check_per_splat
 from gaussian_splat_encoder import synth
 from oracle import c_oracle
 
@@ -16,9 +17,11 @@ def oracle_pairs(mu, sc, H, W, TILE, cutoff=3.0):
     return c_oracle.build_tiles(np_(mu[0]), np_(sc[0]), H, W, TILE, cutoff)
 
 
-def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True):
-    """Forward (and backward) of one batch against the C oracle over the oracle's pair list. Returns the
-    device gradients by name and the oracle's (None without the backward)."""
+def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True, per_splat=True):
+    """Forward (and backward) of one batch against the C oracle over the oracle's pair list. Gradients are held
+    to GRAD_REL_TOL of each tensor's largest magnitude and, with per_splat, every component of every splat to
+    PER_SPLAT_TOL of that splat's own scale for it (the oracle's 'mag'). Returns the device gradients by name
+    and the oracle's (None without the backward)."""
     dev = mu.device
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
@@ -62,7 +65,10 @@ def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bw
         r = gref[name]
         e = rel_err(np_(got[0]), r)
         assert e <= GRAD_REL_TOL, f"{name}: rel {e:.2e}"
-    return dict(zip(names, grads)), gref
+    got = dict(zip(names, grads))
+    if per_splat:
+        check_per_splat(got, gref)
+    return got, gref
 
 
 @pytest.mark.parametrize("odds", [False, True])

@@ -1,11 +1,14 @@
-"""The backward's negligible-pair rule against near-transparent splats, on the CPU oracle.
+"""The backward's negligible-pair rule, on the CPU oracle.
 
-The per-tile backward gives a pair a zero record when the pair's contribution is negligible at every pixel of
-the tile. The opacity gradient g_op = sum da * falloff (render_triton.py:697-698) carries no opacity factor, so
-the rule must look at the falloff alone: a rule on opacity * falloff drops the far tiles of near-transparent
-splats from their opacity gradient. Here both rules are planted in the float64 C oracle (the dropped pairs
-are removed from its pair list) and held to the per-splat check of the GPU tests: the falloff rule passes
-it, the opacity * falloff rule fails it by orders of magnitude.
+The per-tile backward gives a pair a zero record when the pair's falloff stays below 2^-30 of the splat's falloff
+at the pixel centre nearest its centre, at every pixel of the tile. Two alternatives are planted in the float64 C
+oracle (the dropped pairs are removed from its pair list) and held to the per-splat checks of the GPU tests:
+* near-transparent splats: the opacity gradient g_op = sum da * falloff (render_triton.py:697-698) carries no
+  opacity factor, so the rule must look at the falloff alone: a rule on opacity * falloff drops the far tiles of
+  near-transparent splats from their opacity gradient;
+* splats far smaller than a pixel: their best pixel may reach only 2^-20, and the scale gradient sum q u^2 weighs
+  far pixels by u^2, so an absolute cut at 2^-30 drops terms worth 1e-3 of such a splat's scale gradient, where
+  the relative cut keeps every splat's gradients within 1e-7 of its own scale.
 """
 
 import numpy as np
@@ -15,7 +18,8 @@ from _scenes import low_opacity_scene, per_splat_op_err
 from oracle import c_oracle
 from oracle import render_ref as R
 
-CULL_LOG2 = 30.0   # the backward's bound: falloff (or op * falloff) below 2^-30 at every pixel of the tile
+CULL_LOG2 = 30.0   # the backward's bound: falloff below 2^-30 of the splat's nearest-pixel falloff, over the tile
+KWHITEN2 = 0.5 / np.log(2.0)   # m = KWHITEN2 * maha: falloff exp(-maha / 2) = 2^-m
 
 
 def tile_max_falloff(mu, sc, th, gid, st, H, W, TILE):
@@ -35,6 +39,17 @@ def tile_max_falloff(mu, sc, th, gid, st, H, W, TILE):
     ry, rx = c * dy + s * dx, -s * dy + c * dx
     maha = (ry / sc[g, 0:1]) ** 2 + (rx / sc[g, 1:2]) ** 2
     return np.where(inside, np.exp(-0.5 * maha), 0.0).max(axis=1)
+
+
+def near_pixel_falloff(mu, sc, th, H, W):
+    """Per splat, the float64 falloff at the centre of the canvas pixel that holds its centre (clamped to the
+    canvas): the reference of the relative cut."""
+    iy = np.clip(np.floor(mu[:, 0] * H), 0, H - 1)
+    ix = np.clip(np.floor(mu[:, 1] * W), 0, W - 1)
+    dy, dx = (iy + 0.5) / H - mu[:, 0], (ix + 0.5) / W - mu[:, 1]
+    c, s = np.cos(th), np.sin(th)
+    ry, rx = c * dy + s * dx, -s * dy + c * dx
+    return np.exp(-0.5 * ((ry / sc[:, 0]) ** 2 + (rx / sc[:, 1]) ** 2))
 
 
 def drop_pairs(gid, st, drop):
@@ -63,9 +78,10 @@ def test_falloff_rule_keeps_opacity_gradient(odds):
         return c_oracle.bwd_cull(*args, gid_, st_, H, W, 8, odds=odds, fields=True, **ups)
 
     full = g_op(gid, st)
-    fmax = tile_max_falloff(mu.astype(np.float64), sc.astype(np.float64), th.astype(np.float64), gid, st, H, W, 8)
-    thr = 2.0 ** -CULL_LOG2
+    m64 = [x.astype(np.float64) for x in (mu, sc, th)]
+    fmax = tile_max_falloff(*m64, gid, st, H, W, 8)
     tile_of = np.repeat(np.arange(len(st) - 1), np.diff(st))
+    thr = 2.0 ** -CULL_LOG2 * near_pixel_falloff(*m64, H, W)[gid[:len(tile_of)]]
     opp = op[gid[:len(tile_of)]].astype(np.float64)
     falloff_rule = drop_pairs(gid, st, fmax < thr)
     product_rule = drop_pairs(gid, st, opp * fmax < thr)
@@ -101,3 +117,29 @@ def test_op_scale_bounds_the_gradient():
     r1 = c_oracle.bwd_cull(mu[:1], sc[:1], th[:1], op[:1] * 0 + 0.3, col[:1], *one, H, W, 8, fields=True,
                            dslog=-np.ones(H * W), dsa=z, dsac=np.zeros((H * W, 3)))
     assert r1["op"][0] > 0 and abs(r1["op"][0] - r1["op_scale"][0]) <= 1e-12 * r1["op_scale"][0]
+
+
+def test_relative_cut_keeps_subpixel_splats():
+    """Splats of 0.05 to 0.35 px among ordinary ones: the absolute cut (falloff below 2^-30 over the tile) fails the
+    per-splat check on their scale gradients, the relative cut passes it."""
+    from _scenes import per_splat_errors
+    from _scenes import span_scene
+    H = W = 96
+    mu, ls, col, op, bg, th = span_scene(1500, H, W, seed=75, lo=8.5, hi=80.0, frac=0.7)
+    mu, col, op, th = mu[0].numpy(), col[0].numpy(), op[0].numpy(), th[0].numpy()
+    sc = R.activate_scale(ls[0]).numpy()
+    gid, st = c_oracle.build_tiles(mu, sc, H, W, 8)
+    rng = np.random.default_rng(7)
+    ups = dict(dslog=rng.standard_normal(H * W), dsa=rng.standard_normal(H * W),
+               dsac=rng.standard_normal((H * W, 3)))
+    args = (mu, sc, th, op, col)
+    full = c_oracle.bwd_cull(*args, gid, st, H, W, 8, fields=True, **ups)
+    m64 = [x.astype(np.float64) for x in (mu, sc, th)]
+    fmax = tile_max_falloff(*m64, gid, st, H, W, 8)
+    n = len(fmax)
+    rel = drop_pairs(gid, st, fmax < 2.0 ** -CULL_LOG2 * near_pixel_falloff(*m64, H, W)[gid[:n]])
+    ab = drop_pairs(gid, st, fmax < 2.0 ** -CULL_LOG2)
+    worst = lambda r: max(e for e, _ in per_splat_errors({k: r[k] for k in ("mu", "scale", "col", "op", "theta")},
+                                                         full).values())
+    assert worst(c_oracle.bwd_cull(*args, *rel, H, W, 8, fields=True, **ups)) <= 1e-7
+    assert worst(c_oracle.bwd_cull(*args, *ab, H, W, 8, fields=True, **ups)) > 1e-4

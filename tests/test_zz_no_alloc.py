@@ -2,8 +2,10 @@
 in the library's own device scratch), called through the C-ABI and checked bit for bit against splat_bin
 (the same binning with caller-provided workspaces): the decoded records, rects, offsets, totals, the pair list
 and tile starts, and both pair maps. Two calls in a row, the second with a smaller input, so a stale scratch
-from the first call cannot go unseen; then the limits (a pair capacity beyond the scratch, a count beyond the
-caller's buffers)."""
+from the first call cannot go unseen; calls from two threads on two streams at once (the library orders them on
+the device); then the limits (a pair capacity beyond the scratch, a count beyond the caller's buffers)."""
+
+import threading
 
 import numpy as np
 import pytest
@@ -37,7 +39,7 @@ def noalloc_bins(mu, ls, col, op, th, H, W, lv, cap, max_pairs=-1):
                                3.0, lvr, _lib.FLAG_LOG_SCALE, max_pairs, p(out["rec"]), p(out["rect"]), p(out["off"]),
                                p(out["info"]), info_host.data_ptr(), cap, p(out["gid"]), p(out["starts"]),
                                p(out["psplat"]), p(out["pq"]), _lib.stream_ptr(dev))
-    torch.cuda.synchronize()
+    torch.cuda.current_stream(dev).synchronize()
     return rc, out, info_host.numpy()[:2 + L].copy()
 
 
@@ -97,3 +99,36 @@ def test_noalloc_limits(dev):
     rc, got, info = noalloc_bins(*args, None, tot, max_pairs=tot)
     _lib.check(rc, "splat_bin_noalloc")
     assert_same(ref, got, info)
+
+
+def test_noalloc_two_threads_two_streams(dev):
+    """Two threads, each on a stream of its own, bin different scenes through the one scratch at the same time, six
+    times each: every call bit for bit equal to splat_bin's result (the library serialises the calls' kernels on
+    the device, so neither sees the other's workspace)."""
+    s = synth.config("c1").to(dev)
+    a = (s.mu, s.log_scale, s.color, s.opacity, s.theta, s.H, s.W)
+    mu, ls, col, op, _, th = random_scene(20000, 300, 200, seed=78, dev=dev, ls_mean_px=6.0, ls_std=1.0, margin=0.1)
+    b = (mu, ls, col, op, th, 300, 200)
+    refs = [(a, None, reference_bins(*a, None)), (b, _lib.SplatLevels(1, 6, 8.0, 0, 0, 0), None)]
+    refs[1] = (b, refs[1][1], reference_bins(*b, refs[1][1]))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(k):
+        args, lv, ref = refs[k]
+        try:
+            with torch.cuda.stream(torch.cuda.Stream(dev)):
+                for it in range(6):
+                    rc, got, info = noalloc_bins(*args, lv, ref.tot_b[0] + 10)
+                    _lib.check(rc, "splat_bin_noalloc")
+                    assert_same(ref, got, info)
+        except Exception as e:   # reported by the main thread
+            errors.append(f"thread {k}: {e!r}")
+
+    print("noalloc: two threads on two streams", flush=True)
+    ts = [threading.Thread(target=worker, args=(k,)) for k in (0, 1)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
