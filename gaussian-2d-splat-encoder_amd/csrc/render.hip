@@ -75,13 +75,17 @@ __device__ __forceinline__ float uniform_f(float x) {
 }
 
 // Whitened offsets (u, v) of the pixel centre (py0, px0) from a splat with centre (gy, gx) and rotation rows
-// (A, B), (Cc, D), evaluated in float64 and rounded once. A tile's pixels add their own offsets from the tile's
-// first pixel centre to these, so their rounding error is shared by the whole tile; with one rounding it stays
-// at half an ulp of the result, below the rounding the per-pixel form makes at every pixel.
+// (A, B), (Cc, D). A tile's pixels add their own offsets from the tile's first pixel centre to these, so their
+// rounding error is shared by the whole tile. The float32 differences py0 - gy, px0 - gx are exact wherever the
+// two lie within a factor of two (Sterbenz), which holds for every tile a splat reaches away from the canvas'
+// first rows and columns (there the values are small and so is their rounding); each product's rounding error is
+// recovered exactly by an fma and added back, so the result is within about one ulp of the exact offsets (a
+// float64 evaluation rounded once: half an ulp), at a third of the instructions.
 __device__ __forceinline__ float2 offsets_at(float py0, float px0, float gy, float gx, float A, float B, float Cc,
                                              float D) {
-  const double dy = (double)py0 - (double)gy, dx = (double)px0 - (double)gx;
-  return make_float2((float)fma((double)A, dy, (double)B * dx), (float)fma((double)Cc, dy, (double)D * dx));
+  const float dy = py0 - gy, dx = px0 - gx;
+  const float pu = A * dy, pv = Cc * dy;
+  return make_float2(fmaf(B, dx, pu) + fmaf(A, dy, -pu), fmaf(D, dx, pv) + fmaf(Cc, dy, -pv));
 }
 
 // One pixel-pair of the per-tile forward: (u0, v0) are the pair's whitened offsets at the tile's first pixel
@@ -262,6 +266,22 @@ __device__ __forceinline__ TileAt split_item(const LevelTable& L, const SplitTab
   return tile_of(L, L.tbase[l] + j / s, l);
 }
 
+// Pixel centres (render_triton.py:455-456, (i + 0.5) / size in float32) of a tile: lane j < TILE divides for row j
+// and lane TILE + j for column j, one division for the wave, and each lane takes its own row's and column's by
+// shuffles; l is the lane's pixel within the tile, (py0, px0) the tile's first pixel centre.
+template <int TILE>
+__device__ __forceinline__ void tile_centres(const TileAt& ta, int l, int lane, float& py, float& px, float& py0,
+                                             float& px0) {
+  static_assert(2 * TILE <= 64, "one lane per row and column");
+  const bool row = lane < TILE;
+  const int i = row ? ta.ty * TILE + lane : ta.tx * TILE + (lane - TILE);
+  const float c = ((float)i + 0.5f) / (float)(row ? ta.H : ta.W);
+  py = __shfl(c, (l / TILE) % TILE, 64);
+  px = __shfl(c, TILE + l % TILE, 64);
+  py0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c)));
+  px0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), TILE));
+}
+
 // Forward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
 // FIELDS: raw sums into the packed per-level fields slog/sa/sac (slot pbase[l] + pixel).
 // Composite (level 0): out, T, asum, fg; with UPS the coarse levels' packed fields (inputs slog/sa/sac) are
@@ -292,14 +312,8 @@ __global__ __launch_bounds__((fwd_threads<TILE, S>())) void k_fwd_cull(
   const int wv = S > 1 ? wid : 0;
   const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
   const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
-  const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
-  const float px = ((float)xp + 0.5f) / (float)ta.W;
-  // the tile's first pixel centre: lane 0's own when every wave starts at the tile's first pixel
-  constexpr bool kLane0First = S > 1 || tile_threads(TILE) == 64;
-  const float py0 = kLane0First ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(py)))
-                                : ((float)(ta.ty * TILE) + 0.5f) / (float)ta.H;
-  const float px0 = kLane0First ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(px)))
-                                : ((float)(ta.tx * TILE) + 0.5f) / (float)ta.W;
+  float py, px, py0, px0;   // the lane's pixel centre and the tile's first pixel centre
+  tile_centres<TILE>(ta, l, lane, py, px, py0, px0);
   int g0 = starts[ta.t], g1 = starts[ta.t + 1];
   if (S > 1) {
     const int chunk = ((g1 - g0 + S - 1) / S + 3) & ~3;

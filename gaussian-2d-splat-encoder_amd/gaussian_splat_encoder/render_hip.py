@@ -45,17 +45,22 @@ def _batch_args(mu, log_scale, color, opacity, bg, theta):
     image b's data at b times each tensor's batch stride, so every tensor must hold B images. A bg of shape
     [1,C] is broadcast over the batch (the composite of render_triton.py:921, :980 broadcasts it; autograd sums
     its gradient back to [1,C])."""
-    if color.dim() != 3:
-        raise ValueError(f"color must be [B,N,C], got {tuple(color.shape)}")
-    B, N, C = color.shape
-    want = {"mu": (mu, (B, N, 2)), "log_scale": (log_scale, (B, N, 2)), "opacity": (opacity, (B, N)),
-            "theta": (theta, (B, N))}
-    for name, (t, shape) in want.items():
-        if t is not None and tuple(t.shape) != shape:
-            raise ValueError(f"{name} must be {list(shape)} for color {list(color.shape)}, got {list(t.shape)}")
-    if bg.dim() != 2 or bg.shape[1] != C or bg.shape[0] not in (1, B):
-        raise ValueError(f"bg must be [{B},{C}] or [1,{C}] for color {list(color.shape)}, got {list(bg.shape)}")
-    return bg.expand(B, C) if bg.shape[0] != B else bg
+    cs = color.shape
+    if len(cs) != 3:
+        raise ValueError(f"color must be [B,N,C], got {tuple(cs)}")
+    B, N, C = cs
+    bn2, bn = (B, N, 2), (B, N)
+    if mu.shape != bn2 or log_scale.shape != bn2 or opacity.shape != bn or (theta is not None and theta.shape != bn):
+        for name, t, shape in (("mu", mu, bn2), ("log_scale", log_scale, bn2), ("opacity", opacity, bn),
+                               ("theta", theta, bn)):
+            if t is not None and t.shape != shape:
+                raise ValueError(f"{name} must be {list(shape)} for color {list(cs)}, got {list(t.shape)}")
+    bs = bg.shape
+    if bs == (B, C):
+        return bg
+    if bs == (1, C):
+        return bg.expand(B, C)
+    raise ValueError(f"bg must be [{B},{C}] or [1,{C}] for color {list(cs)}, got {list(bs)}")
 
 
 def _f32(t):
@@ -547,8 +552,9 @@ def _composite_buffers(B, P, C, dev):
 
 
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
-                  with_maps=True, scale_is_log=False):
-    """Composite forward (render_triton.py:538-567): out [B,P,C], (T, asum, fg), bins."""
+                  with_maps=True, scale_is_log=False, plan=None):
+    """Composite forward (render_triton.py:538-567): out [B,P,C], (T, asum, fg), bins. plan: a _BwdPlan to
+    prepare for the backward (its buffers are allocated while the pair count is read back)."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
@@ -571,11 +577,83 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
 
     if bins.pending is not None:   # queued on the speculative pair list before the count is read
         launch([_speculated_levels(bins)[0]])
+        if plan is not None:         # the backward's buffers, allocated while the GPU works towards the count
+            plan.allocate(bins, B, N, C, dev, lib, bins.pending.cap)
         if _finish(bins):
             launch(bins.tot_b)
     else:
         launch(bins.tot_b)
+    if plan is not None:
+        plan.bind(bins, B, N, C, dev, lib, stream, flags, (bgf, T, asum, fg))
     return out, (T, asum, fg), bins
+
+
+class _BwdPlan:
+    """The backward of a culled composite render prepared by its forward: the gradient outputs, the per-pair sums
+    and per-tile background partials (allocated while the forward waits for the pair count), and the argument lists
+    of the two backward launches per image, complete but for the upstream gradient's pointer. The backward then runs
+    two C-ABI calls per image (render_triton.py:723-765 in two kernels)."""
+
+    __slots__ = ("grads", "sums", "bg_part", "cap", "bwd_head", "bwd_tail", "red_args", "lsc", "has_th", "keep")
+
+    def __init__(self, has_th, lsc=None):
+        self.has_th = has_th
+        self.lsc = _f32(lsc)   # the raw log-scales as the reduction reads them (kept alive here)
+        self.cap = -1
+        self.sums = self.bg_part = None
+
+    def allocate(self, bins, B, N, C, dev, lib, cap):
+        self.grads = _grads_bg_out(B, N, C, dev, self.has_th)
+        ns = (lib.splat_pair_sums_bytes(max(cap, 1)) // 4 + 3) & ~3   # partials start 16-byte aligned
+        self.sums, self.bg_part = torch.empty(B * ns + C * bins.ntiles0, device=dev).split_with_sizes(
+            (B * ns, C * bins.ntiles0))
+        self.cap = cap
+
+    def bind(self, bins, B, N, C, dev, lib, stream, flags, comp):
+        tots = bins.tot_b
+        if self.sums is None or max(tots) > self.cap:
+            self.allocate(bins, B, N, C, dev, lib, max(tots))
+        ns = self.sums.numel() // max(B, 1)
+        g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
+        bgf, T, asum, fg = comp
+        self.keep = bgf   # the kernels read the background through its pointer
+        lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
+        sums0, bgp = self.sums.data_ptr(), self.bg_part.data_ptr()
+        self.bwd_head, self.bwd_tail, self.red_args = [], [], []
+        for b in range(B):
+            sb = sums0 + 4 * ns * b
+            self.bwd_head.append((bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), bins.p(b, "pq"), tots[b], C,
+                                  bins.H, bins.W, bins.TILE, flags | _wide(bins.TILE, bins.nt, tots[b]), lvr, 0, 1, 1,
+                                  _bptr(bgf, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b)))
+            self.bwd_tail.append((None, None, None, sb, bgp, stream))
+            sl = lambda t: None if N == 0 else _bptr(t, b)
+            self.red_args.append((bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None, None, tots[b], N, C,
+                                  sb, bgp, bins.ntiles0, sl(self.lsc), sl(g_mu), sl(g_scale), sl(g_th), sl(g_op),
+                                  sl(g_col), _bptr(g_bg, b), stream))
+
+    def run(self, lib, grad_out, H, W, C):
+        """The two launches per image with grad_out [B,C,H,W]; returns the gradients (the plan then holds none)."""
+        B = grad_out.shape[0]
+        img = H * W * C
+        if grad_out.dtype is torch.float32 and grad_out.stride() == (img, 1, W * C, C):
+            g0 = grad_out.data_ptr()     # the image's own [B,H,W,C] layout: no copy
+        else:
+            go = grad_out.permute(0, 2, 3, 1).contiguous().float()
+            g0 = go.data_ptr()
+        for b in range(B):
+            ev = kernel_timer.record("bwd")
+            try:
+                check(lib.splat_render_bwd(*self.bwd_head[b], g0 + 4 * img * b, *self.bwd_tail[b]), "splat_render_bwd")
+            finally:
+                kernel_timer.close("bwd", ev)
+            ev = kernel_timer.record("reduce")
+            try:
+                check(lib.splat_reduce_pairs(*self.red_args[b]), "splat_reduce_pairs")
+            finally:
+                kernel_timer.close("reduce", ev)
+        g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
+        self.grads = self.sums = self.bg_part = self.keep = None
+        return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
 def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
@@ -802,11 +880,15 @@ class _AlphaRenderCull(torch.autograd.Function):
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=False, scale_is_log=False):
         B, N, C = color.shape
+        grad = any(ctx.needs_input_grad[:6])
+        plan = _BwdPlan(theta is not None, scale if scale_is_log else None) if grad and N > 0 else None
         out, (T, asum, fg), bins = _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds=odds,
-                                                 with_maps=any(ctx.needs_input_grad[:6]), scale_is_log=scale_is_log)
+                                                 with_maps=grad, scale_is_log=scale_is_log, plan=plan)
         ctx.meta = (B, N, C, mu.device, theta is not None, H, W, TILE, odds, scale_is_log)
         ctx.tiles = bins
         ctx.fwd = (T, asum, fg)
+        ctx.plan = plan
+        # the backward reads bg and the raw log-scales through the plan's pointers: keep them alive
         if scale_is_log:
             ctx.save_for_backward(bg, scale)
         else:
@@ -816,6 +898,10 @@ class _AlphaRenderCull(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         B, N, C, dev, has_th, H, W, TILE, odds, scale_is_log = ctx.meta
+        plan, ctx.plan = ctx.plan, None
+        if plan is not None and plan.grads is not None:
+            g_mu, g_scale, g_col, g_op, g_bg, g_th = plan.run(_lib.load(), grad_out, H, W, C)
+            return g_mu, g_scale, g_col, g_op, g_bg, g_th, None, None, None, None, None, None
         saved = ctx.saved_tensors
         bg = saved[0]
         lsc = saved[1] if scale_is_log else None
