@@ -53,6 +53,31 @@ def algorithmic_bytes_bwd(N, tot, P):
     return 72 * N + 4 * tot + 32 * P
 
 
+def ppe_levels(bins, TILE=8):
+    """Pixel-pair evaluations of a binning over every level (octave / coarse-fine renders): per level, the sum over
+    its tiles of pairs x the tile's pixels on that level's canvas."""
+    if bins.geom is None:
+        return ppe_of(bins, bins.H, bins.W, TILE)
+    st = bins.starts_b[0].long()
+    cnt = (st[1:] - st[:-1]).double()
+    total = 0.0
+    for l, (Hl, Wl, ntx, tb, _) in enumerate(bins.geom):
+        te = bins.geom[l + 1][3] if l + 1 < len(bins.geom) else bins.nt
+        t = torch.arange(te - tb, device=cnt.device)
+        ty, tx = t // ntx, t % ntx
+        ph = torch.clamp(Hl - ty * TILE, max=TILE).double()
+        pw = torch.clamp(Wl - tx * TILE, max=TILE).double()
+        total += float((cnt[tb:te] * ph * pw).sum().item())
+    return total
+
+
+def stage_rate(ppe, flops_per_ppe, ms):
+    """A render stage's algorithmic rate: flops of its pixel-pair evaluations over the stage's whole time (binning
+    and every launch included), and that as a fraction of the fp32 vector peak."""
+    tf = flops_per_ppe * ppe / (ms * 1e-3) / 1e12
+    return {"ppe": int(ppe), "alg_tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_FP32_TFLOPS, 4)}
+
+
 def ppe_of(bins, H, W, TILE=8):
     """Pixel-pair evaluations: sum over tiles of pairs x in-canvas pixels of the tile."""
     st = bins.starts_b[0].long()
@@ -298,8 +323,15 @@ def stress_c4(steps, warmup, odds):
     with torch.no_grad():
         sc = torch.nn.functional.softplus(s.log_scale) + 1e-4
         bins = RH._bin(s.mu, sc, s.color, s.opacity, s.theta, H, W, 8, 3.0, with_maps=False)
+        obins = RH._bin(s.mu, sc, s.color, s.opacity, s.theta, H, W, 8, 3.0, with_maps=False,
+                        lv=RH._octave_levels(H, W, 8.0, 6))
     res["pairs"] = bins.tot_b[0]
-    del bins, leaves, s
+    ppe, oppe = ppe_of(bins, H, W), ppe_levels(obins)
+    ff, fb = FLOPS_FWD[odds], FLOPS_FWD[odds] + FLOPS_BWD[odds]
+    res["stage_roofline"] = {"fwd": stage_rate(ppe, ff, res["fwd_ms"]), "fwd_bwd": stage_rate(ppe, fb, res["fwd_bwd_ms"]),
+                             "octave_fwd": stage_rate(oppe, ff, res["octave_fwd_ms"]),
+                             "octave_fwd_bwd": stage_rate(oppe, fb, res["octave_fwd_bwd_ms"])}
+    del bins, obins, leaves, s
     torch.cuda.empty_cache()
     return res
 
@@ -339,9 +371,108 @@ def e2e_c3(steps, warmup):
     res = {"workload": "768x768 procedural card -> random-init 833,107-parameter adaptive encoder (d=256) -> "
                        "odds octave renders (384^2 coarse, 768^2 full); configs[3]",
            "splats": int(out["mu"].shape[1]), "stages_ms": {k: round(med(v), 4) for k, v in spans.items()}}
+    # the two renders' pixel-pair evaluations: one more frame with the renders' arguments captured
+    from gaussian_splat_encoder import efficient_encoder as EE
+    calls = []
+    orig = EE.render_alpha_octave
+
+    def capture(mu, log_scale, color, opacity, bg, H, W, theta=None, **kw):
+        calls.append((mu, log_scale, color, opacity, H, W, theta))
+        return orig(mu, log_scale, color, opacity, bg, H, W, theta, **kw)
+
+    EE.render_alpha_octave = capture
+    try:
+        with torch.inference_mode():
+            out = enc(x)
+            capture(out["mu"], out["log_scale"], out["color"], out["opacity"], out["bg"], 768, 768, out["theta"],
+                    odds=enc.odds)
+    finally:
+        EE.render_alpha_octave = orig
+    rates = {}
+    with torch.inference_mode():
+        for name, (mu, ls, col, op, H, W, th) in zip(("coarse_render", "full_render"), calls[-2:]):
+            sc = torch.nn.functional.softplus(ls.float()) + 1e-4
+            bins = RH._bin(mu.float(), sc, col.float(), op.float(), None if th is None else th.float(), H, W, 8, 3.0,
+                           with_maps=False, lv=RH._octave_levels(H, W, 8.0, 6))
+            rates[name] = stage_rate(ppe_levels(bins), FLOPS_FWD[bool(enc.odds)], res["stages_ms"][name])
+    res["stage_roofline"] = rates
     del enc, out, x
     torch.cuda.empty_cache()
     return res
+
+
+def pair_classes(name, TILE=8, cutoff=3.0):
+    """How the backward's per-tile kernel (k_bwd_cull) classes the pairs of a configuration's single-res render, and
+    the passes its lanes run: the kernel's tests restated in float64 numpy on the device's own pair lists.
+    negligible: falloff below 2^-30 of the splat's falloff at the pixel centre nearest its centre, at every pixel
+    centre of the tile (a zero record); near-opaque: op * falloff may exceed 0.99 in the tile (one careful pass per
+    pair, lane = pixel); direct: whitened half-span over the tile above 8 (the direct form); moment: the rest.
+    Passes: per tile, the moment pairs and the direct pairs each run in passes of up to 64 (lane = pair); a last
+    pass of r < 64 pairs gives each pair Lp lanes (the largest power of two with r Lp <= 64)."""
+    s = synth.config(name)
+    dev = torch.device("cuda:0")
+    mu, ls = s.mu.to(dev), s.log_scale.to(dev)
+    sc = torch.nn.functional.softplus(ls) + 1e-4
+    gid_b, st_b, ntx, nt = RH._build_tiles(mu, sc, s.H, s.W, TILE, cutoff)
+    gid = gid_b[0].cpu().numpy().astype(np.int64)
+    st = st_b[0].cpu().numpy().astype(np.int64)
+    H, W = s.H, s.W
+    m64 = mu[0].cpu().double().numpy()
+    s64 = sc[0].cpu().double().numpy()
+    th = s.theta[0].double().numpy()
+    op = s.opacity[0].double().numpy()
+    tot = int(st[-1])
+    tile = np.repeat(np.arange(nt), np.diff(st))
+    g = gid[:tot]
+    ty, tx = tile // ntx, tile % ntx
+    c32 = lambda i, n: ((i.astype(np.float32) + np.float32(0.5)) / np.float32(n)).astype(np.float64)
+    py0, py1 = c32(ty * TILE, H), c32(ty * TILE + TILE - 1, H)
+    px0, px1 = c32(tx * TILE, W), c32(tx * TILE + TILE - 1, W)
+    k = np.sqrt(0.5 / np.log(2.0))
+    cs, sn = np.cos(th)[g], np.sin(th)[g]
+    sy, sx = s64[g, 0], s64[g, 1]
+    A, B, Cc, D = k * cs / sy, k * sn / sy, -k * sn / sx, k * cs / sx
+    gy, gx = m64[g, 0], m64[g, 1]
+    u0 = A * (py0 - gy) + B * (px0 - gx)
+    v0 = Cc * (py0 - gy) + D * (px0 - gx)
+    Ly, Lx = py1 - py0, px1 - px0
+
+    def interval_dist(c0, a, b):
+        lo = c0 + np.minimum(a, 0) + np.minimum(b, 0)
+        hi = c0 + np.maximum(a, 0) + np.maximum(b, 0)
+        return np.maximum(np.maximum(lo, -hi), 0)
+
+    du, dv = interval_dist(u0, A * Ly, B * Lx), interval_dist(v0, Cc * Ly, D * Lx)
+    box_m = du * du + dv * dv
+    ny = (np.clip(np.floor(gy * H), 0, H - 1) + 0.5) / H - gy
+    nx = (np.clip(np.floor(gx * W), 0, W - 1) + 0.5) / W - gx
+    un, vn = A * ny + B * nx, Cc * ny + D * nx
+    negl = box_m > 30.0 + (un * un + vn * vn)
+    dy = np.maximum(np.maximum(py0 - gy, gy - py1), 0)
+    dx = np.maximum(np.maximum(px0 - gx, gx - px1), 0)
+    lop = np.log2(np.maximum(op[g], 1e-45))
+    near = ~negl & (op[g] > 0.99) & ((dy * dy + dx * dx) * k * k <
+                                     np.maximum(sy, sx) ** 2 * (lop - np.log2(0.99) + 1e-3))
+    cy, cx = 0.5 * Ly, 0.5 * Lx
+    span = np.maximum(np.abs(A) * cy + np.abs(B) * cx, np.abs(Cc) * cy + np.abs(D) * cx)
+    direct = ~negl & ~near & (span > 8.0)
+    moment = ~negl & ~near & ~direct
+    out = {"pairs": tot, "share": {c: round(float(m.mean()), 5) for c, m in
+                                   (("negligible", negl), ("near_opaque", near), ("direct", direct), ("moment", moment))}}
+    # passes per tile (the kernel's queues: whole passes of 64, then the rest)
+    lane_pairs = 0
+    pass_time = 0.0
+    for m in (moment, direct):
+        n = np.bincount(tile[m], minlength=nt)
+        full, r = n // 64, n % 64
+        lp = np.ones_like(r)
+        for _ in range(6):
+            lp = np.where((r * lp * 2 <= 64) & (lp * 2 <= TILE * TILE), lp * 2, lp)
+        pass_time += float(full.sum() + np.where(r > 0, 1.0 / np.where(r > 0, lp, 1), 0).sum())
+        lane_pairs += int(n.sum())
+    out["row_loop_passes"] = round(pass_time, 1)
+    out["lane_use_in_passes"] = round(lane_pairs / max(64 * pass_time, 1), 4)
+    return out
 
 
 def main():
@@ -356,6 +487,8 @@ def main():
     ap.add_argument("--only", choices=("c3", "c4"), default=None,
                     help="run only the encoder end-to-end frame (c3) or the 2048x2048 stress set (c4) and print its "
                          "JSON object (for profiling one configuration)")
+    ap.add_argument("--pair-classes", action="store_true",
+                    help="only print how the backward classes the pairs of C2 and C4 (shares, passes) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a MIB-MiB copy kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -368,6 +501,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.pair_classes:
+        print(json.dumps({"pair_classes": {c: pair_classes(c) for c in ("c2", "c4")}}), flush=True)
         return
     if args.only == "c3":
         print(json.dumps({"c3": e2e_c3(max(10, args.steps // 2), max(3, args.warmup // 2))}), flush=True)
