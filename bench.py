@@ -169,21 +169,29 @@ def kernel_times(leaves, H, W, odds, reps):
         "bwd": span(lambda: RH._render_bwd(lib, bins, 0, C, flags, (0, 1), 1, up, sums, bg_part, stream)),
         "reduce": span(lambda: RH._reduce(lib, bins, 0, C, sums, bg_part, grads, g_bg[0], stream)),
     }
-    # the binning's kernels alone: count phase then pair phase for the known pair count, back to back (no host
-    # read between them), into the frame's own binning buffers
+    # the binning's kernels alone, as a render queues them: splat_bin with pair buffers for the known pair count
+    # (the count phase, then the pair phase queued before the count is read) and a deferred read, so the calls
+    # queue back to back with no host read between them; each call gets its own pinned totals, read afterwards
     lsf = ls.contiguous()
     N, tot = mu.shape[1], bins.tot_b[0]
     blk, pb = bins.blocks[0], bins.pairs[0]
     thp = None if th is None else th.data_ptr()
+    infos = [torch.zeros(2 + RH._lib.MAX_LEVELS, dtype=torch.int64, pin_memory=True) for _ in range(reps + 3)]
+    queued = []
 
     def bin_kernels():
-        RH._lib.check(lib.splat_bin_count(mu.data_ptr(), lsf.data_ptr(), thp, op.data_ptr(), col.data_ptr(), C, N, H, W,
-                                          8, 3.0, None, RH.FLAG_LOG_SCALE, blk.ptr(0), blk.ptr(1), blk.ptr(2),
-                                          blk.ptr(3), blk.ptr(4), blk.nbytes(4), stream), "splat_bin_count")
-        RH._lib.check(lib.splat_bin_pairs(blk.ptr(1), blk.ptr(2), blk.ptr(4), N, H, W, 8, None, tot, pb.ptr(0), pb.ptr(1),
-                                          None, pb.ptr(2), pb.ptr(3), pb.nbytes(3), stream), "splat_bin_pairs")
+        info = infos[len(queued)]
+        RH._lib.check(lib.splat_bin(mu.data_ptr(), lsf.data_ptr(), thp, op.data_ptr(), col.data_ptr(), C, N, H, W, 8,
+                                    3.0, None, RH.FLAG_LOG_SCALE | RH._lib.FLAG_DEFER, -1, blk.ptr(0), blk.ptr(1),
+                                    blk.ptr(2), blk.ptr(3), info.data_ptr(), blk.ptr(4), blk.nbytes(4), tot, pb.ptr(0),
+                                    pb.ptr(1), None, pb.ptr(2) if bins.with_maps else None, pb.ptr(3), pb.nbytes(3),
+                                    stream), "splat_bin")
+        queued.append(info)
 
     ms["bin_kernels"] = span(bin_kernels)
+    for info in queued:
+        RH._lib.check(lib.splat_bin_finish(info.data_ptr(), blk.ptr(3), 1, -1, tot, stream), "splat_bin_finish")
+        assert int(info[0]) == tot
     RH.kernel_timer.enable(True)
     for _ in range(reps):
         RH._bin(mu, lsf, col, op, th, H, W, 8, 3.0, scale_is_log=True)

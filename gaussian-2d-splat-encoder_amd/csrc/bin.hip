@@ -1294,15 +1294,14 @@ __global__ __launch_bounds__(kRowThreads) void k_expand_row(LevelTable L, const 
       if (lane == 0) s_kc[k][wv] = __popcll(mk[k]);
     }
     __syncthreads();
-    if (t == 0) {   // exclusive prefix in (k, wave) order
-      int run = 0;
-      for (int k = 0; k < kRowItems; ++k)
-        for (int w = 0; w < kRowWaves; ++w) {
-          const int c = s_kc[k][w];
-          s_kc[k][w] = run;
-          run += c;
-        }
-      s_n = run;
+    if (wv == 0) {   // exclusive prefix in (k, wave) order: lane i < kMark takes entry (i / kRowWaves, i % kRowWaves)
+      constexpr int kMark = kRowItems * kRowWaves;
+      static_assert(kMark <= 64, "one lane per entry");
+      int* kc = &s_kc[0][0];
+      const int c = lane < kMark ? kc[lane] : 0;
+      const int inc = wave_incl_scan<int>(c, lane);
+      if (lane < kMark) kc[lane] = inc - c;
+      if (lane == kMark - 1) s_n = inc;
     }
     __syncthreads();
     return s_n;

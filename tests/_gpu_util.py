@@ -49,6 +49,7 @@ def check_per_splat(got, gref, tol=PER_SPLAT_TOL):
     worst = {k: f"{e:.2e} at splat {i // max(1, np.asarray(gref[k]).reshape(len(gref[k]), -1).shape[1])}"
              for k, (e, i) in errs.items() if e > tol}
     assert not worst, f"per-splat gradient errors above {tol:g} of the splat's scale: {worst}"
+    print("per-splat errors (of each splat's scale):", {k: f"{e:.2e}" for k, (e, _) in errs.items()}, flush=True)
     return {k: e for k, (e, _) in errs.items()}
 
 
