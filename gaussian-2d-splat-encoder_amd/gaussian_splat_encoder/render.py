@@ -30,7 +30,7 @@ def render_alpha_subsampled(mu, log_scale, color, opacity, bg, H, W, theta=None,
                             pixel_indices=None):
     """render.py:68-87: exact render at a pixel subsample. Returns (rendered [B,C,n_px], px_idx [B,n_px])."""
     from .params import activate_scale
-    from .render_hip import _AlphaRender
+    from .render_hip import MAX_CHANNELS, _AlphaRender
     B, N, C = color.shape
     device = mu.device
     total = H * W
@@ -45,7 +45,12 @@ def render_alpha_subsampled(mu, log_scale, color, opacity, bg, H, W, theta=None,
         py = ((px_idx[b] // W).to(torch.float32) + 0.5) / H
         px = ((px_idx[b] % W).to(torch.float32) + 0.5) / W
         th = theta[b:b + 1] if theta is not None else None
-        outs.append(_AlphaRender.apply(mu[b:b + 1], scale[b:b + 1], color[b:b + 1], opacity[b:b + 1], bg[b:b + 1],
-                                       th, py.contiguous(), px.contiguous()))
+        bgb = bg[b:b + 1] if bg.shape[0] > 1 else bg
+        # colour channels in chunks of at most MAX_CHANNELS (render_hip._channel_chunks): each chunk's pixels depend
+        # on its own channels only, and autograd adds the chunks' gradients of the shared parameters
+        outs.append(torch.cat([_AlphaRender.apply(mu[b:b + 1], scale[b:b + 1], color[b:b + 1, :, k:k + MAX_CHANNELS],
+                                                  opacity[b:b + 1], bgb[:, k:k + MAX_CHANNELS], th, py.contiguous(),
+                                                  px.contiguous())
+                               for k in range(0, C, MAX_CHANNELS)], dim=-1))
     rendered = torch.cat(outs, 0)                                      # [B, n_px, C]
     return rendered.permute(0, 2, 1), px_idx

@@ -1049,8 +1049,27 @@ def _scale_arg(log_scale):
     return activate_scale(log_scale), False
 
 
+MAX_CHANNELS = 4   # colour channels per launch: the kernels are instantiated for C = 1..4
+
+
+def _channel_chunks(render, color, bg):
+    """A render of C > MAX_CHANNELS colour channels (render_triton.py pads C to the next power of two and takes any
+    count) as renders of at most MAX_CHANNELS channels each, concatenated along the channel dimension of the image
+    (dim 1 of [B,C,H,W], or of [B,C,n] for pixel subsamples). Everything but the colour sums is independent of the
+    colour (pair lists, S_log, S_a), each channel's image depends on its own colour and background only, and the
+    backward is linear in the upstream gradient, so the chunks' images are the image's channels and autograd's sum of
+    the chunks' gradients of the shared parameters is their gradient. render(color_chunk, bg_chunk) renders one
+    chunk; `bg` is [B,C] or [1,C]. Each chunk bins the splats again (the pair lists are the same)."""
+    C = color.shape[-1]
+    return torch.cat([render(color[..., k:k + MAX_CHANNELS], bg[..., k:k + MAX_CHANNELS])
+                      for k in range(0, C, MAX_CHANNELS)], dim=1)
+
+
 def _apply_levels(mu, log_scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv):
     bg = _batch_args(mu, log_scale, color, opacity, bg, theta)
+    if color.shape[-1] > MAX_CHANNELS:
+        return _channel_chunks(lambda c, b: _apply_levels(mu, log_scale, c, opacity, b, theta, H, W, TILE, cutoff,
+                                                          max_pairs, odds, lv), color, bg)
     scale, is_log = _scale_arg(log_scale)
     return _AlphaRenderLevels.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
                                     is_log)
@@ -1062,6 +1081,10 @@ def render_alpha_full_triton(mu, log_scale, color, opacity, bg, H, W, theta=None
     at `cutoff` sigma. Returns [B,C,H,W]. The name is kept for drop-in compatibility; no Triton is used."""
     B, N, C = color.shape
     bg = _batch_args(mu, log_scale, color, opacity, bg, theta)
+    if C > MAX_CHANNELS:
+        return _channel_chunks(lambda c, b: render_alpha_full_triton(mu, log_scale, c, opacity, b, H, W, theta=theta,
+                                                                     cull=cull, TILE=TILE, cutoff=cutoff, odds=odds),
+                               color, bg)
     if cull:
         scale, is_log = _scale_arg(log_scale)
         return _AlphaRenderCull.apply(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds, is_log)

@@ -1,8 +1,9 @@
 """Colour channel counts other than 3. The kernels are instantiated for C = 1..4 (render_triton.py sizes its
-colour blocks by next_pow2(C); every caller of the reference uses C = 3), so each other count is checked against
-the float64 oracle like C = 3 is: the culled render (alpha and odds), the exact render and the multi-level octave
-render, image and the six gradients, at the same tolerances (image 1e-5 max-abs, gradients 1e-4 relative). The
-upstream gradient has C channels."""
+colour blocks by next_pow2(C) and takes any count; every caller of the reference uses C = 3); the Python entry
+points render more channels as chunks of at most 4 (render_hip._channel_chunks). Each count is checked against the
+float64 oracle like C = 3 is: the culled render (alpha and odds), the exact render and the multi-level octave
+render, image and the six gradients, at the same tolerances (image 1e-5 max-abs, gradients 1e-4 relative), and the
+subsampled exact render against the full one. The upstream gradient has C channels."""
 
 import numpy as np
 import pytest
@@ -28,7 +29,7 @@ def gout_c(C, H, W, dev, seed):
     return torch.randn(1, C, H, W, generator=g).to(dev)
 
 
-@pytest.mark.parametrize("C", [1, 2, 4])
+@pytest.mark.parametrize("C", [1, 2, 4, 5, 8])
 @pytest.mark.parametrize("odds", [False, True])
 def test_cull_channels(dev, C, odds):
     H = W = 48
@@ -40,7 +41,7 @@ def test_cull_channels(dev, C, odds):
     compare(out, g, ref, rg)
 
 
-@pytest.mark.parametrize("C", [1, 4])
+@pytest.mark.parametrize("C", [1, 4, 6])
 def test_exact_channels(dev, C):
     H = W = 24
     scene = scene_c(C, 200, H, W, seed=50 + C, dev=dev, ls_mean_px=2.0)
@@ -50,7 +51,7 @@ def test_exact_channels(dev, C):
     compare(out, g, ref, rg)
 
 
-@pytest.mark.parametrize("C", [1, 2, 4])
+@pytest.mark.parametrize("C", [1, 2, 4, 5])
 def test_octave_channels(dev, C):
     """Splats spanning several octaves (as test_gpu_api's multi-level test): the split coarse-level launches, the
     upsample inside the composite and its adjoint, for C channels."""
@@ -69,3 +70,29 @@ def test_octave_channels(dev, C):
     out, gd = device_run(RH.render_alpha_octave, scene, gout, H=H, W=W, odds=True)
     ref, rg = oracle_run("octave", scene, gout, H, W, odds=True)
     compare(out, gd, ref, rg)
+
+
+def test_subsampled_channels(dev):
+    """render_alpha_subsampled with 7 channels (chunks of 4 and 3) at given pixels against the full exact render of
+    the same scene at those pixels (pixel centres (i + 0.5) / H there, linspace in the full render: 1 ulp apart),
+    image and gradients, with a background of shape [1, C] over a batch of two."""
+    from gaussian_splat_encoder import render as RN
+    C, H, W = 7, 20, 28
+    mu, ls, _, op, _, th = random_scene(150, H, W, seed=71, dev=dev, ls_mean_px=2.0, B=2)
+    g = torch.Generator().manual_seed(72)
+    scene = [mu, ls, torch.rand(2, 150, C, generator=g).to(dev), op, torch.rand(1, C, generator=g).to(dev), th]
+    idx = torch.randint(0, H * W, (2, 300), generator=torch.Generator().manual_seed(5)).to(dev)
+    gsub = torch.randn(2, C, 300, generator=torch.Generator().manual_seed(6)).to(dev)
+    leaves = [t.detach().clone().requires_grad_(True) for t in scene]
+    sub, px = RN.render_alpha_subsampled(*leaves[:5], H, W, theta=leaves[5], pixel_indices=idx)
+    assert sub.shape == (2, C, 300) and torch.equal(px, idx)
+    (sub * gsub).sum().backward()
+    g_sub = [t.grad.clone() for t in leaves]
+    leaves2 = [t.detach().clone().requires_grad_(True) for t in scene]
+    full = RN.render_alpha_full(*leaves2[:5], H, W, theta=leaves2[5])
+    picked = full.reshape(2, C, H * W).gather(2, idx.unsqueeze(1).expand(2, C, 300))
+    assert (picked - sub).abs().max().item() <= 1e-5
+    (picked * gsub).sum().backward()
+    for a, b in zip(g_sub, [t.grad for t in leaves2]):
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 1e-4 * max(scale, 1e-9)
