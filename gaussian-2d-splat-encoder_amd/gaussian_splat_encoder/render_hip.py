@@ -510,6 +510,15 @@ def _level_splits(bins, lt, mask):
     return sp
 
 
+def _fwd_order(bins, lt, mask, held):
+    """What the summation order of a levels forward launched for per-level totals lt over the levels in `mask`
+    depends on, over the levels in `held`: each coarse level's chunks per tile (their partial sums are added in
+    chunk order) and the level-0 composite's waves per tile."""
+    sp = _level_splits(bins, lt, mask & ~1)
+    return (tuple(sp[l] for l in range(1, bins.n_levels) if (held >> l) & 1),
+            _wide(bins.TILE, bins.ntiles0, lt[0]))
+
+
 def _fields_buffers(npix, C, dev):
     """Packed level fields S_log [Pt], S_a [Pt], S_ac [Pt,C], views of one allocation."""
     slog, sa, sac = torch.empty(npix * (2 + C), device=dev).split_with_sizes((npix, npix, npix * C))
@@ -576,10 +585,13 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
                 kernel_timer.close("fwd", ev)
 
     if bins.pending is not None:   # queued on the speculative pair list before the count is read
-        launch([_speculated_levels(bins)[0]])
+        spec = _speculated_levels(bins)[0]
+        launch([spec])
         if plan is not None:         # the backward's buffers, allocated while the GPU works towards the count
             plan.allocate(bins, B, N, C, dev, lib, bins.pending.cap)
-        if _finish(bins):
+        # launched again when the pair phase was redone, or when the count asks for another number of waves per
+        # tile than the speculated one (they group the per-pixel sums: the image depends on the inputs alone)
+        if _finish(bins) or _wide(TILE, bins.nt, bins.tot_b[0]) != _wide(TILE, bins.nt, spec):
             launch(bins.tot_b)
     else:
         launch(bins.tot_b)
@@ -708,8 +720,12 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
         mask_spec = _mask_of(lt_spec)
         launch(0, lt_spec, mask_spec)
         redone = _finish(bins)
-        if redone or bins.level_mask(0) & ~mask_spec:
-            launch(0, bins.level_tot_b[0], bins.level_mask(0))
+        lt, held = bins.level_tot_b[0], bins.level_mask(0)
+        # launched again when the pair phase was redone, when a level holding pairs was left out, or when the
+        # count asks for another summation order than the speculated totals gave
+        if redone or held & ~mask_spec or _fwd_order(bins, lt_spec, mask_spec, held) != _fwd_order(bins, lt, held,
+                                                                                                     held):
+            launch(0, lt, held)
     else:
         for b in range(B):
             launch(b, bins.level_tot_b[b], bins.level_mask(b))
