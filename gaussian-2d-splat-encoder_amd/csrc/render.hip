@@ -75,8 +75,8 @@ __device__ __forceinline__ float uniform_f(float x) {
 }
 
 // Whitened offsets (u, v) of the pixel centre (py0, px0) from a splat with centre (gy, gx) and rotation rows
-// (A, B), (Cc, D). A tile's pixels add their own offsets from the tile's first pixel centre to these, so their
-// rounding error is shared by the whole tile. The float32 differences py0 - gy, px0 - gx are exact wherever the
+// (A, B), (Cc, D). A tile's pixels add their own offsets from the tile's reference pixel centre (its middle pixel)
+// to these, so their rounding error is shared by the whole tile. The float32 differences py0 - gy, px0 - gx are exact wherever the
 // two lie within a factor of two (Sterbenz), which holds for every tile a splat reaches away from the canvas'
 // first rows and columns (there the values are small and so is their rounding); each product's rounding error is
 // recovered exactly by an fma and added back, so the result is within about one ulp of the exact offsets (a
@@ -88,7 +88,7 @@ __device__ __forceinline__ float2 offsets_at(float py0, float px0, float gy, flo
   return make_float2(fmaf(B, dx, pu) + fmaf(A, dy, -pu), fmaf(D, dx, pv) + fmaf(Cc, dy, -pv));
 }
 
-// One pixel-pair of the per-tile forward: (u0, v0) are the pair's whitened offsets at the tile's first pixel
+// One pixel-pair of the per-tile forward: (u0, v0) are the pair's whitened offsets at the tile's reference pixel
 // centre, (ly, lx) the lane's pixel centre relative to it, so u = A ly + B lx + u0 and v = Cc ly + D lx + v0.
 // t carries the running product of the group's (1 - a) factors.
 template <int C, bool ODDS, bool CLAMP>
@@ -112,7 +112,7 @@ __device__ __forceinline__ void fwd_tile_pair(const float* __restrict__ r, float
   for (int c = 0; c < C; ++c) sc[c] = fmaf(w, r[R_COL + c], sc[c]);
 }
 
-// Pairs [b0, b1) of one batch (their offsets at the tile origin in s_uv[0, b1 - b0)), in groups of four:
+// Pairs [b0, b1) of one batch (their offsets at the reference pixel in s_uv[0, b1 - b0)), in groups of four:
 // ids and records through scalar loads, offsets by LDS broadcast. The (1 - a) factors of eight pairs (two
 // groups) are multiplied before one log2: each factor is >= 1e-4, so the product stays >= 1e-32, a normal float.
 template <int C, bool ODDS, bool CLAMP>
@@ -150,9 +150,13 @@ __device__ __forceinline__ void fwd_batch(const float* __restrict__ rec, const i
 }
 
 // Forward sums of one pixel over pairs [i0, i1) of the tile's list, in batches of 64 pairs. At the start of a
-// batch lane j computes the offsets (u0, v0) of pair j at the tile origin (py0, px0) into the wave's LDS row
-// s_uv, and a ballot tells whether any pair of the batch can reach the alpha clamp; the pixel loop then reads
-// the offsets by broadcast while the pairs' ids and records come through scalar loads (SGPR operands).
+// batch lane j computes the offsets (u0, v0) of pair j at the tile's reference pixel centre (py0, px0) into the
+// wave's LDS row s_uv, and a ballot tells whether any pair of the batch can reach the alpha clamp; the pixel loop
+// then reads the offsets by broadcast while the pairs' ids and records come through scalar loads (SGPR operands).
+// The reference pixel is the tile's middle one (inside the canvas), so that its offsets and the pixels' own offsets
+// from it stay within about half the pair's whitened span over the tile: their rounding, about one ulp of that
+// size, is shared by the tile's pixels (for a splat far smaller than the tile, a span of hundreds, a few 1e-5 of
+// its falloff).
 // S_log is accumulated in log2 units, one log2 per eight pairs (see fwd_batch).
 template <int C, bool ODDS>
 __device__ __forceinline__ void fwd_tile_pixel(const float* __restrict__ rec, const int* __restrict__ gid, int i0,
@@ -268,7 +272,8 @@ __device__ __forceinline__ TileAt split_item(const LevelTable& L, const SplitTab
 
 // Pixel centres (render_triton.py:455-456, (i + 0.5) / size in float32) of a tile: lane j < TILE divides for row j
 // and lane TILE + j for column j, one division for the wave, and each lane takes its own row's and column's by
-// shuffles; l is the lane's pixel within the tile, (py0, px0) the tile's first pixel centre.
+// shuffles; l is the lane's pixel within the tile, (py0, px0) the centre of its reference pixel: the middle one
+// (TILE / 2, TILE / 2), or the canvas' last row or column where the tile extends past it.
 template <int TILE>
 __device__ __forceinline__ void tile_centres(const TileAt& ta, int l, int lane, float& py, float& px, float& py0,
                                              float& px0) {
@@ -278,8 +283,9 @@ __device__ __forceinline__ void tile_centres(const TileAt& ta, int l, int lane, 
   const float c = ((float)i + 0.5f) / (float)(row ? ta.H : ta.W);
   py = __shfl(c, (l / TILE) % TILE, 64);
   px = __shfl(c, TILE + l % TILE, 64);
-  py0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c)));
-  px0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), TILE));
+  const int ry = min(TILE / 2, ta.H - 1 - ta.ty * TILE), rx = min(TILE / 2, ta.W - 1 - ta.tx * TILE);
+  py0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), ry));
+  px0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), TILE + rx));
 }
 
 // Forward over the tiles [tb0, tb0 + ntiles) of the level table (levels without pairs are skipped).
@@ -312,7 +318,7 @@ __global__ __launch_bounds__((fwd_threads<TILE, S>())) void k_fwd_cull(
   const int wv = S > 1 ? wid : 0;
   const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
   const bool valid = l < TILE * TILE && yp < ta.H && xp < ta.W;
-  float py, px, py0, px0;   // the lane's pixel centre and the tile's first pixel centre
+  float py, px, py0, px0;   // the lane's pixel centre and the tile's reference pixel centre
   tile_centres<TILE>(ta, l, lane, py, px, py0, px0);
   int g0 = starts[ta.t], g1 = starts[ta.t + 1];
   if (S > 1) {
@@ -392,8 +398,9 @@ __global__ __launch_bounds__(tile_threads(TILE)) void k_fwd_fields_split(
   const bool valid = th < TILE * TILE && yp < ta.H && xp < ta.W;
   const float py = ((float)yp + 0.5f) / (float)ta.H;   // render_triton.py:455-456
   const float px = ((float)xp + 0.5f) / (float)ta.W;
-  const float py0 = uniform_f(((float)(ta.ty * TILE) + 0.5f) / (float)ta.H);
-  const float px0 = uniform_f(((float)(ta.tx * TILE) + 0.5f) / (float)ta.W);
+  // the reference pixel: the middle one, or the canvas' last row / column where the tile extends past it
+  const float py0 = uniform_f(((float)min(ta.ty * TILE + TILE / 2, ta.H - 1) + 0.5f) / (float)ta.H);
+  const float px0 = uniform_f(((float)min(ta.tx * TILE + TILE / 2, ta.W - 1) + 0.5f) / (float)ta.W);
   int g0 = starts[ta.t];
   const int g1t = starts[ta.t + 1];
   const int len = ((g1t - g0 + nsplit - 1) / nsplit + 3) & ~3;

@@ -166,8 +166,10 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
  * colour[C]) the sum over the splat's pixel-pairs of the magnitudes of every term that enters that component:
  * the scale against which a per-splat relative error of the component is meaningful. Each pixel-pair's term is
  * the reference's product of factors (render_triton.py:688-710) with every sum in it replaced by the sum of its
- * terms' magnitudes: da by m_da = |dS_log u| + (|dS_a| + sum_c |dS_ac[c] col[c]|) u^k (k = 2 for odds, 0 for
+ * terms' magnitudes: da by m_da = |dS_log| |u| + (|dS_a| + sum_c |dS_ac[c] col[c]|) u^k (k = 2 for odds, 0 for
  * alpha), and the two summands of each of g_mu and g_theta taken apart (|gry c| + |grx s|, |gry rx| + |grx ry|).
+ * In composite mode |dS_log| and |dS_a| are themselves the composite's per-channel terms summed in magnitude
+ * (T sum_c |gout[c] (bg[c] - fg[c])| and sum_c |gout[c] (1 - T) fg[c]| / asum, render_triton.py:650-654).
  * Tiles run in parallel (OpenMP), each thread into accumulators of its own, summed in thread order. */
 enum { ACC_MU = 0, ACC_SC = 2, ACC_TH = 4, ACC_OP = 5, ACC_COL = 6 };
 
@@ -197,6 +199,7 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
         double* A = acc + (size_t)tid * (size_t)(N > 0 ? N : 1) * K;
         double* gb = bgacc + (size_t)tid * 16;
         double dS_ac[16];
+        double dS_log_m, dS_a_m;   /* magnitudes: the composite's per-channel terms summed in absolute value */
 #pragma omp for schedule(dynamic, 4)
         for (int t = 0; t < ntx * nty; ++t) {
             const int ty = t / ntx, tx = t % ntx;
@@ -210,18 +213,23 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
                     if (fields) {
                         dS_log = dslog_in[p]; dS_a = dsa_in[p];
                         for (int c = 0; c < C; ++c) dS_ac[c] = dsac_in[p * C + c];
+                        dS_log_m = fabs(dS_log); dS_a_m = fabs(dS_a);
                     } else {
                         /* render_triton.py:650-654 */
-                        double dTp = 0.0, sfg = 0.0;
+                        double dTp = 0.0, sfg = 0.0, dTp_m = 0.0, sfg_m = 0.0;
                         for (int c = 0; c < C; ++c) {
                             const double go = gout[p * C + c], dfg = go * (1.0 - T[p]);
                             dTp += go * ((double)bg[c] - fg[p * C + c]);
                             sfg += dfg * fg[p * C + c];
+                            dTp_m += fabs(go * ((double)bg[c] - fg[p * C + c]));
+                            sfg_m += fabs(dfg * fg[p * C + c]);
                             dS_ac[c] = dfg / asum[p];
                             gb[c] += go * T[p];
                         }
                         dS_log = dTp * T[p];
                         dS_a = -sfg / asum[p];
+                        dS_log_m = dTp_m * fabs(T[p]);
+                        dS_a_m = sfg_m / fabs(asum[p]);
                     }
                     for (int i = tile_starts[t]; i < tile_starts[t + 1]; ++i) {
                         const int g = gid_sorted[i];
@@ -238,10 +246,10 @@ void orc_bwd_cull(const float* mu, const float* scale, const float* theta, const
                         double da, cw, mag;
                         if (odds) {
                             da = -dS_log * u + (dS_a + col_term) * u * u; cw = a * u;
-                            mag = fabs(dS_log * u) + (fabs(dS_a) + col_abs) * u * u;
+                            mag = dS_log_m * fabs(u) + (dS_a_m + col_abs) * u * u;
                         } else {
                             da = -dS_log * u + dS_a + col_term; cw = a;
-                            mag = fabs(dS_log * u) + fabs(dS_a) + col_abs;
+                            mag = dS_log_m * fabs(u) + dS_a_m + col_abs;
                         }
                         double* m_g = a_g + KG;
                         for (int c = 0; c < C; ++c) {

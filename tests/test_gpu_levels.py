@@ -127,10 +127,27 @@ def test_upsample_adjoint_matches_torch(dev, H, W, C):
             assert e <= 1e-5, f"level {l} term {k}: rel {e:.2e}"
 
 
-def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=3.0):
+def composite_bwd_on(T, S_a, fg, bg, gout):
+    """float64 gradients of the octave/multires composite (render_triton.py:918-921, 976-980: T = exp(S_log),
+    asum = S_a.clamp_min(1e-8), fg = S_ac / asum, out = (1 - T) fg + T bg) w.r.t. S_log [P], S_a [P], S_ac [P,C]
+    and bg [C], evaluated at given forward quantities T [P], unclamped S_a [P] and fg [P,C] (clamp_min passes the
+    gradient where S_a >= 1e-8)."""
+    T, S_a, fg, bg, gout = (np.asarray(a, np.float64) for a in (T, S_a, fg, bg, gout))
+    asum = np.maximum(S_a, 1e-8)
+    omt = 1.0 - T
+    d_slog = T * (gout * (bg[None, :] - fg)).sum(-1)
+    d_sac = gout * (omt / asum)[:, None]
+    d_sa = np.where(S_a >= 1e-8, -(omt / asum) * (gout * fg).sum(-1), 0.0)
+    return d_slog, d_sa, d_sac, (gout * T[:, None]).sum(0)
+
+
+def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=3.0, fwd=None):
     """float64 oracle of one batch: C-oracle fields per level, torch float64 glue, C-oracle fields backward.
     Returns the image [P, C] and the gradients w.r.t. (mu, activated scale, colour, opacity, bg, theta), plus
-    each splat's opacity-gradient scale ("op_scale", see c_oracle.bwd_cull)."""
+    each splat's opacity-gradient scale ("op_scale", see c_oracle.bwd_cull). fwd = (T, S_a, fg): the backward
+    starts from these forward quantities (the device forward's) instead of the oracle's own, so that it checks the
+    backward alone where float32 forward rounding decides the gradients (1 - T below float32 resolution, S_a at
+    the clamp)."""
     mu_, sc_, col_, op_, bg_ = np_(mu), np_(sc), np_(col), np_(op), np_(bg)
     th_ = None if th is None else np_(th)
     N, C = col_.shape
@@ -156,34 +173,65 @@ def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=
              torch.zeros(H * W, C, dtype=torch.float64)]
     bg64 = torch.from_numpy(bg_.astype(np.float64)).requires_grad_(True)
     out = R.composite(*S, bg64, straight_through=False)[0]
-    (out * torch.from_numpy(np_(gout)).double()).sum().backward()
+    if fwd is None:
+        (out * torch.from_numpy(np_(gout)).double()).sum().backward()
+        g_bg = bg64.grad.numpy()
+    else:   # the composite's gradients at the given forward quantities, through the same upsample adjoints
+        d_slog, d_sa, d_sac, g_bg = composite_bwd_on(*fwd, bg_, np_(gout))
+        if leaves:
+            dS = [torch.from_numpy(d_slog), torch.from_numpy(d_sa), torch.from_numpy(d_sac)]
+            sum((s_ * d).sum() for s_, d in zip(S, dS)).backward()
     grads = {"mu": np.zeros((N, 2)), "scale": np.zeros((N, 2)), "col": np.zeros((N, C)), "op": np.zeros(N),
-             "theta": np.zeros(N) if th is not None else None, "bg": bg64.grad.numpy()}
+             "theta": np.zeros(N) if th is not None else None, "bg": g_bg}
     mag = {k: np.zeros_like(v) for k, v in grads.items() if v is not None and k != "bg"}
+    # each splat's scale ('mag') sums the magnitudes of every term along the whole chain: the composite's
+    # per-channel terms, the upsample adjoint's per-destination terms (non-negative weights: the adjoint of the
+    # magnitudes), then the fields backward's terms on those magnitudes
+    if fwd is None:
+        T0 = torch.exp(S[0]).detach().numpy()
+        Sa0 = S[1].detach().numpy()
+        fg0 = (S[2] / S[1].clamp_min(1e-8)[:, None]).detach().numpy()
+    else:
+        T0, Sa0, fg0 = (np.asarray(a, np.float64) for a in fwd)
+    go = np.abs(np_(gout)).astype(np.float64)
+    r0 = (1.0 - T0) / np.maximum(Sa0, 1e-8)
+    m0 = [T0 * (go * np.abs(bg_[None, :].astype(np.float64) - fg0)).sum(-1),
+          np.where(Sa0 >= 1e-8, r0 * (go * np.abs(fg0)).sum(-1), 0.0), go * np.abs(r0)[:, None]]
     for (l, idx, args, gid, st, Hl, Wl), f in zip(per_level, leaves):
         d = [x.grad.numpy() if x.grad is not None else np.zeros(x.shape) for x in f]
         gl = c_oracle.bwd_cull(*args, gid, st, Hl, Wl, TILE, odds=odds, fields=True, dslog=d[0], dsa=d[1], dsac=d[2])
+        if l == 0:
+            dm = m0
+        else:   # adjoint of the upsample applied to the magnitudes
+            xs = [torch.zeros(x.shape, dtype=torch.float64, requires_grad=True) for x in f]
+            sum((R.upsample_field(x, Hl, Wl, H, W) * torch.from_numpy(m)).sum() for x, m in zip(xs, m0)).backward()
+            dm = [x.grad.numpy() for x in xs]
+        gm = c_oracle.bwd_cull(*args, gid, st, Hl, Wl, TILE, odds=odds, fields=True, dslog=dm[0], dsa=dm[1],
+                               dsac=dm[2])
         for k in ("mu", "scale", "col", "op", "theta"):
             if grads[k] is not None:
                 grads[k][idx] = gl[k]
-                mag[k][idx] = gl["mag"][k]
+                mag[k][idx] = np.maximum(gl["mag"][k], gm["mag"][k])
     grads["mag"] = mag
     grads["op_scale"] = mag["op"]
     return out.detach().numpy(), grads
 
 
 def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL,
-               want_grads=False, per_splat=True):
+               want_grads=False, per_splat=True, bwd_on_device_fwd=False):
     """Fused level render of one batch against composed_oracle: the image, every gradient tensor and, with
     per_splat, every gradient component of every splat against that splat's own scale (check_per_splat).
-    Returns the bins, and with want_grads also the device gradients by name and the oracle's."""
+    bwd_on_device_fwd: the gradients are held against the oracle's backward from the device forward's T, S_a and
+    fg (the image still against the oracle's own forward). Returns the bins, and with want_grads also the device
+    gradients by name and the oracle's."""
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
     out, (T, asum, fg), bins = RH._forward_levels(mu, sc, col, op, bg, th, H, W, TILE, 3.0, None, odds, lv)
     gout = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed)).to(mu.device)
     g_mu, g_sc, g_col, g_op, g_bg, g_th = RH._backward_levels(gout, col, bg, th is not None, T, asum, fg, bins, odds)
+    fwd = (np_(T[0]), np_(asum[0]), np_(fg[0])) if bwd_on_device_fwd else None
     img_ref, gref = composed_oracle(mu[0], sc[0], col[0], op[0], bg[0], None if th is None else th[0], H, W, TILE,
-                                    lv, odds, gout[0])
+                                    lv, odds, gout[0], fwd=fwd)
     d = np.abs(np_(out[0]) - img_ref.reshape(P, C)).max()
     assert d <= img_tol, f"image max-abs {d:.2e}"
     for name, got in (("mu", g_mu), ("scale", g_sc), ("col", g_col), ("op", g_op), ("bg", g_bg), ("theta", g_th)):

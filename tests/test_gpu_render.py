@@ -17,11 +17,14 @@ def oracle_pairs(mu, sc, H, W, TILE, cutoff=3.0):
     return c_oracle.build_tiles(np_(mu[0]), np_(sc[0]), H, W, TILE, cutoff)
 
 
-def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True, per_splat=True):
+def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True, per_splat=True,
+             bwd_on_device_fwd=False):
     """Forward (and backward) of one batch against the C oracle over the oracle's pair list. Gradients are held
     to GRAD_REL_TOL of each tensor's largest magnitude and, with per_splat, every component of every splat to
-    PER_SPLAT_TOL of that splat's own scale for it (the oracle's 'mag'). Returns the device gradients by name
-    and the oracle's (None without the backward)."""
+    PER_SPLAT_TOL of that splat's own scale for it (the oracle's 'mag'). bwd_on_device_fwd (composite renders):
+    the oracle's backward starts from the device forward's T, asum and fg instead of its own, so that the
+    gradients check the backward alone (float32 forward rounding can decide them where 1 - T is below float32
+    resolution). Returns the device gradients by name and the oracle's (None without the backward)."""
     dev = mu.device
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
@@ -55,8 +58,10 @@ def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bw
             return
         gout = torch.randn(out.shape, generator=g).to(dev)
         grads = RH._backward_cull(gout, mu, sc, col, op, bg, th, T, asum, fg, bins, H, W, TILE, odds=odds)
-        gref = c_oracle.bwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=False, bg=np_(bg[0]), T=ref[1],
-                                 asum=ref[2], fg=ref[3], gout=np_(gout[0]))
+        Tq, aq, fq = ((np_(T[0]).astype(np.float64), np_(asum[0]).astype(np.float64), np_(fg[0]).astype(np.float64))
+                      if bwd_on_device_fwd else (ref[1], ref[2], ref[3]))
+        gref = c_oracle.bwd_cull(*args, gid, st, H, W, TILE, odds=odds, fields=False, bg=np_(bg[0]), T=Tq,
+                                 asum=aq, fg=fq, gout=np_(gout[0]))
         names = ["mu", "scale", "col", "op", "bg", "theta"]
     for name, got in zip(names, grads):
         if got is None:
