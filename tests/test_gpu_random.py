@@ -11,13 +11,21 @@ count, log-normal splat sizes from a fifth of a pixel to 30 pixels with spreads 
   rounding decides gradients in pixels whose 1 - T is below float32 resolution or whose S_a sits at the 1e-8
   clamp, in the reference's float32 as here, so the backward is held to the bar on the quantities it receives.
   The per-splat scale sums the magnitudes of every term along the chain (composite channels, upsample adjoint).
+
+A second set draws calls of the entry points themselves (render_alpha_full_triton culled and exact,
+render_alpha_octave, render_alpha_multires) with batches of 1 to 3 images, 1 to 7 colour channels (more than four
+render as chunks), a background of shape [B, C] or [1, C], rotation or none, and tile sizes and cutoffs, in
+well-conditioned scenes (opacities 0.45 to 0.95, splats of 1 to 12 pixels): every image of a batch equals its own
+single-image call bit for bit, image and gradients included, and the first image and its gradients meet the image
+and gradient bars against the float64 oracle through autograd (log-scales included).
 """
 
 import numpy as np
 import pytest
 import torch
 
-from _gpu_util import activate_scale, device_bins, random_scene
+from _gpu_util import GRAD_REL_TOL, IMG_TOL, RH, activate_scale, device_bins, np_, random_scene, rel_err
+from test_gpu_api import NAMES, oracle_run
 from test_gpu_levels import octave_lv, run_levels, split_lv
 from test_gpu_render import oracle_pairs, run_case
 
@@ -71,3 +79,72 @@ def test_random_scene(dev, k):
     else:
         run_levels(*scene, H, W, TILE, split_lv(H, W, c["n_coarse"], c["cf"]), c["odds"], seed=k,
                    bwd_on_device_fwd=True)
+
+
+API_SEED0 = 100
+N_API_CASES = 24
+
+
+def draw_api(k, dev):
+    rng = np.random.default_rng(API_SEED0 + k)
+    kind = str(rng.choice(["cull", "cull", "exact", "octave", "multires"]))
+    B, C = int(rng.integers(1, 4)), int(rng.choice([1, 2, 3, 4, 5, 7]))
+    H, W = int(rng.integers(8, 100)), int(rng.integers(8, 100))
+    N = int(rng.integers(1, 1200)) if kind != "exact" else int(rng.integers(1, 300))
+    theta, odds = bool(rng.integers(0, 2)), bool(rng.integers(0, 2)) if kind != "exact" else False
+    bg1 = bool(rng.integers(0, 2))
+    TILE, cutoff = int(rng.choice([4, 8, 16])), float(rng.choice([2.0, 3.0, 4.0]))
+    ls_mean = float(np.exp(rng.uniform(np.log(1.0), np.log(12.0))))
+    g = torch.Generator().manual_seed(API_SEED0 + k)
+    mu = torch.rand(B, N, 2, generator=g) * 1.2 - 0.1
+    ls = np.log(ls_mean / max(H, W)) + 0.5 * torch.randn(B, N, 2, generator=g)
+    col = torch.rand(B, N, C, generator=g)
+    op = torch.rand(B, N, generator=g) * 0.5 + 0.45
+    bg = torch.rand(1 if bg1 else B, C, generator=g)
+    th = torch.rand(B, N, generator=g) * 6.28 if theta else None
+    scene = [None if t is None else t.to(dev) for t in (mu, ls, col, op, bg, th)]
+    gout = torch.randn(B, C, H, W, generator=g).to(dev)
+    if kind == "cull":
+        kw = dict(TILE=TILE, cutoff=cutoff, odds=odds)
+        fn = lambda *a, theta=None: RH.render_alpha_full_triton(*a, H, W, theta=theta, cull=True, **kw)
+    elif kind == "exact":
+        kw = {}
+        fn = lambda *a, theta=None: RH.render_alpha_full_triton(*a, H, W, theta=theta, cull=False)
+    elif kind == "octave":
+        kw = dict(TILE=TILE, odds=odds)
+        fn = lambda *a, theta=None: RH.render_alpha_octave(*a, H, W, theta=theta, **kw)
+    else:
+        kw = dict(TILE=TILE, odds=odds, n_coarse=int(rng.integers(0, N + 1)))
+        fn = lambda *a, theta=None: RH.render_alpha_multires(*a, H, W, theta=theta, **kw)
+    desc = dict(kind=kind, B=B, C=C, H=H, W=W, N=N, theta=theta, bg1=bg1, ls_mean=round(ls_mean, 2), **kw)
+    return desc, fn, kw, scene, gout, bg1
+
+
+def run_api(fn, scene, gout, bg1=False, b=None):
+    """fn on leaves copied from scene (image b alone when given, with the whole bg when bg1); (out, grads)."""
+    sl = [None if t is None else (t if b is None or (n == "bg" and bg1) else t[b:b + 1]) for n, t in zip(NAMES, scene)]
+    L = [None if t is None else t.detach().clone().requires_grad_(True) for t in sl]
+    out = fn(*L[:5], theta=L[5])
+    (out * (gout if b is None else gout[b:b + 1])).sum().backward()
+    return out.detach(), {n: (None if t is None else t.grad) for n, t in zip(NAMES, L)}
+
+
+@pytest.mark.parametrize("k", range(N_API_CASES))
+def test_random_entry_point_call(dev, k):
+    desc, fn, kw, scene, gout, bg1 = draw_api(k, dev)
+    print(f"random entry-point case {k}: {desc}", flush=True)
+    H, W = desc["H"], desc["W"]
+    out, grads = run_api(fn, scene, gout)
+    for b in range(desc["B"]):
+        ob, gb = run_api(fn, scene, gout, bg1, b)
+        assert torch.equal(ob[0], out[b]), f"image {b} differs from its single-image call"
+        for n in NAMES:
+            if gb[n] is not None and n != "bg":
+                assert torch.equal(gb[n][0], grads[n][b]), f"gradient {n} of image {b} differs"
+    ref_img, ref_g = oracle_run(desc["kind"], [None if t is None else t[0:1] for t in scene], gout[0:1], H, W, **kw)
+    d = np.abs(np_(out[0]) - ref_img.numpy()).max()
+    assert d <= IMG_TOL, f"image max-abs {d:.2e}"
+    for n in NAMES:
+        if ref_g[n] is not None and n != "bg":
+            e = rel_err(np_(grads[n][0]), ref_g[n].numpy())
+            assert e <= GRAD_REL_TOL, f"gradient {n}: rel {e:.2e}"
