@@ -289,6 +289,8 @@ def _align(n):
 
 
 _CARVE_OFF = {}   # tuple of sizes -> sub-buffer offsets (the renders of one configuration repeat their sizes)
+_PAIRS_WS = {}    # (binning configuration, capacity) -> pair-phase workspace bytes
+_SUMS_FLOATS = {}   # capacity -> floats of one image's per-pair sums (16-byte aligned)
 
 
 class _Carve:
@@ -346,12 +348,20 @@ def _budget_error(n, max_pairs, H, W, TILE, cutoff, N):
         f"instead of culling at full res. Refusing to allocate.")
 
 
-def _pair_buffers(lib, N, nt, cap, with_maps, dev, geo):
+def _pair_buffers(lib, N, nt, cap, with_maps, dev, geo, key=None):
     """gid, starts, pair_q and the pair-phase workspace for up to `cap` pairs, one allocation.
-    geo = (H, W, TILE, levels byref or None)."""
+    geo = (H, W, TILE, levels byref or None); key: the binning configuration (caches the workspace size)."""
     c = max(cap, 1)
     m = c if with_maps else 0
-    return _Carve([4 * c, 4 * (nt + 1), 4 * m, lib.splat_bin_pairs_workspace_bytes(N, *geo, cap)], dev)
+    wk = None if key is None else (key, cap)
+    wsb = _PAIRS_WS.get(wk) if wk is not None else None
+    if wsb is None:
+        wsb = lib.splat_bin_pairs_workspace_bytes(N, *geo, cap)
+        if wk is not None:
+            if len(_PAIRS_WS) > 4096:
+                _PAIRS_WS.clear()
+            _PAIRS_WS[wk] = wsb
+    return _Carve([4 * c, 4 * (nt + 1), 4 * m, wsb], dev)
 
 
 class _Pending:
@@ -428,7 +438,7 @@ def _bin_impl(mu, scale, color, opacity, theta, H, W, TILE, cutoff, max_pairs, w
     blocks, pairs, tots, level_tots = [], [], [], []
     for b in range(B):
         blk = _Carve([64 * N, 16 * N, 4 * (N + 1), 8 * (2 + L), ws1_bytes], dev)
-        pb = _pair_buffers(lib, N, nt, cap, with_maps, dev, geo) if cap else None
+        pb = _pair_buffers(lib, N, nt, cap, with_maps, dev, geo, key) if cap else None
         pp = (lambda i: None) if pb is None else pb.ptr
         info_np[0] = info_np[1] = 0
         rc = lib.splat_bin(_bptr(mu_, b), _bptr(sc_, b), _bptr(th_, b), _bptr(op_, b), _bptr(col_, b),
@@ -554,10 +564,12 @@ def _render_fwd(lib, bins, b, C, flags, lev, mask, comp, fields, stream):
 
 
 def _composite_buffers(B, P, C, dev):
-    """out [B,P,C], T [B,P], asum [B,P], fg [B,P,C] as views of one allocation."""
+    """out [B,P,C], T [B,P], asum [B,P], fg [B,P,C] as contiguous views of one allocation (strided views: one
+    operation each)."""
     n = B * P
-    out, T, asum, fg = torch.empty(n * (2 * C + 2), device=dev).split_with_sizes((n * C, n, n, n * C))
-    return out.view(B, P, C), T.view(B, P), asum.view(B, P), fg.view(B, P, C)
+    t = torch.empty(n * (2 * C + 2), device=dev)
+    return (t.as_strided((B, P, C), (P * C, C, 1), 0), t.as_strided((B, P), (P, 1), n * C),
+            t.as_strided((B, P), (P, 1), n * (C + 1)), t.as_strided((B, P, C), (P * C, C, 1), n * (C + 2)))
 
 
 def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0, max_pairs=None, odds=False,
@@ -576,11 +588,15 @@ def _forward_cull(mu, scale, color, opacity, bg, theta, H, W, TILE=8, cutoff=3.0
 
     def launch(tots):
         for b in range(B):
+            comp = (_bptr(bgf, b), _bptr(out, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b))
+            if not kernel_timer.enabled:
+                _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, tots[b]), (0, 1), 1, comp, (None,) * 3,
+                            stream)
+                continue
             ev = kernel_timer.record("fwd")
             try:
-                _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, tots[b]), (0, 1), 1,
-                            (_bptr(bgf, b), _bptr(out, b), _bptr(T, b), _bptr(asum, b), _bptr(fg, b)),
-                            (None, None, None), stream)
+                _render_fwd(lib, bins, b, C, flags | _wide(TILE, bins.nt, tots[b]), (0, 1), 1, comp, (None,) * 3,
+                            stream)
             finally:
                 kernel_timer.close("fwd", ev)
 
@@ -606,31 +622,38 @@ class _BwdPlan:
     of the two backward launches per image, complete but for the upstream gradient's pointer. The backward then runs
     two C-ABI calls per image (render_triton.py:723-765 in two kernels)."""
 
-    __slots__ = ("grads", "sums", "bg_part", "cap", "bwd_head", "bwd_tail", "red_args", "lsc", "has_th", "keep")
+    __slots__ = ("grads", "sums", "ns", "cap", "bwd_head", "bwd_tail", "red_args", "lsc", "has_th", "keep")
 
     def __init__(self, has_th, lsc=None):
         self.has_th = has_th
         self.lsc = _f32(lsc)   # the raw log-scales as the reduction reads them (kept alive here)
         self.cap = -1
-        self.sums = self.bg_part = None
+        self.sums = None
 
     def allocate(self, bins, B, N, C, dev, lib, cap):
+        """Gradient outputs and one buffer for the per-pair sums of every image (ns floats each, 16-byte aligned)
+        followed by the per-tile background partials (the kernels take both by pointer)."""
         self.grads = _grads_bg_out(B, N, C, dev, self.has_th)
-        ns = (lib.splat_pair_sums_bytes(max(cap, 1)) // 4 + 3) & ~3   # partials start 16-byte aligned
-        self.sums, self.bg_part = torch.empty(B * ns + C * bins.ntiles0, device=dev).split_with_sizes(
-            (B * ns, C * bins.ntiles0))
+        ns = _SUMS_FLOATS.get(cap)
+        if ns is None:
+            if len(_SUMS_FLOATS) > 1024:
+                _SUMS_FLOATS.clear()
+            ns = _SUMS_FLOATS[cap] = (lib.splat_pair_sums_bytes(max(cap, 1)) // 4 + 3) & ~3
+        self.sums = torch.empty(B * ns + C * bins.ntiles0, device=dev)
+        self.ns = ns
         self.cap = cap
 
     def bind(self, bins, B, N, C, dev, lib, stream, flags, comp):
         tots = bins.tot_b
         if self.sums is None or max(tots) > self.cap:
             self.allocate(bins, B, N, C, dev, lib, max(tots))
-        ns = self.sums.numel() // max(B, 1)
+        ns = self.ns
         g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
         bgf, T, asum, fg = comp
         self.keep = bgf   # the kernels read the background through its pointer
         lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
-        sums0, bgp = self.sums.data_ptr(), self.bg_part.data_ptr()
+        sums0 = self.sums.data_ptr()
+        bgp = sums0 + 4 * B * ns
         self.bwd_head, self.bwd_tail, self.red_args = [], [], []
         for b in range(B):
             sb = sums0 + 4 * ns * b
@@ -652,7 +675,12 @@ class _BwdPlan:
         else:
             go = grad_out.permute(0, 2, 3, 1).contiguous().float()
             g0 = go.data_ptr()
+        timed = kernel_timer.enabled
         for b in range(B):
+            if not timed:
+                check(lib.splat_render_bwd(*self.bwd_head[b], g0 + 4 * img * b, *self.bwd_tail[b]), "splat_render_bwd")
+                check(lib.splat_reduce_pairs(*self.red_args[b]), "splat_reduce_pairs")
+                continue
             ev = kernel_timer.record("bwd")
             try:
                 check(lib.splat_render_bwd(*self.bwd_head[b], g0 + 4 * img * b, *self.bwd_tail[b]), "splat_render_bwd")
@@ -664,7 +692,7 @@ class _BwdPlan:
             finally:
                 kernel_timer.close("reduce", ev)
         g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
-        self.grads = self.sums = self.bg_part = self.keep = None
+        self.grads = self.sums = self.keep = None
         return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
@@ -741,10 +769,12 @@ def _grads_bg_out(B, N, C, dev, has_th):
     """g_mu [B,N,2], g_scale [B,N,2], g_col [B,N,C], g_op [B,N], g_th [B,N] (or None) and g_bg [B,C]: views of one
     allocation (each a contiguous tensor of its own shape)."""
     n2, nc, n1 = B * N * 2, B * N * C, B * N
-    sizes = (n2, n2, nc, n1, n1 if has_th else 0, B * C)
-    g_mu, g_sc, g_col, g_op, g_th, g_bg = torch.empty(sum(sizes), device=dev).split_with_sizes(sizes)
-    return (g_mu.view(B, N, 2), g_sc.view(B, N, 2), g_col.view(B, N, C), g_op.view(B, N),
-            g_th.view(B, N) if has_th else None, g_bg.view(B, C))
+    t = torch.empty(2 * n2 + nc + (2 if has_th else 1) * n1 + B * C, device=dev)
+    o = 2 * n2 + nc + n1
+    return (t.as_strided((B, N, 2), (2 * N, 2, 1), 0), t.as_strided((B, N, 2), (2 * N, 2, 1), n2),
+            t.as_strided((B, N, C), (N * C, C, 1), 2 * n2), t.as_strided((B, N), (N, 1), 2 * n2 + nc),
+            t.as_strided((B, N), (N, 1), o) if has_th else None,
+            t.as_strided((B, C), (C, 1), o + (n1 if has_th else 0)))
 
 
 def _render_bwd(lib, bins, b, C, flags, lev, mask, upstream, sums, bg_part, stream):
