@@ -487,7 +487,7 @@ __device__ __forceinline__ void pixel_upstream(int p, size_t pp, const float* __
                                                const float* __restrict__ Tin, const float* __restrict__ asum_in,
                                                const float* __restrict__ fg_in, const float* __restrict__ gout,
                                                float* __restrict__ dslog, float* __restrict__ dsa,
-                                               float* __restrict__ dsac, float4& pa, float4& pb, float* bgp) {
+                                               float* __restrict__ dsac, float4& pa, float2& pb, float* bgp) {
   float dl, da, dc[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   if (FIELDS) {
     dl = dslog[pp];
@@ -496,7 +496,7 @@ __device__ __forceinline__ void pixel_upstream(int p, size_t pp, const float* __
     for (int c = 0; c < C; ++c) dc[c] = dsac[pp * C + c];
   } else {
     const float T = Tin[p], a_in = asum_in[p];
-    const float as = UPS ? fmaxf(a_in, kAsumMin) : a_in;
+    const float ras = 1.f / (UPS ? fmaxf(a_in, kAsumMin) : a_in);   // one division for the pixel's terms
     float dTp = 0.f, sfg = 0.f;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -504,11 +504,11 @@ __device__ __forceinline__ void pixel_upstream(int p, size_t pp, const float* __
       const float dfg = go * (1.f - T);
       dTp += go * (bg[c] - f);
       sfg += dfg * f;
-      dc[c] = dfg / as;
+      dc[c] = dfg * ras;
       bgp[c] += go * T;
     }
     dl = dTp * T;
-    da = -sfg / as;
+    da = -sfg * ras;
     if (UPS) {
       if (!(a_in >= kAsumMin)) da = 0.f;
       dslog[p] = dl;
@@ -518,7 +518,7 @@ __device__ __forceinline__ void pixel_upstream(int p, size_t pp, const float* __
     }
   }
   pa = make_float4(dl, da, dc[0], dc[1]);
-  pb = make_float4(dc[2], dc[3], 0.f, 0.f);
+  pb = make_float2(dc[2], dc[3]);
 }
 
 // Per-pair sums over pixels, in registers.
@@ -550,7 +550,7 @@ __device__ __forceinline__ PairOp pair_op(float op) {
 // terms to gc (as sum w' * dS_ac with w' = w / op; the caller multiplies by op once per pair) and returns
 // q = da * falloff, the pixel's weight in the pair's moment sums.
 template <int C, bool ODDS>
-__device__ __forceinline__ float bwd_q(float f, float oma, const float4& col, const float4& pa, const float4& pb,
+__device__ __forceinline__ float bwd_q(float f, float oma, const float4& col, const float4& pa, const float2& pb,
                                        float* gc) {
   const float rr = hw_rcp(oma);
   float ct = fmaf(pa.z, col.x, pa.y);   // dS_a + sum_c dS_ac[c] col[c]
@@ -575,7 +575,7 @@ __device__ __forceinline__ float bwd_q(float f, float oma, const float4& col, co
 // Accumulation of one pixel-pair of the backward with its whitened offsets u, v.
 template <int C, bool ODDS>
 __device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, const float4& col, const float4& pa,
-                                        const float4& pb, PairSums<C>& s) {
+                                        const float2& pb, PairSums<C>& s) {
   const float q = bwd_q<C, ODDS>(f, oma, col, pa, pb, s.gc);
   const float qu = q * u, qv = q * v;
   s.q += q;
@@ -591,7 +591,7 @@ __device__ __forceinline__ void bwd_acc(float u, float v, float f, float oma, co
 // falloff (render_triton.py:686, 697), so it adds its colour term here and continues with f = 0.
 template <int C, bool ODDS>
 __device__ __forceinline__ void bwd_px_near(float u, float v, float m, float f, const PairOp& po, const float4& col,
-                                            const float4& pa, const float4& pb, PairSums<C>& s) {
+                                            const float4& pa, const float2& pb, PairSums<C>& s) {
   const float fo = po.op * f;
   float oma = fmaf(-po.op, f, 1.f);
   if (fo > kNearOpaqueBwd) {
@@ -617,7 +617,7 @@ __device__ __forceinline__ void bwd_px_near(float u, float v, float m, float f, 
 // one-fma 1 - a and bwd_px_near (every lane of the wave must be executing).
 template <int C, bool ODDS>
 __device__ __forceinline__ void bwd_px(float u, float v, const PairOp& po, const float4& col, const float4& pa,
-                                       const float4& pb, PairSums<C>& s) {
+                                       const float2& pb, PairSums<C>& s) {
   const float m = fmaf(u, u, v * v);
   const float f = hw_exp2(-m);
   if (__any(f > po.thr))
@@ -719,10 +719,29 @@ __device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
   }
 }
 
-// Row stride (float4) of the per-pixel upstream terms in LDS: one padding slot per row, so the rows that
-// different lanes read at once (row-split remainder chunks) start on different banks.
+// The tile's per-pixel upstream terms in LDS, row by row: TILE float4 (dS_log, dS_a, dS_ac[0], dS_ac[1]), the row's
+// pixel centre (one float4 slot, in .x), then TILE float2 (dS_ac[2], dS_ac[3]). A row's reads take one base address
+// and immediate offsets. Rows are 6 TILE + 4 words (52 for 8 x 8 tiles, a multiple of four words for the 16-byte
+// reads), so the rows that different lanes read at once (row-split remainder chunks) start on different banks.
 template <int TILE>
-__host__ __device__ constexpr int up_stride() { return TILE + 1; }
+struct UpRows {
+  static constexpr int RF = 6 * TILE + 4;   // floats per row
+  float* base;
+  __device__ __forceinline__ const float* row(int yy) const { return base + yy * RF; }
+  __device__ __forceinline__ static float4 pa(const float* r, int xx) {
+    return *reinterpret_cast<const float4*>(r + 4 * xx);
+  }
+  template <int C>
+  __device__ __forceinline__ static float2 pb(const float* r, int xx) {
+    return C > 2 ? *reinterpret_cast<const float2*>(r + 4 * TILE + 4 + 2 * xx) : make_float2(0.f, 0.f);
+  }
+  __device__ __forceinline__ static float py(const float* r) { return r[4 * TILE]; }
+  __device__ __forceinline__ void put(int yy, int xx, const float4& a, const float2& b) const {
+    float* r = base + yy * RF;
+    *reinterpret_cast<float4*>(r + 4 * xx) = a;
+    *reinterpret_cast<float2*>(r + 4 * TILE + 4 + 2 * xx) = b;
+  }
+};
 
 // The tile's pixel centres (render_triton.py:455-456): the first and last row and column (py0, py1, px0, px1),
 // the half extents cy = (py1 - py0) / 2, cx = (px1 - px0) / 2, and every column's centre as a wave-uniform
@@ -836,20 +855,18 @@ __device__ __forceinline__ float2 direct_uv(const DirectGeo& g, const RowTerms& 
 // pair that may be near-opaque in the tile (near_possible) out of the wave's lanes.
 template <int C, bool ODDS, int TILE>
 __device__ __forceinline__ void pair_rows_direct(const DirectGeo& g, float op, const float4& col, int row0, int nrows,
-                                                 const float* s_pya, const TileCentres<TILE>& tc,
-                                                 const float4* s_pa, const float4* s_pb, PairSums<C>& s) {
+                                                 const UpRows<TILE>& ups, const TileCentres<TILE>& tc, PairSums<C>& s) {
   float dx[TILE];   // the columns' offsets from the splat centre, once per pair
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) dx[xx] = tc.pxa[xx] - g.gx;
 #pragma nounroll
   for (int yy = row0; yy < row0 + nrows; ++yy) {
-    const RowTerms rt = row_terms(g, s_pya[yy] - g.gy);
-    const float4* pa_row = s_pa + yy * up_stride<TILE>();
-    const float4* pb_row = s_pb + yy * up_stride<TILE>();
+    const float* r = ups.row(yy);
+    const RowTerms rt = row_terms(g, UpRows<TILE>::py(r) - g.gy);
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
-      const float4 pa = pa_row[xx];
-      const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 pa = UpRows<TILE>::pa(r, xx);
+      const float2 pb = UpRows<TILE>::template pb<C>(r, xx);
       const float2 uv = direct_uv(g, rt, dx[xx]);
       const float u = uv.x, v = uv.y;
       const float f = hw_exp2(-fmaf(u, u, v * v));
@@ -858,11 +875,13 @@ __device__ __forceinline__ void pair_rows_direct(const DirectGeo& g, float op, c
   }
 }
 
-// Moment form over rows [row0, row0 + nrows) for pairs with moment_span_ok (and not near-opaque).
-template <int C, bool ODDS, int TILE>
+// Moment form over rows [row0, row0 + nrows) (nrows >= 1) for pairs with moment_span_ok (and not near-opaque), into
+// a fresh s (its six moment sums are set here, its colour sums accumulate from zero). FULL: every row of the tile
+// (row0 = 0, nrows = TILE), one row at a time for the whole wave, so the row index and the loop's bookkeeping stay
+// in scalar registers. The first row is peeled: it sets the running sums instead of adding to zeros.
+template <int C, bool ODDS, int TILE, bool FULL>
 __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float op, const float4& col, int row0, int nrows,
-                                                  const float* s_pya, const TileCentres<TILE>& tc, const float4* s_pa,
-                                                  const float4* s_pb, PairSums<C>& s) {
+                                                  const UpRows<TILE>& ups, const TileCentres<TILE>& tc, PairSums<C>& s) {
   // the pair's centre (ey, ex): the splat centre clamped into the box of the tile's pixel centres; u, v there
   const float ey = fminf(fmaxf(g.gy, tc.py0), tc.py1), ex = fminf(fmaxf(g.gx, tc.px0), tc.px1);
   const float eyg = ey - g.gy, exg = ex - g.gx;
@@ -874,32 +893,44 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float op, co
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) lxp[xx] = tc.pxa[xx] - ex;
   // sum q {1, ly', ly'^2, lx' ly'} by rows; sum q {lx', lx'^2} from the column sums cq of q after the rows
-  float m0 = 0.f, my = 0.f, myy = 0.f, mxy = 0.f, cq[TILE];
-#pragma unroll
-  for (int xx = 0; xx < TILE; ++xx) cq[xx] = 0.f;
-#pragma nounroll
-  for (int yy = row0; yy < row0 + nrows; ++yy) {
-    const float ly = s_pya[yy] - ey;
+  float m0, my, myy, mxy, cq[TILE];
+  auto row = [&](int yy, auto first) {
+    constexpr bool FIRST = decltype(first)::value != 0;
+    const float* r = ups.row(yy);
+    const float ly = UpRows<TILE>::py(r) - ey;
     const float uy = fmaf(g.A, ly, up), vy = fmaf(g.Cc, ly, vp);
     const float a0 = fmaf(uy, uy, vy * vy), a1 = fmaf(uy, b2, vy * d2);
-    const float4* pa_row = s_pa + yy * up_stride<TILE>();
-    const float4* pb_row = s_pb + yy * up_stride<TILE>();
     float r0 = 0.f, r1 = 0.f;
 #pragma unroll
     for (int xx = 0; xx < TILE; ++xx) {
-      const float4 pa = pa_row[xx];
-      const float4 pb = C > 2 ? pb_row[xx] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 pa = UpRows<TILE>::pa(r, xx);
+      const float2 pb = UpRows<TILE>::template pb<C>(r, xx);
       const float lx = lxp[xx];
       const float f = hw_exp2(-fmaf(fmaf(a2, lx, a1), lx, a0));
       const float q = bwd_q<C, ODDS>(f, fmaf(-op, f, 1.f), col, pa, pb, s.gc);
       r0 += q;
-      cq[xx] += q;
+      cq[xx] = FIRST ? q : cq[xx] + q;
       r1 = fmaf(q, lx, r1);
     }
-    m0 += r0;
-    my = fmaf(ly, r0, my);
-    myy = fmaf(ly * ly, r0, myy);
-    mxy = fmaf(ly, r1, mxy);
+    if (FIRST) {
+      m0 = r0;
+      my = ly * r0;
+      myy = (ly * ly) * r0;
+      mxy = ly * r1;
+    } else {
+      m0 += r0;
+      my = fmaf(ly, r0, my);
+      myy = fmaf(ly * ly, r0, myy);
+      mxy = fmaf(ly, r1, mxy);
+    }
+  };
+  row(row0, IC<1>{});
+  if constexpr (FULL) {
+#pragma nounroll
+    for (int yy = 1; yy < TILE; ++yy) row(yy, IC<0>{});
+  } else {
+#pragma nounroll
+    for (int yy = row0 + 1; yy < row0 + nrows; ++yy) row(yy, IC<0>{});
   }
   float mx = 0.f, mxx = 0.f;
 #pragma unroll
@@ -914,30 +945,29 @@ __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float op, co
   const float suu = fmaf(g.A * g.A, myy, fmaf(2.f * g.A * g.B, mxy, g.B * g.B * mxx));
   const float svv = fmaf(g.Cc * g.Cc, myy, fmaf(2.f * g.Cc * g.D, mxy, g.D * g.D * mxx));
   const float suv = fmaf(g.A * g.Cc, myy, fmaf(fmaf(g.A, g.D, g.B * g.Cc), mxy, g.B * g.D * mxx));
-  s.q += m0;
-  s.qu += fmaf(up, m0, su);
-  s.qv += fmaf(vp, m0, sv);
-  s.quu += fmaf(up, fmaf(up, m0, 2.f * su), suu);
-  s.qvv += fmaf(vp, fmaf(vp, m0, 2.f * sv), svv);
-  s.quv += fmaf(up, fmaf(vp, m0, sv), fmaf(vp, su, suv));
+  s.q = m0;
+  s.qu = fmaf(up, m0, su);
+  s.qv = fmaf(vp, m0, sv);
+  s.quu = fmaf(up, fmaf(up, m0, 2.f * su), suu);
+  s.qvv = fmaf(vp, fmaf(vp, m0, 2.f * sv), svv);
+  s.quv = fmaf(up, fmaf(vp, m0, sv), fmaf(vp, su, suv));
 }
 
 // Per-pair sums over the pixels [j0, j0 + npx) of one row of the tile (lane = pair, lane-varying j0): the
 // remainder chunks that give a pair fewer pixels than a row.
 template <int C, bool ODDS, int TILE>
 __device__ __forceinline__ void pair_row_part(const DirectGeo& g, float op, const float4& col, int j0, int npx,
-                                              const float* s_pya, const float* s_pxa, const float4* s_pa,
-                                              const float4* s_pb, PairSums<C>& s) {
+                                              const UpRows<TILE>& ups, const float* s_pxa, PairSums<C>& s) {
   const int yy = j0 / TILE;
-  const RowTerms rt = row_terms(g, s_pya[yy] - g.gy);
+  const float* r = ups.row(yy);
+  const RowTerms rt = row_terms(g, UpRows<TILE>::py(r) - g.gy);
   for (int l = j0; l < j0 + npx; ++l) {
     const int xx = l - yy * TILE;
-    const int k = yy * up_stride<TILE>() + xx;
-    const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
     const float2 uv = direct_uv(g, rt, s_pxa[xx] - g.gx);
     const float u = uv.x, v = uv.y;
     const float f = hw_exp2(-fmaf(u, u, v * v));
-    bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, s_pa[k], pb, s);
+    bwd_acc<C, ODDS>(u, v, f, fmaf(-op, f, 1.f), col, UpRows<TILE>::pa(r, xx), UpRows<TILE>::template pb<C>(r, xx),
+                     s);
   }
 }
 
@@ -946,9 +976,8 @@ __device__ __forceinline__ void pair_row_part(const DirectGeo& g, float op, cons
 // of the lane-per-pair loops (a few near-opaque splats around their centre tile, and splats far smaller than
 // the tile).
 template <int C, bool ODDS, int TILE>
-__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, const float* s_pya,
-                                                    const float* s_pxa, const float4* s_pa, const float4* s_pb, int lane,
-                                                    float& op) {
+__device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ rec, int g, const UpRows<TILE>& ups,
+                                                    const float* s_pxa, int lane, float& op) {
   const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
   const float4 r0 = r4[0], r1 = r4[1], col = r4[2];
   const DirectGeo dg = direct_geo(r0, r4[3]);
@@ -957,12 +986,12 @@ __device__ __forceinline__ PairSums<C> careful_pair(const float* __restrict__ re
   PairSums<C> s;
   for (int l = lane; l < TILE * TILE; l += 64) {
     const int yy = l / TILE, xx = l % TILE;
-    const float2 uv = direct_uv(dg, row_terms(dg, s_pya[yy] - dg.gy), s_pxa[xx] - dg.gx);
+    const float* r = ups.row(yy);
+    const float2 uv = direct_uv(dg, row_terms(dg, UpRows<TILE>::py(r) - dg.gy), s_pxa[xx] - dg.gx);
     const float u = uv.x, v = uv.y;
     const float m = fmaf(u, u, v * v);
-    const int k = yy * up_stride<TILE>() + xx;
-    const float4 pb = C > 2 ? s_pb[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-    bwd_px_near<C, ODDS>(u, v, m, hw_exp2(-m), po, col, s_pa[k], pb, s);
+    bwd_px_near<C, ODDS>(u, v, m, hw_exp2(-m), po, col, UpRows<TILE>::pa(r, xx), UpRows<TILE>::template pb<C>(r, xx),
+                         s);
   }
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) xor_reduce<C>(s, d);
@@ -990,9 +1019,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     float* __restrict__ bg_part, SplitTable P) {
   static_assert(!SPLIT || (FIELDS && S == 1), "split items: FIELDS backward, one wave per item");
   constexpr int NP = TILE * TILE;
-  constexpr int RS = up_stride<TILE>();
-  __shared__ float4 s_pa[TILE * RS];
-  __shared__ float4 s_pb[TILE * RS];
+  __shared__ float4 s_up4[TILE * UpRows<TILE>::RF / 4];
+  const UpRows<TILE> ups{reinterpret_cast<float*>(s_up4)};
   __shared__ float s_pya[TILE], s_pxa[TILE];
   __shared__ int s_defer_w[S][128], s_mi_w[S][128];
   int chunk = 0, nsplit = 1;
@@ -1006,15 +1034,14 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int l = (int)threadIdx.x; l < NP; l += 64 * S) {
     const int yp = ta.ty * TILE + l / TILE, xp = ta.tx * TILE + l % TILE;
-    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 pb = make_float2(0.f, 0.f);
     if (yp < ta.H && xp < ta.W) {
       const int p = yp * ta.W + xp;
       pixel_upstream<C, FIELDS, UPS>(p, (size_t)L.pbase[ta.l] + p, bg, Tin, asum_in, fg_in, gout, dslog, dsa, dsac,
                                      pa, pb, bgp);
     }
-    const int k = (l / TILE) * RS + l % TILE;
-    s_pa[k] = pa;
-    s_pb[k] = pb;
+    ups.put(l / TILE, l % TILE, pa, pb);
   }
   if (!FIELDS && bg_part) {   // the tile's partial sums, waves added in wave order
     __shared__ float s_bgw[S][kMaxC];
@@ -1033,7 +1060,9 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   // the tile's pixel centres (render_triton.py:455-456): rows and columns in LDS, columns also wave-uniform
   const float fH = (float)ta.H, fW = (float)ta.W;
   if (threadIdx.x < TILE) {
-    s_pya[lane] = ((float)(ta.ty * TILE + lane) + 0.5f) / fH;
+    const float pyc = ((float)(ta.ty * TILE + lane) + 0.5f) / fH;
+    s_pya[lane] = pyc;
+    ups.base[lane * UpRows<TILE>::RF + 4 * TILE] = pyc;
     s_pxa[lane] = ((float)(ta.tx * TILE + lane) + 0.5f) / fW;
   }
   __syncthreads();
@@ -1047,7 +1076,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) tc.pxa[xx] = uniform_f(s_pxa[xx]);
   const float py0 = tc.py0, px0 = tc.px0, py1 = tc.py1, px1 = tc.px1;
-  const float rH = uniform_f(1.f / fH), rW = uniform_f(1.f / fW);
+  const float rH = uniform_f(hw_rcp(fH)), rW = uniform_f(hw_rcp(fW));   // for near_pixel_m's bound only
   int g0 = starts[t], g1 = starts[t + 1];
   if (SPLIT) {   // the item's chunk: whole passes of 64 pairs where the tile's list allows
     const int len = (((g1 - g0 + nsplit - 1) / nsplit) + 63) & ~63;
@@ -1086,8 +1115,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     for (unsigned long long nm = __ballot(near); nm; nm &= nm - 1) {
       const int j = __builtin_ctzll(nm);
       float opj;
-      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), s_pya, s_pxa, s_pa,
-                                                          s_pb, lane, opj);
+      const PairSums<C> cs = careful_pair<C, ODDS, TILE>(rec, __builtin_amdgcn_readlane(g, j), ups, s_pxa, lane, opj);
       if (lane == 0) store_pair<C>(psum + (size_t)__builtin_amdgcn_readlane(q, j) * pair_rec<C>(), cs, opj);
     }
     const unsigned long long dm = __ballot(defer), mm = __ballot(mom);
@@ -1117,14 +1145,17 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     if (MOM && npx >= TILE) {   // whole rows (uniform branch; the loops' bounds are wave-uniform)
       PairGeo pg = pair_geo(r0, r1);
       mute_pair(!act, pg);
-      pair_rows_moments<C, ODDS, TILE>(pg, op, col, sub * (npx / TILE), npx / TILE, s_pya, tc, s_pa, s_pb, s);
+      if (TILE <= 8 && lg == 0)   // one lane per pair: every row
+        pair_rows_moments<C, ODDS, TILE, true>(pg, op, col, 0, TILE, ups, tc, s);
+      else
+        pair_rows_moments<C, ODDS, TILE, false>(pg, op, col, sub * (npx / TILE), npx / TILE, ups, tc, s);
     } else {
       DirectGeo dg = direct_geo(r0, r4[3]);
       mute_direct(!act, dg);
       if (npx >= TILE)
-        pair_rows_direct<C, ODDS, TILE>(dg, op, col, sub * (npx / TILE), npx / TILE, s_pya, tc, s_pa, s_pb, s);
+        pair_rows_direct<C, ODDS, TILE>(dg, op, col, sub * (npx / TILE), npx / TILE, ups, tc, s);
       else
-        pair_row_part<C, ODDS, TILE>(dg, op, col, sub * npx, npx, s_pya, s_pxa, s_pa, s_pb, s);
+        pair_row_part<C, ODDS, TILE>(dg, op, col, sub * npx, npx, ups, s_pxa, s);
     }
     for (int d = 1; d < Lp; d <<= 1) xor_reduce<C>(s, d);
     if (act && sub == 0) store_pair<C>(psum + (size_t)pair_q[i] * pair_rec<C>(), s, op);
@@ -1338,8 +1369,8 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
                                                   const float* __restrict__ Tin, const float* __restrict__ asum_in,
                                                   const float* __restrict__ fg_in, const float* __restrict__ gout,
                                                   float* __restrict__ acc) {
-  __shared__ float4 s_pa[64], s_pb[64];
-  __shared__ float2 s_pyx[64];
+  __shared__ float4 s_pa[64];
+  __shared__ float2 s_pb[64], s_pyx[64];
   const int lane = threadIdx.x;
   const int g = blockIdx.x * 64 + lane;
   const int gs = g < N ? g : N - 1;
@@ -1351,8 +1382,8 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
   float bgp[kMaxC] = {0.f, 0.f, 0.f, 0.f};
   for (int p0 = 0; p0 < P; p0 += 64) {
     const int p = p0 + lane;
-    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
-    float2 pyx = make_float2(0.f, 0.f);
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 pb = make_float2(0.f, 0.f), pyx = pb;
     if (p < P) {
       pixel_upstream<C, false, false>(p, 0, bg, Tin, asum_in, fg_in, gout, nullptr, nullptr, nullptr, pa, pb, bgp);
       pyx = make_float2(pyv[p], pxv[p]);
@@ -1367,7 +1398,7 @@ __global__ __launch_bounds__(64) void k_bwd_exact(const float* __restrict__ rec,
       const float2 q = s_pyx[j];
       const float dy = q.x - gy, dx = q.y - gx;
       bwd_px<C, false>(fmaf(A, dy, B * dx), fmaf(Cc, dy, D * dx), po, col, s_pa[j],
-                               C > 2 ? s_pb[j] : make_float4(0.f, 0.f, 0.f, 0.f), s);
+                               C > 2 ? s_pb[j] : make_float2(0.f, 0.f), s);
     }
   }
   if (g >= N) return;
