@@ -441,16 +441,11 @@ def pair_classes(name, TILE=8, cutoff=3.0):
     sy, sx = s64[g, 0], s64[g, 1]
     A, B, Cc, D = k * cs / sy, k * sn / sy, -k * sn / sx, k * cs / sx
     gy, gx = m64[g, 0], m64[g, 1]
-    u0 = A * (py0 - gy) + B * (px0 - gx)
-    v0 = Cc * (py0 - gy) + D * (px0 - gx)
-    Ly, Lx = py1 - py0, px1 - px0
-
-    def interval_dist(c0, a, b):
-        lo = c0 + np.minimum(a, 0) + np.minimum(b, 0)
-        hi = c0 + np.maximum(a, 0) + np.maximum(b, 0)
-        return np.maximum(np.maximum(lo, -hi), 0)
-
-    du, dv = interval_dist(u0, A * Ly, B * Lx), interval_dist(v0, Cc * Ly, D * Lx)
+    cy, cx = 0.5 * (py1 - py0), 0.5 * (px1 - px0)
+    uc = A * (py0 + cy - gy) + B * (px0 + cx - gx)   # u, v at the middle of the tile's pixel centres
+    vc = Cc * (py0 + cy - gy) + D * (px0 + cx - gx)
+    su, sv = np.abs(A) * cy + np.abs(B) * cx, np.abs(Cc) * cy + np.abs(D) * cx   # their half-spans over the box
+    du, dv = np.maximum(np.abs(uc) - su, 0), np.maximum(np.abs(vc) - sv, 0)
     box_m = du * du + dv * dv
     ny = (np.clip(np.floor(gy * H), 0, H - 1) + 0.5) / H - gy
     nx = (np.clip(np.floor(gx * W), 0, W - 1) + 0.5) / W - gx
@@ -461,8 +456,7 @@ def pair_classes(name, TILE=8, cutoff=3.0):
     lop = np.log2(np.maximum(op[g], 1e-45))
     near = ~negl & (op[g] > 0.99) & ((dy * dy + dx * dx) * k * k <
                                      np.maximum(sy, sx) ** 2 * (lop - np.log2(0.99) + 1e-3))
-    cy, cx = 0.5 * Ly, 0.5 * Lx
-    span = np.maximum(np.abs(A) * cy + np.abs(B) * cx, np.abs(Cc) * cy + np.abs(D) * cx)
+    span = np.maximum(su, sv)
     direct = ~negl & ~near & (span > 8.0)
     moment = ~negl & ~near & ~direct
     out = {"pairs": tot, "share": {c: round(float(m.mean()), 5) for c, m in

@@ -770,19 +770,17 @@ constexpr float kCullLog2 = 30.f;
 // centre position need not be the exact float32 pixel centre for a cut).
 __device__ __forceinline__ float near_pixel_m(float gy, float gx, float A, float B, float Cc, float D, float fH,
                                               float fW, float rH, float rW) {
-  const float ny = fmaf(fminf(fmaxf(floorf(gy * fH), 0.f), fH - 1.f) + 0.5f, rH, -gy);
-  const float nx = fmaf(fminf(fmaxf(floorf(gx * fW), 0.f), fW - 1.f) + 0.5f, rW, -gx);
+  const float ny = fmaf(__builtin_amdgcn_fmed3f(floorf(gy * fH), 0.f, fH - 1.f) + 0.5f, rH, -gy);
+  const float nx = fmaf(__builtin_amdgcn_fmed3f(floorf(gx * fW), 0.f, fW - 1.f) + 0.5f, rW, -gx);
   const float u = fmaf(A, ny, B * nx), v = fmaf(Cc, ny, D * nx);
   return fmaf(u, u, v * v);
 }
 
-// Lower bound of u^2 + v^2 over ly in [0, Ly], lx in [0, Lx] with u = u0 + A ly + B lx, v = v0 + Cc ly + D lx.
-__device__ __forceinline__ float box_min_m(float u0, float v0, float A, float B, float Cc, float D, float Ly,
-                                           float Lx) {
-  const float ua = A * Ly, ub = B * Lx, va = Cc * Ly, vb = D * Lx;
-  const float ulo = u0 + fminf(ua, 0.f) + fminf(ub, 0.f), uhi = u0 + fmaxf(ua, 0.f) + fmaxf(ub, 0.f);
-  const float vlo = v0 + fminf(va, 0.f) + fminf(vb, 0.f), vhi = v0 + fmaxf(va, 0.f) + fmaxf(vb, 0.f);
-  const float du = fmaxf(fmaxf(ulo, -uhi), 0.f), dv = fmaxf(fmaxf(vlo, -vhi), 0.f);
+// Lower bound of u^2 + v^2 over the box of the tile's pixel centres, from u, v at the box's middle (uc, vc) and
+// their half-spans over the box (su, sv): u and v are affine in the pixel position, so over the box u lies in
+// [uc - su, uc + su] and v in [vc - sv, vc + sv].
+__device__ __forceinline__ float box_min_m(float uc, float vc, float su, float sv) {
+  const float du = fmaxf(fabsf(uc) - su, 0.f), dv = fmaxf(fabsf(vc) - sv, 0.f);
   return fmaf(du, du, dv * dv);
 }
 
@@ -803,11 +801,13 @@ __device__ __forceinline__ float box_min_m(float u0, float v0, float A, float B,
 // Pairs with a span above kMomentSpan take the direct form.
 constexpr float kMomentSpan = 8.f;
 
+// Half-spans of u and v over the box of the tile's pixel centres (half extents cy, cx) for the rotation rows
+// (A, B), (Cc, D); the moment form takes pairs whose larger half-span is at most kMomentSpan.
 template <int TILE>
-__device__ __forceinline__ bool moment_span_ok(const PairGeo& g, const TileCentres<TILE>& tc) {
-  return fmaxf(fmaf(fabsf(g.A), tc.cy, fabsf(g.B) * tc.cx), fmaf(fabsf(g.Cc), tc.cy, fabsf(g.D) * tc.cx)) <=
-         kMomentSpan;
+__device__ __forceinline__ float2 half_spans(float A, float B, float Cc, float D, const TileCentres<TILE>& tc) {
+  return make_float2(fmaf(fabsf(A), tc.cy, fabsf(B) * tc.cx), fmaf(fabsf(Cc), tc.cy, fabsf(D) * tc.cx));
 }
+__device__ __forceinline__ bool moment_span_ok(float2 hs) { return fmaxf(hs.x, hs.y) <= kMomentSpan; }
 
 // Geometry of one pair in the direct form: the splat centre, the rotation (cs, sn) and the whitening factors
 // ky = k / sy, kx = k / sx (the decode pass's own values), so that u = ky (cs dy + sn dx) and
@@ -883,7 +883,7 @@ template <int C, bool ODDS, int TILE, bool FULL>
 __device__ __forceinline__ void pair_rows_moments(const PairGeo& g, float op, const float4& col, int row0, int nrows,
                                                   const UpRows<TILE>& ups, const TileCentres<TILE>& tc, PairSums<C>& s) {
   // the pair's centre (ey, ex): the splat centre clamped into the box of the tile's pixel centres; u, v there
-  const float ey = fminf(fmaxf(g.gy, tc.py0), tc.py1), ex = fminf(fmaxf(g.gx, tc.px0), tc.px1);
+  const float ey = __builtin_amdgcn_fmed3f(g.gy, tc.py0, tc.py1), ex = __builtin_amdgcn_fmed3f(g.gx, tc.px0, tc.px1);
   const float eyg = ey - g.gy, exg = ex - g.gx;
   const float up = fmaf(g.A, eyg, g.B * exg);
   const float vp = fmaf(g.Cc, eyg, g.D * exg);
@@ -1076,6 +1076,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
 #pragma unroll
   for (int xx = 0; xx < TILE; ++xx) tc.pxa[xx] = uniform_f(s_pxa[xx]);
   const float py0 = tc.py0, px0 = tc.px0, py1 = tc.py1, px1 = tc.px1;
+  const float pym = py0 + tc.cy, pxm = px0 + tc.cx;   // the middle of the box of the tile's pixel centres
   const float rH = uniform_f(hw_rcp(fH)), rW = uniform_f(hw_rcp(fW));   // for near_pixel_m's bound only
   int g0 = starts[t], g1 = starts[t + 1];
   if (SPLIT) {   // the item's chunk: whole passes of 64 pairs where the tile's list allows
@@ -1094,7 +1095,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   // (summed by careful_pair at once), small
   // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi for a moment
   // pass). Only queued pairs occupy lanes of the row loops. The classification bounds u and v over the tile from
-  // their values at the tile's first pixel centre (float64 offsets, rounded once).
+  // their values at the middle of the tile's pixel centres and their half-spans (which also decide the form).
   int nmain = 0, ndefer = 0;
   auto classify = [&](int c0) {
     const int i = c0 + lane;
@@ -1103,12 +1104,12 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     const float4* r4 = reinterpret_cast<const float4*>(rec) + (size_t)g * 4;
     const float4 r0 = r4[0], r1 = r4[1];
     const float2 sc = *reinterpret_cast<const float2*>(rec + (size_t)g * kRec + R_SY);
-    const float2 uv = offsets_at(py0, px0, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
-    const PairGeo pg = pair_geo(r0, r1);
-    const bool negl = act && box_min_m(uv.x, uv.y, r0.z, r0.w, r1.x, r1.y, py1 - py0, px1 - px0) >
+    const float2 uv = offsets_at(pym, pxm, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
+    const float2 hs = half_spans<TILE>(r0.z, r0.w, r1.x, r1.y, tc);
+    const bool negl = act && box_min_m(uv.x, uv.y, hs.x, hs.y) >
                                  kCullLog2 + near_pixel_m(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, fH, fW, rH, rW);
     const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
-    const bool defer = act && !negl && !near && !moment_span_ok<TILE>(pg, tc);
+    const bool defer = act && !negl && !near && !moment_span_ok(hs);
     const bool mom = act && !negl && !near && !defer;
     const int q = (negl || near) ? pair_q[i] : 0;
     if (negl) store_pair<C>(psum + (size_t)q * pair_rec<C>(), PairSums<C>(), 1.f);
