@@ -726,6 +726,8 @@ __device__ __forceinline__ void mute_pair(bool mute, PairGeo& g) {
 template <int TILE>
 struct UpRows {
   static constexpr int RF = 6 * TILE + 4;   // floats per row
+  static_assert(RF % 4 == 0, "rows start 16-byte aligned (float4 reads)");
+  static_assert((4 * TILE + 4) % 2 == 0, "the float2 part starts 8-byte aligned");
   float* base;
   __device__ __forceinline__ const float* row(int yy) const { return base + yy * RF; }
   __device__ __forceinline__ static float4 pa(const float* r, int xx) {
