@@ -12,7 +12,8 @@ Also reported: forward-only, the render_alpha_octave entry point, t
 ms), per-stage event times (back-to-back launches), the device time of the step's kernel chain, per-step
 median / p10 / p90, the roofline of the dominant kernel from HIP events that its launches record at their own
 start and end in fwd+bwd steps, and the reference's CPU renderer (render.py math) on the host cores: a bounded
-band of the same frame, and configs[0] (64x64, 1,024 splats) as BASELINE.md plans it.
+band of the same frame, and configs[0] (64x64, 1,024 splats, seed 0: 3 warm-ups and 20 timed runs, median, p10
+and p90).
 """
 
 from __future__ import annotations
@@ -496,7 +497,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              f"multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+              f"the multi-GPU sharding of this path is a design only, not built", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no HIP device", file=sys.stderr)

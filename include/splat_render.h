@@ -16,7 +16,8 @@
  *   Pixel fields are row-major: [P] or [P,C] with P = H*W, p = y*W + x.
  *
  * The reference (bigwolfeman/gaussian-2d-splat-encoder) is Python + Triton; each function below replaces
- * the cited part of gaussian_splat_encoder/render_triton.py. A ctypes binding is in INTEGRATION.md.
+ * the cited part of gaussian_splat_encoder/render_triton.py. The package's ctypes binding is
+ * gaussian-2d-splat-encoder_amd/gaussian_splat_encoder/_lib.py.
  */
 #ifndef SPLAT_RENDER_H
 #define SPLAT_RENDER_H
