@@ -69,6 +69,20 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Sum over the 64 lanes of a wave (every lane active), in a fixed order: within each row of 16 lanes by DPP
+// (pairs, quads, half-rows, rows: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror; after the
+// first two steps every lane of a quad holds the quad's sum, so each mirror adds the other quad or half-row), then
+// the four rows' sums read from lanes 0, 16, 32 and 48 as (r0 + r1) + (r2 + r3). No LDS traffic, unlike shuffles.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  const int b = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) + __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+
 // A value every lane of the wave holds, as a wave-uniform (scalar) value.
 __device__ __forceinline__ float uniform_f(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
@@ -1049,7 +1063,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     __shared__ float s_bgw[S][kMaxC];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const float v = wave_sum(bgp[c]);
+      const float v = wave_sum_dpp(bgp[c]);
       if (lane == 0) s_bgw[wid][c] = v;
     }
     __syncthreads();
