@@ -713,10 +713,11 @@ def _forward_cull_fields(mu, scale, color, opacity, theta, H, W, TILE=8, cutoff=
 
 
 def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv, with_maps=True,
-                    scale_is_log=False):
+                    scale_is_log=False, plan=None):
     """Fused multi-level forward (render_triton.py:879-980 without the per-group torch glue): one binning
     over every level, FIELDS renders of the coarse levels into packed fields, then the level-0 composite
-    adds their bilinear upsamples. Returns out [B,P,C], (T, asum unclamped, fg), bins."""
+    adds their bilinear upsamples. Returns out [B,P,C], (T, asum unclamped, fg), bins. plan: a _LevelsBwdPlan to
+    prepare for the backward (its buffers are allocated while the pair count is read back)."""
     B, N, C = color.shape
     P = H * W
     dev = mu.device
@@ -747,6 +748,8 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
         lt_spec = _speculated_levels(bins)
         mask_spec = _mask_of(lt_spec)
         launch(0, lt_spec, mask_spec)
+        if plan is not None:         # the backward's buffers, allocated while the GPU works towards the count
+            plan.allocate(bins, B, N, C, dev, lib, bins.pending.cap)
         redone = _finish(bins)
         lt, held = bins.level_tot_b[0], bins.level_mask(0)
         # launched again when the pair phase was redone, when a level holding pairs was left out, or when the
@@ -757,6 +760,8 @@ def _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, ma
     else:
         for b in range(B):
             launch(b, bins.level_tot_b[b], bins.level_mask(b))
+    if plan is not None:
+        plan.bind(bins, B, N, C, dev, lib, stream, odd, (bgf, T, asum, fg))
     return out, (T, asum, fg), bins
 
 
@@ -914,6 +919,99 @@ def _backward_levels(grad_out, color, bg, has_theta, T, asum, fg, bins, odds, lo
     return g_mu, g_scale, g_col, g_op, g_bg, g_th
 
 
+class _LevelsBwdPlan:
+    """_backward_levels prepared by its forward: the gradient outputs, the pixel upstream fields, the upsample
+    adjoint's workspace, the per-pair sums and the level-0 background partials (allocated while the forward waits
+    for the pair count), and the argument lists of the backward's launches per image, complete but for the
+    upstream gradient's pointer. The backward then runs its C-ABI calls only (the same launches, in the same order,
+    as _backward_levels)."""
+
+    __slots__ = ("grads", "dS", "adj", "adj_n", "sums", "ns", "cap", "calls", "lsc", "has_th", "keep")
+
+    def __init__(self, has_th, lsc=None):
+        self.has_th = has_th
+        self.lsc = _f32(lsc)   # the raw log-scales as the reduction reads them (kept alive here)
+        self.cap = -1
+        self.sums = None
+
+    def allocate(self, bins, B, N, C, dev, lib, cap):
+        self.grads = _grads_bg_out(B, N, C, dev, self.has_th)
+        L = bins.n_levels
+        self.dS = _fields_buffers(bins.npix if L > 1 else bins.H * bins.W, C, dev)   # reused across the batch
+        self.adj, self.adj_n = None, 0
+        if L > 1:
+            key = (C, bins.H, bins.W, bins.TILE, _lv_key(bins.lv))
+            nb = _ADJ_WS.get(key)
+            if nb is None:
+                lvr = _lib.ctypes.byref(bins.lv)
+                nb = _ADJ_WS[key] = lib.splat_upsample_adjoint_workspace_bytes(C, bins.H, bins.W, bins.TILE, lvr)
+            self.adj = _ws(nb, dev)
+            self.adj_n = self.adj.numel()
+        ns = _SUMS_FLOATS.get(cap)
+        if ns is None:
+            if len(_SUMS_FLOATS) > 1024:
+                _SUMS_FLOATS.clear()
+            ns = _SUMS_FLOATS[cap] = (lib.splat_pair_sums_bytes(max(cap, 1)) // 4 + 3) & ~3
+        self.sums = torch.empty(B * ns + C * bins.ntiles0, device=dev)   # per-image sums, then the partials
+        self.ns = ns
+        self.cap = cap
+
+    def bind(self, bins, B, N, C, dev, lib, stream, odd, comp):
+        tots = bins.tot_b
+        if self.sums is None or max(tots) > self.cap:
+            self.allocate(bins, B, N, C, dev, lib, max(tots))
+        g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
+        bgf, T, asum, fg = comp
+        self.keep = bgf   # the kernels read the background through its pointer
+        L = bins.n_levels
+        lvr = None if bins.lv is None else _lib.ctypes.byref(bins.lv)
+        ds = tuple(t.data_ptr() for t in self.dS)
+        sums0 = self.sums.data_ptr()
+        bgp = sums0 + 4 * B * self.ns
+        nt0 = bins.ntiles0
+        self.calls = []
+        for b in range(B):
+            mask, lt = bins.level_mask(b), bins.level_tot_b[b]
+            sb = sums0 + 4 * self.ns * b
+            head = (bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), bins.p(b, "pq"), tots[b], C, bins.H,
+                    bins.W, bins.TILE, FLAG_UPS | odd | _wide(bins.TILE, nt0, lt[0]), lvr, 0, 1, mask, _bptr(bgf, b),
+                    _bptr(T, b), _bptr(asum, b), _bptr(fg, b))
+            tail = (*ds, sb, bgp, stream)
+            adj = split = None
+            if mask & ~1:
+                adj = (C, bins.H, bins.W, bins.TILE, lvr, mask, *ds, ptr(self.adj), self.adj_n, stream)
+                split = (bins.p(b, "rec"), bins.p(b, "gid"), bins.p(b, "starts"), bins.p(b, "pq"), tots[b], C, bins.H,
+                         bins.W, bins.TILE, odd, lvr, 1, L, mask & ~1, _level_splits(bins, lt, mask & ~1), *ds, sb,
+                         stream)
+            sl = lambda t: None if N == 0 else _bptr(t, b)
+            red = (bins.p(b, "rec") if N else None, bins.p(b, "off") if N else None, None, tots[b], N, C, sb, bgp, nt0,
+                   sl(self.lsc), sl(g_mu), sl(g_scale), sl(g_th), sl(g_op), sl(g_col), _bptr(g_bg, b), stream)
+            self.calls.append((head, tail, adj, split, red))
+
+    def run(self, lib, go):
+        """The launches per image with the upstream gradient go [B,P,C] (float32, contiguous per image); returns the
+        gradients (the plan then holds none)."""
+        img = go.shape[1] * go.shape[2]
+        g0 = go.data_ptr()
+        for b, (head, tail, adj, split, red) in enumerate(self.calls):
+            ev = kernel_timer.record("bwd")
+            try:
+                check(lib.splat_render_bwd(*head, g0 + 4 * img * b, *tail), "splat_render_bwd")
+                if adj is not None:
+                    check(lib.splat_upsample_adjoint(*adj), "splat_upsample_adjoint")
+                    check(lib.splat_render_fields_split_bwd(*split), "splat_render_fields_split_bwd")
+            finally:
+                kernel_timer.close("bwd", ev)
+            ev = kernel_timer.record("reduce")
+            try:
+                check(lib.splat_reduce_pairs(*red), "splat_reduce_pairs")
+            finally:
+                kernel_timer.close("reduce", ev)
+        g_mu, g_scale, g_col, g_op, g_th, g_bg = self.grads
+        self.grads = self.sums = self.keep = self.dS = self.adj = None
+        return g_mu, g_scale, g_col, g_op, g_bg, g_th
+
+
 class _AlphaRenderCull(torch.autograd.Function):
     """render_triton.py:813-833. Inputs (mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, odds).
     scale_is_log=True: `scale` is the fp32 raw log-scale, activated inside the binning's decode pass, and its
@@ -997,9 +1095,12 @@ class _AlphaRenderLevels(torch.autograd.Function):
     @staticmethod
     def forward(ctx, mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff, max_pairs, odds, lv,
                 scale_is_log=False):
+        grad = any(ctx.needs_input_grad[:6])
+        N = color.shape[1]
+        plan = _LevelsBwdPlan(theta is not None, scale if scale_is_log else None) if grad and N > 0 else None
         out, (T, asum, fg), bins = _forward_levels(mu, scale, color, opacity, bg, theta, H, W, TILE, cutoff,
-                                                   max_pairs, odds, lv, any(ctx.needs_input_grad[:6]),
-                                                   scale_is_log=scale_is_log)
+                                                   max_pairs, odds, lv, grad, scale_is_log=scale_is_log, plan=plan)
+        ctx.plan = plan
         ctx.has_theta = theta is not None
         ctx.odds = odds
         ctx.tiles = bins
@@ -1015,8 +1116,12 @@ class _AlphaRenderLevels(torch.autograd.Function):
         T, asum, fg = ctx.fwd
         B, C, H, W = grad_out.shape
         go = grad_out.permute(0, 2, 3, 1).reshape(B, H * W, C)   # a view when the gradient has the image's layout
-        g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(go, color, bg, ctx.has_theta, T, asum, fg,
-                                                                  ctx.tiles, ctx.odds, log_scale)
+        plan, ctx.plan = ctx.plan, None
+        if plan is not None:
+            g_mu, g_scale, g_col, g_op, g_bg, g_th = plan.run(_lib.load(), _f32(go))
+        else:
+            g_mu, g_scale, g_col, g_op, g_bg, g_th = _backward_levels(go, color, bg, ctx.has_theta, T, asum, fg,
+                                                                      ctx.tiles, ctx.odds, log_scale)
         return (g_mu, g_scale, g_col, g_op, g_bg, g_th) + (None,) * 8
 
 
