@@ -106,7 +106,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_count(
     float2 s = reinterpret_cast<const float2*>(scale)[g];   // (sy, sx), or raw log-scales with act
     if (act) s = make_float2(activate_scale(s.x), activate_scale(s.y));
     float sn = 0.f, cs = 1.f;
-    if (theta) sincosf(theta[g], &sn, &cs);
+    if (theta) {   // the float32 values nearest cos and sin of the float32 angle (double sincos, rounded once)
+      double sd, cd;
+      sincos((double)theta[g], &sd, &cd);
+      sn = (float)sd;
+      cs = (float)cd;
+    }
     const float ky = kWhiten / s.x, kx = kWhiten / s.y;
     float4 col = make_float4(0.f, 0.f, 0.f, 0.f);
     col.x = color[(size_t)g * C];

@@ -35,6 +35,19 @@ def _p(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
+class rot32:
+    """Within this context the oracle rounds each splat's cos and sin to the nearest float32 values (the precision
+    in which the reference and the HIP decode hold the rotation); outside it they stay float64."""
+
+    def __enter__(self):
+        lib().orc_set_rot32(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_rot32(0)
+        return False
+
+
 def _f32(a):
     return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
 

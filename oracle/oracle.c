@@ -77,13 +77,24 @@ typedef struct {
     double* sn;           /* [N] sin(theta) */
 } orc_splats;
 
+/* The splats' rotation: cos and sin of the float32 angle in float64 (the default), or, after orc_set_rot32(1), each
+ * rounded to the nearest float32 value: the precision in which the reference holds its rotation (cos and sin of a
+ * float32 angle in float32 arithmetic, render_triton.py:95-96, :480-481) and in which the HIP decode stores it. */
+static int g_rot32 = 0;
+void orc_set_rot32(int on) { g_rot32 = on; }
+
 static void trig_tables(orc_splats* s, int N) {
     s->cs = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
     s->sn = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
     for (int g = 0; g < N; ++g) {
         const double th = s->theta ? (double)s->theta[g] : 0.0;
-        s->cs[g] = s->theta ? cos(th) : 1.0;
-        s->sn[g] = s->theta ? sin(th) : 0.0;
+        double c = s->theta ? cos(th) : 1.0, sn = s->theta ? sin(th) : 0.0;
+        if (g_rot32) {
+            c = (double)(float)c;
+            sn = (double)(float)sn;
+        }
+        s->cs[g] = c;
+        s->sn[g] = sn;
     }
 }
 static void trig_free(orc_splats* s) { free(s->cs); free(s->sn); }

@@ -7,6 +7,8 @@
   the glue, then the C oracle's fields backward per level).
 """
 
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -218,12 +220,19 @@ def composed_oracle(mu, sc, col, op, bg, th, H, W, TILE, lv, odds, gout, cutoff=
 
 
 def run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol=IMG_TOL, grad_tol=GRAD_REL_TOL,
-               want_grads=False, per_splat=True, bwd_on_device_fwd=False):
+               want_grads=False, per_splat=True, bwd_on_device_fwd=False, rot32=True):
     """Fused level render of one batch against composed_oracle: the image, every gradient tensor and, with
     per_splat, every gradient component of every splat against that splat's own scale (check_per_splat).
     bwd_on_device_fwd: the gradients are held against the oracle's backward from the device forward's T, S_a and
-    fg (the image still against the oracle's own forward). Returns the bins, and with want_grads also the device
-    gradients by name and the oracle's."""
+    fg (the image still against the oracle's own forward). rot32: as in test_gpu_render.run_case. Returns the bins,
+    and with want_grads also the device gradients by name and the oracle's."""
+    with (c_oracle.rot32() if rot32 else contextlib.nullcontext()):
+        return _run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol, grad_tol, want_grads,
+                           per_splat, bwd_on_device_fwd)
+
+
+def _run_levels(mu, ls, col, op, bg, th, H, W, TILE, lv, odds, seed, img_tol, grad_tol, want_grads, per_splat,
+                bwd_on_device_fwd):
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
     out, (T, asum, fg), bins = RH._forward_levels(mu, sc, col, op, bg, th, H, W, TILE, 3.0, None, odds, lv)

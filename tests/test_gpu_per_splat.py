@@ -8,7 +8,9 @@ every splat is held to 1e-4 of that splat's own scale for the component (the flo
 magnitudes, render_triton.py:688-710), beside the tensor-wide bar, on scenes built around that limit:
 * splats whose smaller axis puts their spans over an 8 x 8 tile at 5 to 11 (sigma about 0.3 to 0.7 px);
 * splats far smaller than a pixel (direct form);
-* the benchmark frame through the octave render (alpha and odds).
+* the benchmark frame through the octave render (alpha and odds);
+* a thin rotated splat (0.06 x 0.67 px), against the oracle with the float32 rotation the reference and the device
+  hold, and the size of the float32 rotation's own effect against a float64 rotation.
 Every run_case / run_levels call of the other GPU tests applies the same per-splat check.
 """
 
@@ -72,3 +74,29 @@ def test_c2_octave_per_splat(dev, odds):
     s = synth.config("c2").to(dev)
     run_levels(s.mu, s.log_scale, s.color, s.opacity, s.bg, s.theta, s.H, s.W, 8, _lib.SplatLevels(1, 6, 8.0, 0, 0, 0),
                odds, seed=80)
+
+
+def test_float32_rotation_of_a_thin_splat(dev):
+    """A random scene (seed 50039; FIELDS, odds) holding splat 617, 0.06 x 0.67 px rotated by 2.23 rad: an aspect of
+    11.5 and far thinner than a pixel, so its pairs take the direct form. The device holds every splat's cos and
+    sin as the nearest float32 values (render_triton.py:95-96 holds them in float32 as well). Against the oracle
+    with the same float32 rotation every component of every splat meets the per-splat bar with a wide margin.
+    Against the float64 rotation the float32 rounding of that splat's cos and sin alone moves its theta gradient by
+    about 1e-4 of its scale: the oracle's own float32 and float64 rotations differ by as much, and the device's
+    difference from the float64-rotation oracle stays within that."""
+    from _scenes import per_splat_errors
+    from _gpu_util import random_scene
+    H, W = 186, 44
+    scene = random_scene(626, H, W, seed=50039, dev=dev, ls_mean_px=0.3713114842386114,
+                         ls_std=1.2326931862574066, op_max=0.5, theta=True)
+    got, ref32 = run_case(*scene, H, W, 8, True, True, seed=39, rot32=True)   # per-splat bar inside
+    got_np = {k: None if v is None else np_(v[0]) for k, v in got.items()}
+    e32 = per_splat_errors(got_np, ref32)
+    assert max(e for e, _ in e32.values()) < 1e-5, e32
+    _, ref64 = run_case(*scene, H, W, 8, True, True, seed=39, per_splat=False, rot32=False)
+    dev_th, at_dev = per_splat_errors(got_np, ref64)["theta"]
+    rot_th, at_rot = per_splat_errors({"theta": ref32["theta"]}, ref64)["theta"]
+    print(f"theta per-splat: device vs float64 rotation {dev_th:.2e} (splat {at_dev}), float32 vs float64 rotation "
+          f"in the oracle {rot_th:.2e} (splat {at_rot})", flush=True)
+    assert rot_th > 3e-5            # the scene exercises the rounding of a thin splat's rotation
+    assert dev_th <= rot_th + 1e-5  # and the device's difference from the float64 rotation is that rounding

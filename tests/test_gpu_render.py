@@ -1,6 +1,8 @@
 """Kernel-level parity of the per-tile forward and backward against the float64 C oracle over the same
 (bit-exact) pair lists: images within 1e-5 max-abs, gradients within 1e-4 relative."""
 
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -18,13 +20,22 @@ def oracle_pairs(mu, sc, H, W, TILE, cutoff=3.0):
 
 
 def run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed=0, check_bwd=True, per_splat=True,
-             bwd_on_device_fwd=False):
+             bwd_on_device_fwd=False, rot32=True):
     """Forward (and backward) of one batch against the C oracle over the oracle's pair list. Gradients are held
     to GRAD_REL_TOL of each tensor's largest magnitude and, with per_splat, every component of every splat to
     PER_SPLAT_TOL of that splat's own scale for it (the oracle's 'mag'). bwd_on_device_fwd (composite renders):
     the oracle's backward starts from the device forward's T, asum and fg instead of its own, so that the
     gradients check the backward alone (float32 forward rounding can decide them where 1 - T is below float32
-    resolution). Returns the device gradients by name and the oracle's (None without the backward)."""
+    resolution). rot32 (the default): the oracle holds each splat's cos and sin as the nearest float32 values, as
+    the reference and the device do (rot32=False: in float64; for an elongated splat far thinner than a pixel the
+    rounding of its rotation alone then moves its theta gradient by up to ~2e-4 of its scale, see
+    test_gpu_per_splat.py). Returns the device gradients by name and the oracle's (None without the backward)."""
+    with (c_oracle.rot32() if rot32 else contextlib.nullcontext()):
+        return _run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed, check_bwd, per_splat,
+                         bwd_on_device_fwd)
+
+
+def _run_case(mu, ls, col, op, bg, th, H, W, TILE, odds, fields, seed, check_bwd, per_splat, bwd_on_device_fwd):
     dev = mu.device
     sc = activate_scale(ls)
     P, C = H * W, col.shape[-1]
