@@ -413,8 +413,8 @@ def e2e_c3(steps, warmup):
 def pair_classes(name, TILE=8, cutoff=3.0):
     """How the backward's per-tile kernel (k_bwd_cull) classes the pairs of a configuration's single-res render, and
     the passes its lanes run: the kernel's tests restated in float64 numpy on the device's own pair lists.
-    negligible: falloff below 2^-30 of the splat's falloff at the pixel centre nearest its centre, at every pixel
-    centre of the tile (a zero record); near-opaque: op * falloff may exceed 0.99 in the tile (one careful pass per
+    negligible: falloff below 2^-30 of the splat's falloff at the 3 x 3 pixel centres around the one nearest its
+    centre (an upper bound of m over them), at every pixel centre of the tile (a zero record); near-opaque: op * falloff may exceed 0.99 in the tile (one careful pass per
     pair, lane = pixel); direct: whitened half-span over the tile above 8 (the direct form); moment: the rest.
     Passes: per tile, the moment pairs and the direct pairs each run in passes of up to 64 (lane = pair); a last
     pass of r < 64 pairs gives each pair Lp lanes (the largest power of two with r Lp <= 64)."""
@@ -450,7 +450,8 @@ def pair_classes(name, TILE=8, cutoff=3.0):
     box_m = du * du + dv * dv
     ny = (np.clip(np.floor(gy * H), 0, H - 1) + 0.5) / H - gy
     nx = (np.clip(np.floor(gx * W), 0, W - 1) + 0.5) / W - gx
-    un, vn = A * ny + B * nx, Cc * ny + D * nx
+    un = np.abs(A * ny + B * nx) + np.abs(A) / H + np.abs(B) / W   # |u|, |v| at the nearest centre + one pixel step
+    vn = np.abs(Cc * ny + D * nx) + np.abs(Cc) / H + np.abs(D) / W
     negl = box_m > 30.0 + (un * un + vn * vn)
     dy = np.maximum(np.maximum(py0 - gy, gy - py1), 0)
     dx = np.maximum(np.maximum(px0 - gx, gx - px1), 0)

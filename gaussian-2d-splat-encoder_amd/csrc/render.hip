@@ -768,12 +768,16 @@ struct TileCentres {
   float pxa[TILE];
 };
 
-// Pairs whose falloff stays below 2^-kCullLog2 (about 1e-9) of the splat's own falloff at the pixel centre
-// nearest its centre, at every pixel centre of the tile, add nothing the backward keeps: their sums would change
-// the splat's gradients by about 1e-9 of their size. They get a zero record and no lanes of the row loops. The
-// bound is relative to the splat's own pixel: a splat far smaller than a pixel whose centre lies between pixel
-// centres may reach only 2^-20 at its best pixel, and an absolute cut at 2^-30 would drop tiles worth 1e-3 of
-// its scale gradient (sum q u^2 weighs its far pixels by u^2). The test is on the falloff alone, not on
+// Pairs whose falloff stays below 2^-kCullLog2 (about 1e-9) of the splat's own falloff at each of the 3 x 3 pixel
+// centres around the one nearest its centre, at every pixel centre of the tile, add nothing the backward keeps:
+// their sums would change the splat's gradients by about 1e-9 of their size. They get a zero record and no lanes
+// of the row loops. The bound is relative to the splat's own pixels: a splat far smaller than a pixel whose
+// centre lies between pixel centres may reach only 2^-20 at its best pixel, and an absolute cut at 2^-30 would drop
+// tiles worth 1e-3 of its scale gradient (sum q u^2 weighs its far pixels by u^2). It takes in the ring around the
+// nearest centre because a splat far thinner than a pixel has its moments across the thin axis (sum q v^2 with v
+// along it) from that ring alone: v vanishes at a centre on its axis, and the ring's falloff can be 2^-31 of the
+// centre's (a 0.15 px sigma one pixel away), so a cut relative to the nearest centre alone dropped half of such a
+// moment where the splat's axis fell on a tile edge. The test is on the falloff alone, not on
 // op * falloff: the opacity gradient sum da * falloff (render_triton.py:698) carries no opacity factor, so a
 // near-transparent splat's far tiles weigh as much in it as an opaque one's. At the 768 x 768 benchmark about a
 // tenth of the pairs qualify, mostly elongated splats' tiles across their narrow axis. The test is a lower bound
@@ -781,14 +785,16 @@ struct TileCentres {
 // the box each lies in an interval given by the corners, and m >= dist(0, u-interval)^2 + dist(0, v-interval)^2.
 constexpr float kCullLog2 = 30.f;
 
-// m = u^2 + v^2 of a splat at the centre of the canvas pixel that holds its centre (clamped to the canvas of H x W
-// pixels, rH = 1 / H, rW = 1 / W): an upper bound of the splat's smallest m over the canvas' pixel centres (the
-// centre position need not be the exact float32 pixel centre for a cut).
-__device__ __forceinline__ float near_pixel_m(float gy, float gx, float A, float B, float Cc, float D, float fH,
+// An upper bound of m = u^2 + v^2 of a splat over the 3 x 3 pixel centres around the centre of the canvas pixel that
+// holds its centre (clamped to the canvas of H x W pixels, rH = 1 / H, rW = 1 / W): u and v at that centre plus
+// their largest change over one pixel step in y and in x (the centre position need not be the exact float32 pixel
+// centre for a cut, and the bound may take in centres past the canvas' edge: it only keeps more pairs).
+__device__ __forceinline__ float ring_pixel_m(float gy, float gx, float A, float B, float Cc, float D, float fH,
                                               float fW, float rH, float rW) {
   const float ny = fmaf(__builtin_amdgcn_fmed3f(floorf(gy * fH), 0.f, fH - 1.f) + 0.5f, rH, -gy);
   const float nx = fmaf(__builtin_amdgcn_fmed3f(floorf(gx * fW), 0.f, fW - 1.f) + 0.5f, rW, -gx);
-  const float u = fmaf(A, ny, B * nx), v = fmaf(Cc, ny, D * nx);
+  const float u = fabsf(fmaf(A, ny, B * nx)) + fmaf(fabsf(A), rH, fabsf(B) * rW);
+  const float v = fabsf(fmaf(Cc, ny, D * nx)) + fmaf(fabsf(Cc), rH, fabsf(D) * rW);
   return fmaf(u, u, v * v);
 }
 
@@ -1093,7 +1099,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   for (int xx = 0; xx < TILE; ++xx) tc.pxa[xx] = uniform_f(s_pxa[xx]);
   const float py0 = tc.py0, px0 = tc.px0, py1 = tc.py1, px1 = tc.px1;
   const float pym = py0 + tc.cy, pxm = px0 + tc.cx;   // the middle of the box of the tile's pixel centres
-  const float rH = uniform_f(hw_rcp(fH)), rW = uniform_f(hw_rcp(fW));   // for near_pixel_m's bound only
+  const float rH = uniform_f(hw_rcp(fH)), rW = uniform_f(hw_rcp(fW));   // for ring_pixel_m's bound only
   int g0 = starts[t], g1 = starts[t + 1];
   if (SPLIT) {   // the item's chunk: whole passes of 64 pairs where the tile's list allows
     const int len = (((g1 - g0 + nsplit - 1) / nsplit) + 63) & ~63;
@@ -1107,7 +1113,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
   }
   const unsigned long long below = (1ull << lane) - 1ull;
   // Classification of the tile's pairs, 64 at a time (lane = pair), into: negligible (falloff below 2^-kCullLog2
-  // of the splat's falloff at its nearest pixel centre, at every pixel centre: a zero record), near-opaque
+  // of the splat's falloff at the pixel centres around its nearest one, at every pixel centre: a zero record),
+  // near-opaque
   // (summed by careful_pair at once), small
   // (span above kMomentSpan: queued in s_defer for a direct pass) and the others (queued in s_mi for a moment
   // pass). Only queued pairs occupy lanes of the row loops. The classification bounds u and v over the tile from
@@ -1123,7 +1130,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     const float2 uv = offsets_at(pym, pxm, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y);
     const float2 hs = half_spans<TILE>(r0.z, r0.w, r1.x, r1.y, tc);
     const bool negl = act && box_min_m(uv.x, uv.y, hs.x, hs.y) >
-                                 kCullLog2 + near_pixel_m(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, fH, fW, rH, rW);
+                                 kCullLog2 + ring_pixel_m(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, fH, fW, rH, rW);
     const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
     const bool defer = act && !negl && !near && !moment_span_ok(hs);
     const bool mom = act && !negl && !near && !defer;

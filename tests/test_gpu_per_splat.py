@@ -100,3 +100,19 @@ def test_float32_rotation_of_a_thin_splat(dev):
           f"in the oracle {rot_th:.2e} (splat {at_rot})", flush=True)
     assert rot_th > 3e-5            # the scene exercises the rounding of a thin splat's rotation
     assert dev_th <= rot_th + 1e-5  # and the device's difference from the float64 rotation is that rounding
+
+
+def test_thin_splat_on_a_tile_edge(dev):
+    """A random scene (seed 90296; FIELDS, alpha, no rotation) holding splat 2008, 1.06 x 0.15 px, its centre on the
+    pixel column at a tile edge (x = 8.5 px). Its moment across the thin axis, sum q v^2 (its x-scale gradient), comes
+    from the pixel columns one pixel to either side, whose falloff is 2^-31 of the centre column's; the column to the
+    left lies in the neighbouring tile. The backward keeps that tile (a negligible pair's falloff is measured against
+    the 3 x 3 pixel centres around the splat's nearest one), and every component of every splat meets the per-splat
+    bar; measured against the nearest centre alone the tile was dropped, half of that moment with it."""
+    from _gpu_util import random_scene
+    H, W = 176, 42
+    scene = random_scene(2259, H, W, seed=90296, dev=dev, ls_mean_px=1.2930040205251416, ls_std=0.8795019694762315,
+                         op_max=0.99, theta=False)
+    sc = np_(activate_scale(scene[1])[0])
+    assert abs(sc[2008, 1] * W - 0.152) < 1e-3 and abs(np_(scene[0][0])[2008, 1] * W - 8.5) < 1e-3
+    run_case(*scene, H, W, 8, False, True, seed=296)
