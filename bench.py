@@ -414,8 +414,10 @@ def pair_classes(name, TILE=8, cutoff=3.0):
     """How the backward's per-tile kernel (k_bwd_cull) classes the pairs of a configuration's single-res render, and
     the passes its lanes run: the kernel's tests restated in float64 numpy on the device's own pair lists.
     negligible: falloff below 2^-30 of the splat's falloff at the 3 x 3 pixel centres around the one nearest its
-    centre (an upper bound of m over them), at every pixel centre of the tile (a zero record); near-opaque: op * falloff may exceed 0.99 in the tile (one careful pass per
-    pair, lane = pixel); direct: whitened half-span over the tile above 8 (the direct form); moment: the rest.
+    centre (an upper bound of m over them), at every pixel centre of the tile (a zero record); near-opaque:
+    op * falloff may exceed 0.99 in the tile (one careful pass per pair, lane = pixel); direct: whitened half-span
+    over the tile above 8, or above 4 for a splat whose scales differ by more than a factor of 16 (the direct form);
+    moment: the rest.
     Passes: per tile, the moment pairs and the direct pairs each run in passes of up to 64 (lane = pair); a last
     pass of r < 64 pairs gives each pair Lp lanes (the largest power of two with r Lp <= 64)."""
     s = synth.config(name)
@@ -459,7 +461,8 @@ def pair_classes(name, TILE=8, cutoff=3.0):
     near = ~negl & (op[g] > 0.99) & ((dy * dy + dx * dx) * k * k <
                                      np.maximum(sy, sx) ** 2 * (lop - np.log2(0.99) + 1e-3))
     span = np.maximum(su, sv)
-    direct = ~negl & ~near & (span > 8.0)
+    elong = np.maximum(sy, sx) > 16.0 * np.minimum(sy, sx)
+    direct = ~negl & ~near & ((span > 8.0) | (elong & (span > 4.0)))
     moment = ~negl & ~near & ~direct
     out = {"pairs": tot, "share": {c: round(float(m.mean()), 5) for c, m in
                                    (("negligible", negl), ("near_opaque", near), ("direct", direct), ("moment", moment))}}

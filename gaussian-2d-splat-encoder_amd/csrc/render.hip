@@ -818,18 +818,30 @@ __device__ __forceinline__ float box_min_m(float uc, float vc, float su, float s
 // centre, du = u - up): the terms cancel where q sits away from that centre, and the rounding error grows
 // with the pair's whitened span over the tile, max |du|. In a float32 emulation of the form (random pair
 // geometries, spans up to 8, 8x8 tiles, signed upstream) each sum's error stays below 1.2e-5 of the sum of its
-// terms' magnitudes, also for elongated rotated splats whose du^2 = (A ly' + B lx')^2 cancels along their long
-// axis; the GPU tests hold every splat's gradients to 1e-4 of their own term magnitudes across this limit.
-// Pairs with a span above kMomentSpan take the direct form.
+// terms' magnitudes; the GPU tests hold every splat's gradients to 1e-4 of their own term magnitudes across this
+// limit. Pairs with a span above kMomentSpan take the direct form, and so do those of very elongated splats with
+// a span above kElongSpan (moment_form_ok).
 constexpr float kMomentSpan = 8.f;
 
 // Half-spans of u and v over the box of the tile's pixel centres (half extents cy, cx) for the rotation rows
-// (A, B), (Cc, D); the moment form takes pairs whose larger half-span is at most kMomentSpan.
+// (A, B), (Cc, D).
 template <int TILE>
 __device__ __forceinline__ float2 half_spans(float A, float B, float Cc, float D, const TileCentres<TILE>& tc) {
   return make_float2(fmaf(fabsf(A), tc.cy, fabsf(B) * tc.cx), fmaf(fabsf(Cc), tc.cy, fabsf(D) * tc.cx));
 }
-__device__ __forceinline__ bool moment_span_ok(float2 hs) { return fmaxf(hs.x, hs.y) <= kMomentSpan; }
+
+// Whether a pair takes the moment form, from its half-spans hs and the splat's scales sc = (sy, sx): a span at most
+// kMomentSpan, and at most kElongSpan for a splat more elongated than kElongAspect. Along an elongated splat's long
+// axis a pair's q sits where u (or v) nearly vanishes while the tile spans large values of it: sum q u^2 is then a
+// small difference of the mapped moments' terms (A^2 sum q ly'^2, 2 A B sum q lx' ly', B^2 sum q lx'^2), and a
+// randomized sweep found a splat of aspect 139 whose pairs at spans 6 to 8 missed the per-splat bar by 4.6e-4 of its
+// scale gradient.
+constexpr float kElongSpan = 4.f;
+constexpr float kElongAspect = 16.f;
+__device__ __forceinline__ bool moment_form_ok(float2 hs, float2 sc) {
+  const float span = fmaxf(hs.x, hs.y);
+  return span <= kMomentSpan && (span <= kElongSpan || fmaxf(sc.x, sc.y) <= kElongAspect * fminf(sc.x, sc.y));
+}
 
 // Geometry of one pair in the direct form: the splat centre, the rotation (cs, sn) and the whitening factors
 // ky = k / sy, kx = k / sx (the decode pass's own values), so that u = ky (cs dy + sn dx) and
@@ -897,7 +909,7 @@ __device__ __forceinline__ void pair_rows_direct(const DirectGeo& g, float op, c
   }
 }
 
-// Moment form over rows [row0, row0 + nrows) (nrows >= 1) for pairs with moment_span_ok (and not near-opaque), into
+// Moment form over rows [row0, row0 + nrows) (nrows >= 1) for pairs with moment_form_ok (and not near-opaque), into
 // a fresh s (its six moment sums are set here, its colour sums accumulate from zero). FULL: every row of the tile
 // (row0 = 0, nrows = TILE), one row at a time for the whole wave, so the row index and the loop's bookkeeping stay
 // in scalar registers. The first row is peeled: it sets the running sums instead of adding to zeros.
@@ -1132,7 +1144,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(5))) voi
     const bool negl = act && box_min_m(uv.x, uv.y, hs.x, hs.y) >
                                  kCullLog2 + ring_pixel_m(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, fH, fW, rH, rW);
     const bool near = act && !negl && near_possible(r1.z, r1.w, r0.x, r0.y, fmaxf(sc.x, sc.y), py0, py1, px0, px1);
-    const bool defer = act && !negl && !near && !moment_span_ok(hs);
+    const bool defer = act && !negl && !near && !moment_form_ok(hs, sc);
     const bool mom = act && !negl && !near && !defer;
     const int q = (negl || near) ? pair_q[i] : 0;
     if (negl) store_pair<C>(psum + (size_t)q * pair_rec<C>(), PairSums<C>(), 1.f);

@@ -48,6 +48,19 @@ class rot32:
         return False
 
 
+class off32:
+    """Within this context the oracle rounds each pixel centre's offsets from a splat centre to float32, as the
+    reference's float32 arithmetic and the kernels form them; outside it they are exact."""
+
+    def __enter__(self):
+        lib().orc_set_off32(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_off32(0)
+        return False
+
+
 def _f32(a):
     return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
 
@@ -76,8 +89,11 @@ def build_tiles(mu, scale, H, W, TILE=8, cutoff=3.0):
     return gid, starts
 
 
-def fwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=False, fields=False, bg=None):
-    """float64 cull forward of one batch. Returns (S_log, S_a, S_ac) if fields else (out, T, asum, fg)."""
+def fwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=False, fields=False, bg=None,
+             cond=False):
+    """float64 cull forward of one batch. Returns (S_log, S_a, S_ac) if fields else (out, T, asum, fg). cond (with
+    fields): also return the fields' sensitivities to a relative change of every unclamped alpha, (K_log, K_a,
+    K_ac) = (sum a / (1 - a), sum a dw/da, sum |c| a dw/da) per pixel, as a fourth element."""
     mu, scale, theta, opacity, color = map(_f32, (mu, scale, theta, opacity, color))
     C = color.shape[1]
     P = H * W
@@ -90,7 +106,7 @@ def fwd_cull(mu, scale, theta, opacity, color, gid, starts, H, W, TILE=8, odds=F
                        ctypes.c_int(H), ctypes.c_int(W), ctypes.c_int(TILE), ctypes.c_int(int(odds)),
                        ctypes.c_int(int(fields)), _p(bg), *[_p(x) for x in a], *[_p(x) for x in f])
     if fields:
-        return f[0], f[1], f[2].reshape(P, C)
+        return (f[0], f[1], f[2].reshape(P, C)) + (((a[1], a[2], a[3].reshape(P, C)),) if cond else ())
     return a[0].reshape(P, C), a[1], a[2], a[3].reshape(P, C)
 
 

@@ -99,14 +99,26 @@ static void trig_tables(orc_splats* s, int N) {
 }
 static void trig_free(orc_splats* s) { free(s->cs); free(s->sn); }
 
-#define ORC_CLAMP (1.0 - 1e-4)
+/* The offsets of a pixel centre from a splat centre: the exact difference of the two float32 values (the default),
+ * or, after orc_set_off32(1), that difference rounded to float32, as the reference's float32 arithmetic and the HIP
+ * kernels form it. */
+static int g_off32 = 0;
+void orc_set_off32(int on) { g_off32 = on; }
+
+/* The alpha clamp 1 - 1e-4 as the reference applies it to float32 alphas (render_triton.py:106, :235, :491, :684):
+ * the float32 value nearest 0.9999, so 1 - a on the clamp is 1.00017e-4 there, not 1e-4. */
+#define ORC_CLAMP 0.99989998340606689453125
 
 /* Pixel centre of the cull kernels: fp32 (i + 0.5) / size (render_triton.py:455-456). */
 static inline double centre(int i, int size) { return (double)(((float)i + 0.5f) / (float)size); }
 
 static inline void splat_alpha(const orc_splats* s, int g, double py, double px, double* ry_o, double* rx_o,
                                double* f_o, double* fo_o, double* a_o) {
-    const double dy = py - (double)s->mu[2 * g], dx = px - (double)s->mu[2 * g + 1];
+    double dy = py - (double)s->mu[2 * g], dx = px - (double)s->mu[2 * g + 1];
+    if (g_off32) {
+        dy = (double)((float)py - s->mu[2 * g]);
+        dx = (double)((float)px - s->mu[2 * g + 1]);
+    }
     double ry = dy, rx = dx;
     if (s->theta) {
         const double c = s->cs[g], sn = s->sn[g];
@@ -121,8 +133,11 @@ static inline void splat_alpha(const orc_splats* s, int g, double py, double px,
     *a_o = fo < ORC_CLAMP ? fo : ORC_CLAMP;
 }
 
-/* Forward over one batch. fields != 0: write S_log[P], S_a[P] (unclamped), S_ac[P*C]; else composite
- * into out[P*C], T[P], asum[P], fg[P*C] with bg[C]. */
+/* Forward over one batch. fields != 0: write S_log[P], S_a[P] (unclamped), S_ac[P*C], and into T[P], asum[P] and
+ * fg[P*C] the fields' sensitivities to a relative change of every unclamped alpha, d/de at a -> a (1 + e):
+ * sum a / (1 - a), sum a dw/da and sum |c| a dw/da over the pixel's pairs (dw/da = 1, or 1 / (1 - a)^2 for odds
+ * weights; 0 for a pair on the clamp), the condition of each field under float32 falloff rounding; else
+ * composite into out[P*C], T[P], asum[P], fg[P*C] with bg[C]. */
 void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const float* opacity,
                   const float* color, int C, const int* gid_sorted, const int* tile_starts, int H, int W,
                   int TILE, int odds, int fields, const float* bg, double* out, double* T, double* asum,
@@ -142,8 +157,8 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
                     const int yp = ty * TILE + ly, xp = tx * TILE + lx;
                     if (yp >= H || xp >= W) continue;
                     const double py = centre(yp, H), px = centre(xp, W);
-                    double S_log = 0.0, S_a = 0.0;
-                    for (int c = 0; c < C; ++c) acc[c] = 0.0;
+                    double S_log = 0.0, S_a = 0.0, K_log = 0.0, K_a = 0.0, K_ac[16];
+                    for (int c = 0; c < C; ++c) acc[c] = K_ac[c] = 0.0;
                     for (int i = tile_starts[t]; i < tile_starts[t + 1]; ++i) {
                         const int g = gid_sorted[i];
                         double ry, rx, f, fo, a;
@@ -152,11 +167,19 @@ void orc_fwd_cull(const float* mu, const float* scale, const float* theta, const
                         const double w = odds ? a / (1.0 - a) : a;
                         S_a += w;
                         for (int c = 0; c < C; ++c) acc[c] += w * (double)color[g * C + c];
+                        if (fields && fo < ORC_CLAMP) {
+                            const double k = odds ? a / ((1.0 - a) * (1.0 - a)) : a;
+                            K_log += a / (1.0 - a);
+                            K_a += k;
+                            for (int c = 0; c < C; ++c) K_ac[c] += k * fabs((double)color[g * C + c]);
+                        }
                     }
                     const int p = yp * W + xp;
                     if (fields) {
                         slog[p] = S_log; sa[p] = S_a;
                         for (int c = 0; c < C; ++c) sac[p * C + c] = acc[c];
+                        T[p] = K_log; asum[p] = K_a;
+                        for (int c = 0; c < C; ++c) fg[p * C + c] = K_ac[c];
                     } else {
                         const double Tp = exp(S_log), as = S_a > 1e-8 ? S_a : 1e-8;
                         T[p] = Tp; asum[p] = as;

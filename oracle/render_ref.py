@@ -24,7 +24,7 @@ import torch.nn.functional as F
 
 from . import binning
 
-CLAMP = 1.0 - 1e-4
+CLAMP = float(np.float32(1.0 - 1e-4))   # the clamp as the reference applies it to float32 alphas (render_triton.py:106)
 f64 = torch.float64
 
 

@@ -58,13 +58,13 @@ def test_zero_opacity_gives_background_and_clamp():
     out, T, _, _ = R.cull_composite(mu.to(f64), scale, col.to(f64), torch.zeros(40, dtype=f64), bg.to(f64),
                                     th.to(f64), gid, st, H, W)
     assert torch.equal(out, bg.to(f64).expand_as(out)) and torch.all(T == 1)
-    # opacity 1 at the splat centre hits the clamp: a = 1 - 1e-4 exactly, T = 1e-4
+    # opacity 1 at the splat centre hits the clamp: a = float32(1 - 1e-4), T = 1 - a = 1.00017e-4
     mu1 = ((torch.tensor([[8.0, 8.0]]) + 0.5) / 16).to(f64)
     s1 = torch.tensor([[0.05, 0.05]], dtype=f64)
     g1, st1 = bins(mu1, s1, H, W)
     _, T1, _, _ = R.cull_composite(mu1, s1, torch.ones(1, 3, dtype=f64), torch.ones(1, dtype=f64),
                                    torch.zeros(3, dtype=f64), None, g1, st1, H, W)
-    assert abs(T1[8 * W + 8].item() - 1e-4) < 1e-12
+    assert abs(T1[8 * W + 8].item() - (1.0 - R.CLAMP)) < 1e-12 and abs(1.0 - R.CLAMP - 1.0001659e-4) < 1e-11
 
 
 def test_theta_none_equals_theta_zero():
@@ -170,6 +170,36 @@ def test_c_forward_matches_torch_forward():
                                fields=False, bg=bg.numpy())
         for a, b in zip(out, Co):
             assert np.allclose(a.numpy(), b, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("odds", [False, True])
+def test_fields_alpha_sensitivity_matches_central_differences(odds):
+    """The C oracle's sensitivities of the fields to a relative change of every unclamped alpha (the condition
+    behind the GPU tests' fields bar) equal central differences of the float64 torch fields over opacity (1 +- e),
+    which scales every alpha below the clamp by the same factor; a splat of opacity 1 centred on a pixel puts pairs
+    on the clamp, whose share is zero. The colour term takes |c|: negating the colours leaves it unchanged."""
+    H, W = 24, 24
+    mu, ls, col, op, bg, th = scene(60, H, W, 11, ls_shift=-2.0, op_hi=0.95)
+    mu[0] = torch.tensor([12.5 / 24, 12.5 / 24])
+    op[0] = 1.0
+    sc = R.activate_scale(ls)
+    gid, st = bins(mu, sc, H, W)
+    args = [mu.numpy(), sc.numpy(), th.numpy(), op.numpy()]
+    _, _, _, K = c_oracle.fwd_cull(*args, col.numpy(), gid, st, H, W, odds=odds, fields=True, cond=True)
+    _, _, _, Kn = c_oracle.fwd_cull(*args, -col.numpy(), gid, st, H, W, odds=odds, fields=True, cond=True)
+    e = 1e-6
+    Sp, Sm = (R.cull_fields(mu.to(f64), sc.to(f64), col.to(f64), op.to(f64) * (1 + s * e), th.to(f64), gid, st, H, W,
+                            odds=odds) for s in (1, -1))
+    fd = [(p - m).numpy() / (2 * e) for p, m in zip(Sp, Sm)]
+    assert K[0].max() > 1.0
+    for k, d, sign in zip(K, fd, (-1.0, 1.0, 1.0)):
+        assert np.allclose(k, sign * d, rtol=1e-6, atol=1e-9 * np.abs(k).max())
+    assert np.array_equal(K[2], Kn[2])
+    # at the splat centre the clamped pair adds nothing: the clamp holds a, and a (1 + e) stays on it
+    p = 12 * W + 12
+    base = c_oracle.fwd_cull(*[a[1:] for a in args], col.numpy()[1:], *bins(mu[1:], sc[1:], H, W), H, W, odds=odds,
+                             fields=True, cond=True)[3]
+    assert abs(K[0][p] - base[0][p]) <= 1e-12 * max(1.0, K[0][p])
 
 
 # ---------------------------------------------------------------- limits and identities
