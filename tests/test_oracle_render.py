@@ -1,6 +1,7 @@
 """Pins the float64 render oracle (oracle/render_ref.py, oracle/oracle.c) with closed forms, central
 finite differences, the cull->exact limit, and cross-checks between the autograd and analytic backwards."""
 
+import contextlib
 import math
 
 import numpy as np
@@ -170,6 +171,62 @@ def test_c_forward_matches_torch_forward():
                                fields=False, bg=bg.numpy())
         for a, b in zip(out, Co):
             assert np.allclose(a.numpy(), b, rtol=1e-12, atol=1e-12)
+
+
+def test_float32_rotation_and_offset_options_single_splat():
+    """`c_oracle.rot32` (cos and sin rounded to float32) and `c_oracle.off32` (pixel-centre offsets from the splat
+    centre rounded to float32) on one elongated rotated splat whose centre lies near the canvas' left edge, so that
+    the float32 offsets of the pixels along its long axis are not exact (pixel and splat centre more than a factor of
+    two apart): in each of the four combinations S_log equals the single-splat closed form evaluated in numpy with the
+    same roundings, and each option changes the result; at theta = 0 (cos and sin exact in float32) rot32 changes
+    nothing."""
+    H, W = 24, 40
+    mu = np.array([[0.4137, 0.0213]], np.float32)
+    sc = np.array([[0.006, 0.3]], np.float32)
+    op = np.array([0.8], np.float32)
+    col = np.ones((1, 3), np.float32)
+    gid, st = binning.build_tiles(mu, sc, H, W, 8, 3.0)
+    ntx = (W + 7) // 8
+    tiles = np.repeat(np.arange(len(st) - 1), np.diff(st))
+    yy, xx = np.meshgrid(np.arange(H), np.arange(W), indexing="ij")
+    covered = np.isin((yy // 8) * ntx + xx // 8, tiles).reshape(-1)
+    py32 = ((yy + np.float32(0.5)) / np.float32(H)).astype(np.float32).reshape(-1)
+    px32 = ((xx + np.float32(0.5)) / np.float32(W)).astype(np.float32).reshape(-1)
+
+    def closed_form(theta, r32, o32):
+        th = np.float64(np.float32(theta))
+        c, s = np.cos(th), np.sin(th)
+        if r32:
+            c, s = float(np.float32(c)), float(np.float32(s))
+        if o32:
+            dy = (py32 - mu[0, 0]).astype(np.float64)       # float32 subtraction, rounded once
+            dx = (px32 - mu[0, 1]).astype(np.float64)
+        else:
+            dy = py32.astype(np.float64) - np.float64(mu[0, 0])
+            dx = px32.astype(np.float64) - np.float64(mu[0, 1])
+        ry, rx = c * dy + s * dx, -s * dy + c * dx
+        m = ry ** 2 / np.float64(sc[0, 0]) ** 2 + rx ** 2 / np.float64(sc[0, 1]) ** 2
+        a = np.minimum(np.exp(-0.5 * m) * np.float64(op[0]), R.CLAMP)
+        return np.where(covered, np.log(1.0 - a), 0.0)
+
+    def oracle(theta, r32, o32):
+        th = np.array([theta], np.float32)
+        with contextlib.ExitStack() as es:
+            if r32:
+                es.enter_context(c_oracle.rot32())
+            if o32:
+                es.enter_context(c_oracle.off32())
+            return c_oracle.fwd_cull(mu, sc, th, op, col, gid, st, H, W, fields=True)[0]
+
+    got = {}
+    for r32 in (False, True):
+        for o32 in (False, True):
+            got[r32, o32] = oracle(0.37, r32, o32)
+            want = closed_form(0.37, r32, o32)
+            assert np.allclose(got[r32, o32], want, rtol=1e-12, atol=0.0), (r32, o32)
+    assert np.abs(got[True, False] - got[False, False]).max() > 1e-9
+    assert np.abs(got[False, True] - got[False, False]).max() > 1e-9
+    assert np.array_equal(oracle(0.0, True, False), oracle(0.0, False, False))
 
 
 @pytest.mark.parametrize("odds", [False, True])
