@@ -30,7 +30,7 @@ from test_gpu_render import run_case
 pytestmark = pytest.mark.gpu
 
 SEED0 = 7000
-N_CASES = 40
+N_CASES = 200
 FWD_TOL = 1e-4
 
 
