@@ -148,3 +148,12 @@ def test_random_entry_point_call(dev, k):
         if ref_g[n] is not None and n != "bg":
             e = rel_err(np_(grads[n][0]), ref_g[n].numpy())
             assert e <= GRAD_REL_TOL, f"gradient {n}: rel {e:.2e}"
+
+
+def test_elongated_splat_moment_form(dev):
+    """Draw 399,016 of the generator above (seed 400,016): a coarse/fine odds render on 4 x 4 tiles whose coarse level
+    holds a splat of aspect 139 with pairs at whitened spans 6 to 8. In the moment form, sum q u^2 along such a
+    splat's long axis is a small difference of the mapped moments' terms; with those pairs in the moment form the
+    scale gradient missed the tensor-wide bar (1.6e-4) and the splat's own per-splat bar (4.6e-4 of its scale). The
+    backward gives pairs of splats more elongated than 16:1 the direct form above span 4."""
+    test_random_scene(dev, 399_016)
